@@ -1,0 +1,97 @@
+/*
+ * k3hip -- MI355X (gfx950) C-ABI for the MXFP4 expert / latent-MLA decode hot path.
+ *
+ * Every entry point:
+ *   - takes raw device pointers, int64 sizes and a hipStream_t (passed as void*),
+ *   - is asynchronous and stream-ordered (the caller synchronises),
+ *   - allocates nothing: outputs and workspaces belong to the caller,
+ *   - returns K3_OK (0) or a K3_ERR_* status; k3_last_error() gives the message for
+ *     the calling thread.
+ *
+ * Layouts (all row-major, contiguous):
+ *   packed  uint8 [N, K/2]   E2M1 codes, element 2i = low nibble of byte i
+ *   scales  uint8 [N, K/32]  E8M0, 2^(b-127) for elements 32j..32j+31 of the row
+ *   (air_llm/models/kimi_k3/mxfp4.py:3-11, k3ref/weights.py:26-37)
+ */
+#ifndef K3HIP_H
+#define K3HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- status codes ------------------------------------------------------------------ */
+#define K3_OK              0
+#define K3_ERR_SHAPE       1  /* inconsistent / unsupported sizes (reference: ValueError) */
+#define K3_ERR_DTYPE       2  /* unsupported dtype enum                                   */
+#define K3_ERR_ALIGN       3  /* pointer not 16-byte aligned where a 128-bit path needs it */
+#define K3_ERR_SCALE_RANGE 4  /* E8M0 bytes outside 2..252 (reference: ValueError)        */
+#define K3_ERR_WORKSPACE   5  /* workspace too small                                      */
+#define K3_ERR_HIP         6  /* a HIP launch / runtime call failed                      */
+#define K3_ERR_NULL        7  /* required pointer is NULL                                 */
+
+/* ---- dtype enums ------------------------------------------------------------------- */
+#define K3_F32   0
+#define K3_BF16  1
+
+/* ---- activation enums (expert FFN) ------------------------------------------------- */
+#define K3_ACT_SILU  0   /* silu(g) * u                         (air_llm/models/kimi_k3/ops.py:42-43) */
+#define K3_ACT_SITU  1   /* b*tanh(g/b)*sigmoid(g) * bl*tanh(u/bl) (air_llm/models/kimi_k3/ops.py:17-28) */
+
+/* ---- router enums ------------------------------------------------------------------ */
+#define K3_ROUTE_SOFTMAX      0  /* softmax(logits), top-k on probabilities                 */
+#define K3_ROUTE_SIGMOID_BIAS 1  /* sigmoid(logits); select on +bias; weights from raw (moe.py:65-76) */
+
+const char *k3_last_error(void);
+const char *k3_version(void);
+
+/* Bit-exact dequantisation to fp32 (out_dtype K3_F32) or bf16 (K3_BF16), [N, K].
+ * Replaces decode_mxfp4_mlx (air_llm/models/kimi_k3/mxfp4.py:68-81) with the values of
+ * k3ref.weights.decode_mxfp4 (k3ref/weights.py:29-37) for every code and scale byte. */
+int k3_mxfp4_decode(const void *packed, const void *scales, void *out, int out_dtype,
+                    int64_t N, int64_t K, void *stream);
+
+/* Device-side min and max of n E8M0 bytes into minmax[0], minmax[1] (int32).
+ * Backs assert_scales_representable (air_llm/models/kimi_k3/mxfp4.py:58-65). */
+int k3_scale_minmax(const void *scales, int64_t n, int32_t *minmax, void *stream);
+
+/* Fused MXFP4 matvec / small-M matmul: out[M, N] = x[M, K] @ W^T, W given by
+ * (packed, scales), weights decoded in registers, fp32 accumulation.
+ * x_dtype K3_F32 or K3_BF16; out_dtype K3_F32 (the reference kernel's output) or K3_BF16
+ * (round-to-nearest-even of the fp32 accumulator).
+ * Replaces mxfp4_matvec_fused (air_llm/kernels/metal/mxfp4_matvec.py:75-96) and the
+ * Metal kernel body (air_llm/kernels/metal/mxfp4_matvec.py:29-63). */
+int k3_mxfp4_matvec(const void *x, int x_dtype, const void *packed, const void *scales,
+                    void *out, int out_dtype, int64_t M, int64_t N, int64_t K, void *stream);
+
+/* Same as k3_mxfp4_matvec with an explicit launch shape (rows per wave 1/2/4/8, groups of
+ * 32 per lane per sweep 1/2/4); used by launch-shape sweeps.  No reference counterpart. */
+int k3_mxfp4_matvec_cfg(const void *x, int x_dtype, const void *packed, const void *scales,
+                        void *out, int out_dtype, int64_t M, int64_t N, int64_t K,
+                        int rows_per_wave, int groups_per_lane, void *stream);
+
+/* ---- MoE expert FFN ---------------------------------------------------------------- */
+
+/* Workspace bytes k3_expert_ffn needs for intermediate size I.  The workspace must be
+ * zero-filled once before its first use; the kernel leaves it ready for the next call.
+ * One workspace per stream: calls that share a workspace must not overlap. */
+int64_t k3_expert_ffn_workspace_size(int64_t I);
+
+/* One routed expert at batch 1 in a single launch: out[H] = act(x Wg^T, x Wu^T) Wd^T with
+ * gate/up packed [I, H/2] / scales [I, H/32] and down packed [H, I/2] / scales [H, I/32].
+ * act_kind K3_ACT_SILU (beta ignored) or K3_ACT_SITU (linear_beta <= 0 means None).
+ * H and I must be multiples of 128.
+ * Replaces LatentMoE.expert_forward (air_llm/models/kimi_k3/moe.py:90-103) with the
+ * k3ref semantics (k3ref/layers.py:226-234). */
+int k3_expert_ffn(const void *x, int x_dtype, const void *gate_packed, const void *gate_scales,
+                  const void *up_packed, const void *up_scales, const void *down_packed,
+                  const void *down_scales, void *out, int out_dtype, int64_t H, int64_t I,
+                  int act_kind, float beta, float linear_beta, void *workspace,
+                  int64_t workspace_bytes, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* K3HIP_H */

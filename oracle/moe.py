@@ -1,0 +1,129 @@
+"""MoE routing / expert FFN / layer-combine oracle (test infrastructure only).
+
+Follows ``k3ref/layers.py:198-261`` (``LatentMoE``) and ``air_llm/models/kimi_k3/moe.py:65-132``
+without the K3 latent down/norm/up wrapper, which is not on the benchmarked path:
+
+* ``route_softmax``     softmax over router logits, top-k, optional renormalisation by
+                        ``sum + 1e-20`` and a scaling factor (the reference's weight
+                        convention, ``k3ref/layers.py:221-224``).
+* ``route_sigmoid_bias`` the reference router: sigmoid scores, selection on
+                        ``scores + bias``, weights gathered from the RAW scores
+                        (``k3ref/layers.py:214-224``, ``moe.py:65-76``).
+* ``expert_ffn``        ``act(x Wg^T, x Wu^T) Wd^T`` with ``act`` = SwiGLU
+                        (``silu(g) * u``, ``ops.py:42-43``) or SiTU (``ops.py:17-28``,
+                        ``k3ref/layers.py:53-60``).
+* ``moe_layer``         weighted sum of the routed experts plus the shared expert on the
+                        original hidden state (``k3ref/layers.py:241-261``).
+
+Everything is float64.  Ties in top-k go to the lower expert index.
+
+Pinning (``tests/test_oracle_moe.py``): softmax/top-k against ``torch.softmax`` /
+``torch.topk`` as library routines plus the invariants of ``tests/test_k3ref_layers.py:113-127``
+(k distinct indices, weights sum to the scaling factor, selection by corrected scores,
+weights from raw scores); SwiGLU/SiTU against their closed forms at chosen points
+(silu(0)=0, silu(x)->x for large x, situ's tanh saturation at +-beta); the expert FFN
+against a brute-force per-row loop; the layer against a loop over experts.
+"""
+from __future__ import annotations
+
+import numpy as np
+
+from .mxfp4 import decode_mxfp4
+
+
+def sigmoid(g: np.ndarray) -> np.ndarray:
+    """Overflow-free logistic: 1/(1+e^-g) == (1 + tanh(g/2)) / 2."""
+    return 0.5 * (1.0 + np.tanh(0.5 * np.asarray(g, dtype=np.float64)))
+
+
+def silu(g: np.ndarray) -> np.ndarray:
+    g = np.asarray(g, dtype=np.float64)
+    return g * sigmoid(g)
+
+
+def situ(g: np.ndarray, u: np.ndarray, beta: float, linear_beta: float | None) -> np.ndarray:
+    """``beta*tanh(g/beta)*sigmoid(g) * linear_beta*tanh(u/linear_beta)``."""
+    g = np.asarray(g, dtype=np.float64)
+    u = np.asarray(u, dtype=np.float64)
+    a = beta * np.tanh(g / beta) * sigmoid(g)
+    if linear_beta is not None:
+        u = linear_beta * np.tanh(u / linear_beta)
+    return a * u
+
+
+def activation(g, u, kind: str = "silu", beta: float = 1.0, linear_beta=None):
+    if kind == "silu":
+        return silu(g) * np.asarray(u, dtype=np.float64)
+    if kind == "situ":
+        return situ(g, u, beta, linear_beta)
+    raise ValueError(kind)
+
+
+def topk_lowest_index(scores: np.ndarray, k: int) -> np.ndarray:
+    """Indices of the k largest entries per row, largest first, ties to the lower index."""
+    s = np.asarray(scores, dtype=np.float64)
+    order = np.lexsort((np.broadcast_to(np.arange(s.shape[-1]), s.shape), -s), axis=-1)
+    return order[..., :k]
+
+
+def route_softmax(x, router_w, k: int, renormalize: bool = True, scaling: float = 1.0):
+    """x [T, H], router_w [E, H] -> (idx [T, k], weights [T, k], probs [T, E], logits)."""
+    logits = np.asarray(x, np.float64) @ np.asarray(router_w, np.float64).T
+    z = logits - logits.max(axis=-1, keepdims=True)
+    e = np.exp(z)
+    probs = e / e.sum(axis=-1, keepdims=True)
+    idx = topk_lowest_index(probs, k)
+    w = np.take_along_axis(probs, idx, axis=-1)
+    if renormalize and k > 1:
+        w = w / (w.sum(axis=-1, keepdims=True) + 1e-20)
+    return idx, w * scaling, probs, logits
+
+
+def route_sigmoid_bias(x, router_w, bias, k: int, renormalize: bool = True,
+                       scaling: float = 1.0):
+    """The reference router (``k3ref/layers.py:214-224``)."""
+    logits = np.asarray(x, np.float64) @ np.asarray(router_w, np.float64).T
+    raw = sigmoid(logits)
+    corrected = raw + np.asarray(bias, np.float64)[None, :]
+    idx = topk_lowest_index(corrected, k)
+    w = np.take_along_axis(raw, idx, axis=-1)
+    if renormalize and k > 1:
+        w = w / (w.sum(axis=-1, keepdims=True) + 1e-20)
+    return idx, w * scaling, raw, corrected
+
+
+def dense_ffn(x, wg, wu, wd, kind="silu", beta=1.0, linear_beta=None):
+    """Expert FFN on already-dense (float) weights [I, H], [I, H], [H, I]."""
+    x = np.asarray(x, np.float64)
+    g = x @ np.asarray(wg, np.float64).T
+    u = x @ np.asarray(wu, np.float64).T
+    a = activation(g, u, kind, beta, linear_beta)
+    return a @ np.asarray(wd, np.float64).T, g, u, a
+
+
+def expert_ffn(x, gate, up, down, kind="silu", beta=1.0, linear_beta=None):
+    """One MXFP4 expert; ``gate``/``up``/``down`` are ``(packed, scales)`` pairs."""
+    return dense_ffn(x, decode_mxfp4(*gate), decode_mxfp4(*up), decode_mxfp4(*down),
+                     kind, beta, linear_beta)
+
+
+def moe_layer(x, idx, weights, experts, shared=None, kind="silu", beta=1.0,
+              linear_beta=None):
+    """Weighted sum of routed experts (+ shared expert on the same hidden state).
+
+    ``experts[e]`` is ``(gate, up, down)`` of (packed, scales) pairs; ``shared`` is
+    ``(wg, wu, wd)`` of dense float weights or None.  Tokens are processed one at a time,
+    experts visited in ascending id as in ``k3ref/layers.py:252-256``.
+    """
+    x = np.atleast_2d(np.asarray(x, np.float64))
+    idx = np.atleast_2d(idx)
+    weights = np.atleast_2d(weights)
+    y = np.zeros((x.shape[0], x.shape[1]), np.float64)
+    for e in sorted({int(v) for v in idx.reshape(-1)}):
+        tok, slot = np.nonzero(idx == e)
+        out = expert_ffn(x[tok], *experts[e], kind=kind, beta=beta,
+                         linear_beta=linear_beta)[0]
+        y[tok] += out * weights[tok, slot][:, None]
+    if shared is not None:
+        y += dense_ffn(x, *shared, kind=kind, beta=beta, linear_beta=linear_beta)[0]
+    return y
