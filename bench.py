@@ -1,0 +1,249 @@
+"""Benchmark: MXFP4 expert GEMV GB/s (% of HBM peak) and us per MoE layer at batch 1.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--workloads expert,layer,gemv]
+
+One JSON line on stdout.  The headline workload is one SwiGLU expert at batch 1
+(hidden 7168, intermediate 2048, MXFP4 weights with E8M0 scales in [118, 130], bf16 x):
+a step is one expert FFN launch on a different resident expert (64 experts rotate, 1.5 GB,
+so the 256 MB MALL cannot serve the weights).  `value` is algorithmic weight bytes per
+second over the K timed steps.  The same line carries the MoE-layer figure (384 resident
+experts, top-8 softmax routing, one bf16 shared expert, a fresh token per step), the
+single-projection GEMV figure, the roofline of the dominant kernel and a CPU baseline
+(torch-CPU restatement of the k3ref path timed on a bounded sample on this host).
+
+Synthetic, seeded data; weights are random-init with the benchmark shapes.  Steps are
+captured once into a HIP graph and replayed, so the timed region is GPU work plus the
+graph's launch gaps, without Python launch overhead.  `--gpus N` with N > 1 exits: the
+single-GPU build has no multi-GPU path.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+for _p in (ROOT, ROOT / "kimi-k3-mlx-macmini_amd"):
+    if str(_p) not in sys.path:
+        sys.path.insert(0, str(_p))
+
+HBM_PEAK_GBS = 8000.0           # MI355X HBM3E, published
+H, I = 7168, 2048
+E_LAYER, TOPK = 384, 8
+ROTATE = 64                     # distinct experts cycled by the expert / GEMV benches
+
+METRIC = "MXFP4 expert GEMV GB/s (% of HBM peak); us per MoE layer at batch 1"
+
+
+def proj_bytes(n, k):
+    return n * k // 2 + n * k // 32
+
+
+EXPERT_BYTES = 2 * proj_bytes(I, H) + proj_bytes(H, I)          # 23,396,352
+EXPERT_IO = H * 2 + H * 4                                        # x bf16 in, y fp32 out
+LAYER_BYTES = E_LAYER * H * 2 + TOPK * EXPERT_BYTES + 3 * H * I * 2   # 280,756,224
+GEMV_BYTES = proj_bytes(I, H) + H * 2 + I * 2                     # 7,817,216
+
+
+def rand_mxfp4(torch, gen, n, k, device):
+    p = torch.randint(0, 256, (n, k // 2), dtype=torch.uint8, device=device, generator=gen)
+    s = torch.randint(118, 131, (n, k // 32), dtype=torch.uint8, device=device, generator=gen)
+    return p, s
+
+
+def graph_time(torch, fn, steps, warmup):
+    """Capture `steps` calls of fn(i) into one graph and replay it; also replay a graph of
+    `warmup` calls first.  Returns seconds for the timed replay (synchronised both sides)."""
+    stream = torch.cuda.current_stream()
+    for i in range(3):
+        fn(i)
+    torch.cuda.synchronize()
+    if warmup:
+        gw = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(gw):
+            for i in range(warmup):
+                fn(i)
+        gw.replay()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for i in range(steps):
+            fn(i)
+    torch.cuda.synchronize()
+    g.replay()                      # first replay pays one-time costs
+    torch.cuda.synchronize()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    e0.record(stream)
+    g.replay()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    return e0.elapsed_time(e1) / 1e3, wall
+
+
+# --------------------------------------------------------------------- workloads
+
+def bench_expert(torch, steps, warmup, dev):
+    from k3hip.moe import expert_ffn_fused
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(1002)
+    experts = [(rand_mxfp4(torch, gen, I, H, dev), rand_mxfp4(torch, gen, I, H, dev),
+                rand_mxfp4(torch, gen, H, I, dev)) for _ in range(ROTATE)]
+    x = torch.randn(1, H, device=dev, generator=gen).to(torch.bfloat16)
+    outs = [torch.empty(1, H, device=dev) for _ in range(2)]
+
+    def step(i):
+        outs[i & 1] = expert_ffn_fused(x, *experts[i % ROTATE])
+
+    sec, wall = graph_time(torch, step, steps, warmup)
+    del experts
+    return sec, wall
+
+
+def bench_gemv(torch, steps, warmup, dev):
+    from k3hip.mxfp4_matvec import mxfp4_matvec_fused
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(1001)
+    ws = [rand_mxfp4(torch, gen, I, H, dev) for _ in range(ROTATE)]
+    x = torch.randn(1, H, device=dev, generator=gen).to(torch.bfloat16)
+
+    def step(i):
+        mxfp4_matvec_fused(x, *ws[i % ROTATE], out_dtype=torch.bfloat16)
+
+    sec, _ = graph_time(torch, step, steps, warmup)
+    return sec
+
+
+def build_layer(torch, dev):
+    from k3hip.moe import MoEConfig, RoutedMoE
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(1003)
+    experts = [(rand_mxfp4(torch, gen, I, H, dev), rand_mxfp4(torch, gen, I, H, dev),
+                rand_mxfp4(torch, gen, H, I, dev)) for _ in range(E_LAYER)]
+    w = {"gate.weight": (torch.randn(E_LAYER, H, device=dev, generator=gen) * 0.02).to(torch.bfloat16)}
+    for name, shape in (("gate", (I, H)), ("up", (I, H)), ("down", (H, I))):
+        w[f"shared_experts.{name}_proj.weight"] = (torch.randn(*shape, device=dev, generator=gen) * 0.02
+                                                   ).to(torch.bfloat16)
+    which = {"w1": 0, "w3": 1, "w2": 2}
+    cfg = MoEConfig(hidden_size=H, moe_intermediate_size=I, num_experts=E_LAYER, num_experts_per_token=TOPK,
+                    shared_intermediate_size=I, router="softmax", activation="silu")
+    return RoutedMoE(cfg, 0, w, lambda L, e, wh: experts[e][which[wh]]), experts
+
+
+def bench_layer(torch, steps, warmup, dev):
+    moe, experts = build_layer(torch, dev)
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(7)
+    xs = torch.randn(steps + warmup + 3, H, device=dev, generator=gen).to(torch.bfloat16)
+    touched = set()
+
+    def step(i):
+        moe(xs[i:i + 1])
+
+    sec, _ = graph_time(torch, step, steps, warmup)
+    # distinct experts the timed tokens routed to (evidence the MALL could not hold them)
+    for i in range(min(steps, 32)):
+        touched.update(moe.route(xs[i:i + 1]).expert_indices.view(-1).tolist())
+    del moe, experts
+    return sec, len(touched)
+
+
+def bench_cpu(sample_s=12.0):
+    """torch-CPU restatement of the k3ref expert path (k3ref/layers.py:226-234 with the
+    decode of k3ref/weights.py:29-37 on every access), timed on this host."""
+    import numpy as np
+    import torch
+
+    from oracle import cpu_baseline
+    n = len(os.sched_getaffinity(0))
+    torch.set_num_threads(n)
+    return cpu_baseline.time_expert(H, I, sample_s=sample_s, threads=n)
+
+
+def traffic_from_profiles():
+    """HBM bytes per expert launch from the committed rocprofv3 --pmc summary, if any."""
+    f = ROOT / "profiles" / "expert_ffn_b1_traffic.json"
+    if f.exists():
+        try:
+            return json.loads(f.read_text()).get("bytes_per_launch")
+        except (ValueError, OSError):
+            return None
+    return None
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=512)
+    ap.add_argument("--warmup", type=int, default=64)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--workloads", default="expert,layer,gemv")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py: this build runs on one GPU only (no multi-GPU path); use --gpus 1",
+              file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    if not torch.cuda.is_available():
+        print("bench.py: no GPU visible", file=sys.stderr)
+        sys.exit(2)
+    import k3hip
+    k3hip.lib()   # fails loudly when libk3hip.so is missing: there is no fallback
+    dev = torch.device("cuda:0")
+    work = set(args.workloads.split(","))
+    K, W = args.steps, args.warmup
+
+    sec, wall = bench_expert(torch, K, W, dev)
+    per_step = sec / K
+    gbs = EXPERT_BYTES / per_step / 1e9
+    line = {
+        "metric": METRIC,
+        "value": round(gbs, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": K,
+        "warmup": W,
+        "ms_per_step": round(per_step * 1e3, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "mxfp4xbf16->f32",
+        "data": "synthetic (seeded random MXFP4 weights, E8M0 in [118,130], bf16 x ~ N(0,1))",
+        "config": {"workload": "expert_swiglu_ffn_b1", "hidden": H, "intermediate": I,
+                   "experts_rotated": ROTATE, "act": "silu", "x": "bf16", "out": "f32"},
+        "pct_hbm_peak": round(100 * gbs / HBM_PEAK_GBS, 1),
+        "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": traffic_from_profiles(),
+                     "kernel": "expert_ffn_kernel", "bytes_per_launch": EXPERT_BYTES,
+                     "avg_launch_us": round(per_step * 1e6, 3)},
+        "wall_s": round(wall, 4),
+    }
+    if "layer" in work:
+        lsec, touched = bench_layer(torch, min(K, 256), min(W, 32), dev)
+        lus = lsec / min(K, 256) * 1e6
+        lgbs = LAYER_BYTES / (lus * 1e-6) / 1e9
+        line["moe_layer"] = {"us_per_layer": round(lus, 2), "GB/s": round(lgbs, 1),
+                             "pct_hbm_peak": round(100 * lgbs / HBM_PEAK_GBS, 1),
+                             "bytes_per_layer": LAYER_BYTES, "experts": E_LAYER, "top_k": TOPK,
+                             "shared_expert": "bf16", "distinct_experts_routed_first32": touched,
+                             "launches_per_layer": 3}
+    if "gemv" in work:
+        gsec = bench_gemv(torch, K, W, dev)
+        gus = gsec / K * 1e6
+        line["gemv"] = {"us": round(gus, 3), "GB/s": round(GEMV_BYTES / (gus * 1e-6) / 1e9, 1),
+                        "shape": [I, H], "x": "bf16", "out": "bf16", "bytes": GEMV_BYTES}
+    if not args.no_cpu:
+        cpu = bench_cpu(args.cpu_seconds)
+        line["cpu_baseline"] = cpu
+        line["gpu_vs_cpu"] = round(gbs / cpu["value"], 1) if cpu.get("value") else None
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -91,6 +91,47 @@ int k3_expert_ffn(const void *x, int x_dtype, const void *gate_packed, const voi
                   int act_kind, float beta, float linear_beta, void *workspace,
                   int64_t workspace_bytes, void *stream);
 
+/* ---- routed MoE layer at batch 1 ------------------------------------------------------ */
+
+/* Workspace bytes for k3_moe_layer_decode / k3_moe_route (pass shared_I = 0 without a
+ * shared expert).  Needs no initialisation. */
+int64_t k3_moe_layer_workspace_size(int64_t H, int64_t I, int64_t shared_I, int64_t n_experts,
+                                    int64_t top_k);
+
+/* Byte offsets of the workspace's records: [0] logits[E] f32, [1] scores[E] f32 (softmax
+ * probabilities or raw sigmoid scores), [2] corrected scores[E] f32, [3] top-k expert ids
+ * int32[k], [4] top-k weights f32[k], [5] shared act, [6] routed act, [7] shared output.
+ * The RouterResult of LatentMoE.route (air_llm/models/kimi_k3/moe.py:32-37) is read there. */
+int k3_moe_layer_workspace_offsets(int64_t H, int64_t I, int64_t shared_I, int64_t n_experts,
+                                   int64_t top_k, int64_t *offsets);
+
+/* Router + top-k only (LatentMoE.route, air_llm/models/kimi_k3/moe.py:65-76 and
+ * k3ref/layers.py:214-224): router_w bf16 [E, H]; route_kind K3_ROUTE_SOFTMAX or
+ * K3_ROUTE_SIGMOID_BIAS (router_bias f32 [E] added for selection only); weights gathered
+ * from the raw scores, divided by (sum + 1e-20) when renormalize and top_k > 1, times
+ * scaling.  Ties go to the lower expert index.  Results land in the workspace records. */
+int k3_moe_route(const void *x, int x_dtype, const void *router_w, const void *router_bias,
+                 int route_kind, int renormalize, float scaling, int64_t H, int64_t n_experts,
+                 int64_t top_k, void *workspace, int64_t workspace_bytes, void *stream);
+
+/* Whole routed MoE layer for one token: route (as k3_moe_route), then
+ *   out[H] = shared(x) + sum_j w_j * expert_{idx_j}(x)
+ * with no device-to-host synchronisation.  expert_table is a device array of
+ * n_experts x 6 uint64 pointers (gate packed, gate scales, up packed, up scales, down
+ * packed, down scales) in the k3_expert_ffn layouts, so every expert stays resident and
+ * each selected expert is read once.  shared_gate/up bf16 [shared_I, H] and shared_down
+ * bf16 [H, shared_I] are optional (all NULL: no shared expert).  top_k <= 16,
+ * n_experts <= 1024, H/I/shared_I multiples of 128.
+ * Replaces LatentMoE.__call__ / expert_forward / shared_forward
+ * (air_llm/models/kimi_k3/moe.py:90-132; k3ref/layers.py:226-261) without the K3
+ * latent down/norm/up wrapper. */
+int k3_moe_layer_decode(const void *x, int x_dtype, const void *router_w, const void *router_bias,
+                        int route_kind, int renormalize, float scaling, const void *expert_table,
+                        const void *shared_gate, const void *shared_up, const void *shared_down,
+                        void *out, int out_dtype, int64_t H, int64_t I, int64_t shared_I,
+                        int64_t n_experts, int64_t top_k, int act_kind, float beta,
+                        float linear_beta, void *workspace, int64_t workspace_bytes, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -144,27 +144,33 @@ __global__ __launch_bounds__(256) void expert_ffn_kernel(FfnArgs a) {
     }
     __syncthreads();
     if (wave == 0) return;
+    float acc[RB];
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb) acc[rb] = 0.f;
+#pragma unroll
+    for (int u = 0; u < GB; ++u) {
+        const int g = u * 64 + lane;
+        if (g < GI) {
+            float4 ac[8];
+#pragma unroll
+            for (int q = 0; q < 8; ++q) ac[q] = reinterpret_cast<const float4 *>(as)[XTile<float>::slot(g, q)];
+#pragma unroll
+            for (int rb = 0; rb < RB; ++rb) {
+                const int n = pw + rb * PW;
+                acc[rb] = fmaf(group_dot(wd_[rb][u], ac),
+                               e8m0_to_f32(scale_byte(sd_[rb][u], static_cast<uint32_t>(n * GI), g)), acc[rb]);
+            }
+        }
+    }
 #pragma unroll
     for (int rb = 0; rb < RB; ++rb) {
         const int n = pw + rb * PW;
-        float acc = 0.f;
-#pragma unroll
-        for (int u = 0; u < GB; ++u) {
-            const int g = u * 64 + lane;
-            if (n < a.H && g < GI) {
-                float4 ac[8];
-#pragma unroll
-                for (int q = 0; q < 8; ++q) ac[q] = reinterpret_cast<const float4 *>(as)[XTile<float>::slot(g, q)];
-                acc = fmaf(group_dot(wd_[rb][u], ac),
-                           e8m0_to_f32(scale_byte(sd_[rb][u], static_cast<uint32_t>(n * GI), g)), acc);
-            }
-        }
-        acc = wave_sum_to_lane63(acc);
+        const float t = wave_sum_to_lane63(acc[rb]);
         if (lane == 63 && n < a.H) {
             if (a.out_bf16)
-                static_cast<uint16_t *>(a.out)[n] = f32_to_bf16(acc);
+                static_cast<uint16_t *>(a.out)[n] = f32_to_bf16(t);
             else
-                static_cast<float *>(a.out)[n] = acc;
+                static_cast<float *>(a.out)[n] = t;
         }
     }
 }

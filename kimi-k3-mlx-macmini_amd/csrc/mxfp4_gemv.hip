@@ -177,15 +177,10 @@ static int launch_one(const GemvArgs &a, hipStream_t st) {
         return set_error(K3_ERR_SHAPE, "mxfp4 matvec: K=%lld needs %zu bytes of LDS (max %zu)",
                          (long long)a.K, lds, kGemvMaxLds);
     if (lds > 64 * 1024) {  // above the default dynamic-LDS limit: opt in (gfx950 has 160 KiB)
-        static bool raised = false;
-        if (!raised) {
-            int rc = check_hip(hipFuncSetAttribute(reinterpret_cast<const void *>(&gemv_kernel<XT, RPW, GPL, MT>),
-                                                   hipFuncAttributeMaxDynamicSharedMemorySize,
-                                                   static_cast<int>(kGemvMaxLds)),
-                               "mxfp4 matvec: raise LDS limit");
-            if (rc) return rc;
-            raised = true;
-        }
+        int rc = check_hip(hipFuncSetAttribute(reinterpret_cast<const void *>(&gemv_kernel<XT, RPW, GPL, MT>),
+                                               hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds)),
+                           "mxfp4 matvec: raise LDS limit");
+        if (rc) return rc;
     }
     const dim3 grid(static_cast<unsigned>(cdiv(a.N, 4 * RPW)));
     gemv_kernel<XT, RPW, GPL, MT><<<grid, 256, lds, st>>>(a);

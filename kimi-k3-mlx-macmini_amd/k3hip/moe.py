@@ -51,3 +51,219 @@ def expert_ffn_fused(x: torch.Tensor, gate, up, down, act: str = "silu", beta: f
               _act_code(act), float(beta), float(linear_beta or 0.0), T.ptr(ws), ws.numel(),
               T.stream(x2))
     return out.reshape(-1) if squeeze else out
+
+
+# ----------------------------------------------------------------------- routed layer
+
+from dataclasses import dataclass  # noqa: E402
+from typing import Callable  # noqa: E402
+
+ROUTES = {"softmax": _lib.K3_ROUTE_SOFTMAX, "sigmoid_bias": _lib.K3_ROUTE_SIGMOID_BIAS}
+
+
+@dataclass
+class RouterResult:
+    """Same fields as the reference's RouterResult (air_llm/models/kimi_k3/moe.py:32-37)."""
+    expert_indices: torch.Tensor      # [N, top_k] int64, largest weight first
+    expert_weights: torch.Tensor      # [N, top_k] float32
+    raw_scores: torch.Tensor          # [N, num_experts] softmax probabilities / sigmoid scores
+    corrected_scores: torch.Tensor    # raw + e_score_correction_bias (== raw for softmax)
+
+
+@dataclass
+class MoEConfig:
+    """The config fields the routed layer reads (names follow K3Config,
+    air_llm/models/kimi_k3/config.py), plus the router / activation choice."""
+    hidden_size: int
+    moe_intermediate_size: int
+    num_experts: int
+    num_experts_per_token: int
+    shared_intermediate_size: int = 0
+    moe_renormalize: bool = True
+    routed_scaling_factor: float = 1.0
+    router: str = "softmax"               # "softmax" (benchmark) | "sigmoid_bias" (K3)
+    activation: str = "silu"              # "silu" (benchmark) | "situ" (K3)
+    situ_beta: float = 1.0
+    situ_linear_beta: float | None = None
+
+
+class RoutedMoE:
+    """Drop-in for the routed path of LatentMoE (air_llm/models/kimi_k3/moe.py:40-132).
+
+    ``RoutedMoE(cfg, layer, w, expert_source, fused=True)`` keeps the reference
+    constructor: ``w`` holds ``gate.weight`` (bf16 [E, H]), optionally
+    ``gate.e_score_correction_bias`` and ``shared_experts.{gate,up,down}_proj.weight``
+    (bf16); ``expert_source(layer, expert, which)`` returns ``(packed, scales)`` device
+    tensors for ``which`` in ``w1`` (gate), ``w3`` (up), ``w2`` (down).
+
+    All experts are made resident once (the source is called E x 3 times at build) and
+    addressed through a device pointer table, so a decode step is three launches with no
+    host synchronisation; ``fused=False`` keeps the reference's unfused definition
+    (decode to bf16, BLAS matmul) for debugging, as ``moe.py:79-88`` does.
+    """
+
+    def __init__(self, cfg, layer: int, w: dict, expert_source: Callable, fused: bool = True):
+        self.cfg, self.L = cfg, layer
+        self.src = expert_source
+        self.fused = fused
+        self.gate_w = w["gate.weight"]
+        self.gate_b = w.get("gate.e_score_correction_bias")
+        self.sh_gate = w.get("shared_experts.gate_proj.weight")
+        self.sh_up = w.get("shared_experts.up_proj.weight")
+        self.sh_down = w.get("shared_experts.down_proj.weight")
+        self.device = self.gate_w.device
+        if self.gate_w.dtype != torch.bfloat16:
+            raise TypeError("gate.weight must be bfloat16")
+        if self.gate_b is not None:
+            self.gate_b = self.gate_b.to(torch.float32).contiguous()
+        for t in (self.sh_gate, self.sh_up, self.sh_down):
+            if t is not None and t.dtype != torch.bfloat16:
+                raise TypeError("shared expert weights must be bfloat16")
+        self._table = None
+        self._keep = []
+
+    # ------------------------------------------------------------------ helpers
+    @property
+    def _H(self):
+        return self.gate_w.shape[1]
+
+    @property
+    def _E(self):
+        return self.gate_w.shape[0]
+
+    @property
+    def _k(self):
+        return int(self.cfg.num_experts_per_token)
+
+    @property
+    def _I(self):
+        return int(self.cfg.moe_intermediate_size)
+
+    @property
+    def _Is(self):
+        return 0 if self.sh_gate is None else self.sh_gate.shape[0]
+
+    def _act(self):
+        act = getattr(self.cfg, "activation", "silu")
+        beta = float(getattr(self.cfg, "situ_beta", 1.0) or 1.0)
+        lb = getattr(self.cfg, "situ_linear_beta", None)
+        return act, beta, lb
+
+    def _route_args(self):
+        kind = ROUTES[getattr(self.cfg, "router", "softmax")]
+        bias = self.gate_b if kind == _lib.K3_ROUTE_SIGMOID_BIAS else None
+        return kind, bias
+
+    def expert_table(self) -> torch.Tensor:
+        """[E, 6] int64 device pointers, built once from expert_source."""
+        if self._table is None:
+            ptrs = []
+            for e in range(self._E):
+                row = []
+                for which in ("w1", "w3", "w2"):
+                    p, s = self.src(self.L, e, which)
+                    p = T.contiguous_aligned(p)
+                    s = s.contiguous()
+                    T.require_device(p, s)
+                    if p.device != self.device:
+                        raise ValueError("experts must live on the router's device")
+                    self._keep += [p, s]
+                    row += [p.data_ptr(), s.data_ptr()]
+                ptrs.append(row)
+            self._table = torch.tensor(ptrs, dtype=torch.int64, device=self.device)
+        return self._table
+
+    def _workspace(self):
+        nbytes = int(_lib.lib().k3_moe_layer_workspace_size(self._H, self._I, self._Is, self._E, self._k))
+        return _workspace.get(self.device, nbytes, "moe_layer")
+
+    def _records(self, ws: torch.Tensor) -> RouterResult:
+        import ctypes
+        off = (ctypes.c_int64 * 8)()
+        _lib.call("k3_moe_layer_workspace_offsets", self._H, self._I, self._Is, self._E, self._k, off)
+        E, k = self._E, self._k
+
+        def f32(o, n):
+            return ws[o:o + 4 * n].view(torch.float32).clone()
+
+        idx = ws[off[3]:off[3] + 4 * k].view(torch.int32).to(torch.int64).reshape(1, k)
+        return RouterResult(idx, f32(off[4], k).reshape(1, k), f32(off[1], E).reshape(1, E),
+                            f32(off[2], E).reshape(1, E))
+
+    def _x1(self, x):
+        x1 = x.reshape(1, -1)
+        if x1.dtype not in (torch.float32, torch.bfloat16):
+            x1 = x1.to(torch.float32)
+        return T.contiguous_aligned(x1)
+
+    # ------------------------------------------------------------------ API
+    def route(self, x: torch.Tensor) -> RouterResult:
+        """Router + top-k for each token of x [..., H] (moe.py:65-76)."""
+        flat = x.reshape(-1, x.shape[-1])
+        kind, bias = self._route_args()
+        results = []
+        for t in range(flat.shape[0]):
+            xt = self._x1(flat[t])
+            ws = self._workspace()
+            _lib.call("k3_moe_route", T.ptr(xt), T.dtype_code(xt.dtype), T.ptr(self.gate_w), T.ptr(bias), kind,
+                      int(bool(self.cfg.moe_renormalize)), float(self.cfg.routed_scaling_factor), self._H,
+                      self._E, self._k, T.ptr(ws), ws.numel(), T.stream(xt))
+            results.append(self._records(ws))
+        return RouterResult(*(torch.cat([getattr(r, f) for r in results]) for f in
+                              ("expert_indices", "expert_weights", "raw_scores", "corrected_scores")))
+
+    def expert_forward(self, h: torch.Tensor, e: int) -> torch.Tensor:
+        """One routed expert on h [N, H] (moe.py:90-103)."""
+        gate, up, down = (self.src(self.L, e, w) for w in ("w1", "w3", "w2"))
+        act, beta, lb = self._act()
+        if not self.fused:
+            from .mxfp4 import decode_mxfp4
+            ws = [decode_mxfp4(p, s, out_dtype=torch.bfloat16) for p, s in (gate, up, down)]
+            hf = h.to(torch.float32)
+            g, u = hf @ ws[0].float().T, hf @ ws[1].float().T
+            return _act_torch(g, u, act, beta, lb) @ ws[2].float().T
+        return torch.cat([expert_ffn_fused(h[t:t + 1], gate, up, down, act, beta, lb)
+                          for t in range(h.shape[0])])
+
+    def shared_forward(self, x: torch.Tensor) -> torch.Tensor:
+        """Shared expert on the original hidden (moe.py:105-107), via the bf16 path of the
+        unfused definition; inside a decode step it runs fused in the layer kernels."""
+        act, beta, lb = self._act()
+        xf = x.to(torch.float32)
+        g = xf @ self.sh_gate.float().T
+        u = xf @ self.sh_up.float().T
+        return _act_torch(g, u, act, beta, lb) @ self.sh_down.float().T
+
+    def __call__(self, x: torch.Tensor, return_router: bool = False, out_dtype=torch.float32):
+        orig = x.shape
+        flat = x.reshape(-1, orig[-1])
+        kind, bias = self._route_args()
+        act, beta, lb = self._act()
+        table = self.expert_table()
+        outs, recs = [], []
+        for t in range(flat.shape[0]):
+            xt = self._x1(flat[t])
+            ws = self._workspace()
+            out = torch.empty((1, self._H), dtype=out_dtype, device=self.device)
+            _lib.call("k3_moe_layer_decode", T.ptr(xt), T.dtype_code(xt.dtype), T.ptr(self.gate_w), T.ptr(bias),
+                      kind, int(bool(self.cfg.moe_renormalize)), float(self.cfg.routed_scaling_factor),
+                      T.ptr(table), T.ptr(self.sh_gate), T.ptr(self.sh_up), T.ptr(self.sh_down), T.ptr(out),
+                      T.dtype_code(out_dtype), self._H, self._I, self._Is, self._E, self._k, ACTS[act],
+                      float(beta), float(lb or 0.0), T.ptr(ws), ws.numel(), T.stream(xt))
+            outs.append(out)
+            if return_router:
+                recs.append(self._records(ws))
+        y = torch.cat(outs).reshape(*orig[:-1], self._H)
+        if not return_router:
+            return y
+        r = RouterResult(*(torch.cat([getattr(rr, f) for rr in recs]) for f in
+                           ("expert_indices", "expert_weights", "raw_scores", "corrected_scores")))
+        return y, r
+
+
+def _act_torch(g, u, act, beta, lb):
+    """Torch form of the activations for the unfused (debug) path only."""
+    if act == "situ":
+        a = beta * torch.tanh(g / beta) * torch.sigmoid(g)
+        return a * (lb * torch.tanh(u / lb) if lb else u)
+    return torch.nn.functional.silu(g) * u

@@ -74,5 +74,6 @@ def test_expert_ffn_repeated_calls_and_bf16_out():
         torch.cuda.synchronize()
         for e in range(3):
             assert torch.equal(outs[e], ref[e])
-    for buf in _workspace._cache.values():
-        assert _workspace.error_flag(buf) == 0
+    for key, buf in _workspace._cache.items():
+        if key[2] == "expert_ffn":     # only the persistent kernel's workspaces carry the flag
+            assert _workspace.error_flag(buf) == 0

@@ -1,0 +1,156 @@
+"""GPU parity of the routed MoE layer (router + top-k + routed experts + shared expert)
+against the fp64 oracle, through the LatentMoE-shaped dispatcher."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import moe as omoe
+from oracle import mxfp4 as om
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def make_layer(seed, H, I, E, k, Is=0, distinct=None, router="softmax", act="silu", beta=1.0, lbeta=None,
+               renorm=True, scaling=1.0):
+    """Random layer.  `distinct` experts are generated and expert e aliases e % distinct,
+    which exercises the device pointer table at large E with little memory."""
+    from k3hip.moe import MoEConfig
+    rng = np.random.default_rng(seed)
+    D = distinct or E
+    experts_np = [(om.random_mxfp4(rng, I, H), om.random_mxfp4(rng, I, H), om.random_mxfp4(rng, H, I))
+                  for _ in range(D)]
+    experts_dev = [tuple(tuple(torch.from_numpy(a).to(DEV) for a in pair) for pair in ex) for ex in experts_np]
+    router_w = om.bf16_round((rng.standard_normal((E, H)) * 0.02).astype(np.float32))
+    w = {"gate.weight": torch.from_numpy(router_w).to(DEV).to(torch.bfloat16)}
+    bias = None
+    if router == "sigmoid_bias":
+        bias = (rng.standard_normal(E) * 0.05).astype(np.float32)
+        w["gate.e_score_correction_bias"] = torch.from_numpy(bias).to(DEV)
+    shared_np = None
+    if Is:
+        shared_np = tuple(om.bf16_round((rng.standard_normal(s) * 0.02).astype(np.float32))
+                          for s in ((Is, H), (Is, H), (H, Is)))
+        for name, a in zip(("gate", "up", "down"), shared_np):
+            w[f"shared_experts.{name}_proj.weight"] = torch.from_numpy(a).to(DEV).to(torch.bfloat16)
+    which_ix = {"w1": 0, "w3": 1, "w2": 2}
+
+    def source(layer, e, which):
+        return experts_dev[e % D][which_ix[which]]
+
+    cfg = MoEConfig(hidden_size=H, moe_intermediate_size=I, num_experts=E, num_experts_per_token=k,
+                    shared_intermediate_size=Is, moe_renormalize=renorm, routed_scaling_factor=scaling,
+                    router=router, activation=act, situ_beta=beta, situ_linear_beta=lbeta)
+    oracle_experts = {e: experts_np[e % D] for e in range(E)}
+    return cfg, w, source, router_w, bias, oracle_experts, shared_np
+
+
+def oracle_layer(x32, router_w, bias, experts, shared, cfg):
+    if cfg.router == "softmax":
+        idx, wts, raw, _ = omoe.route_softmax(x32, router_w, cfg.num_experts_per_token, cfg.moe_renormalize,
+                                              cfg.routed_scaling_factor)
+        corrected = raw
+    else:
+        idx, wts, raw, corrected = omoe.route_sigmoid_bias(x32, router_w, bias, cfg.num_experts_per_token,
+                                                           cfg.moe_renormalize, cfg.routed_scaling_factor)
+    y = omoe.moe_layer(x32, idx, wts, experts, shared, kind=cfg.activation, beta=cfg.situ_beta,
+                       linear_beta=cfg.situ_linear_beta)
+    return y, idx, wts, raw, corrected
+
+
+def topk_margin(sel, k):
+    s = np.sort(np.asarray(sel, np.float64).ravel())[::-1]
+    return s[k - 1] - s[k]
+
+
+CASES = [
+    # H, I, E, k, Is, distinct, router, act, xdt
+    (1024, 256, 16, 4, 256, None, "softmax", "silu", torch.bfloat16),
+    (1024, 256, 16, 4, 0, None, "softmax", "silu", torch.float32),
+    (2048, 384, 64, 8, 512, 8, "sigmoid_bias", "situ", torch.bfloat16),
+    (7168, 2048, 384, 8, 2048, 12, "softmax", "silu", torch.bfloat16),
+    (3584, 3072, 96, 8, 0, 6, "sigmoid_bias", "situ", torch.bfloat16),
+]
+
+
+@pytest.mark.parametrize("H,I,E,k,Is,distinct,router,act,xdt", CASES)
+def test_layer_matches_oracle(H, I, E, k, Is, distinct, router, act, xdt):
+    from k3hip.moe import RoutedMoE
+    beta, lbeta = (4.0, 25.0) if act == "situ" else (1.0, None)
+    cfg, w, source, router_w, bias, experts, shared = make_layer(H + E, H, I, E, k, Is, distinct, router, act,
+                                                                 beta, lbeta)
+    moe = RoutedMoE(cfg, 1, w, source)
+    rng = np.random.default_rng(E)
+    x32 = rng.standard_normal((1, H)).astype(np.float32)
+    if xdt == torch.bfloat16:
+        x32 = om.bf16_round(x32)
+    x = torch.from_numpy(x32).to(DEV).to(xdt)
+    y_want, idx, wts, raw, corrected = oracle_layer(x32, router_w, bias, experts, shared, cfg)
+    sel = corrected if router == "sigmoid_bias" else raw
+    assert topk_margin(sel, k) > 1e-5, "seed gives a near-tie at the top-k boundary"
+    y, r = moe(x, return_router=True)
+    got_idx = r.expert_indices.cpu().numpy()
+    assert np.array_equal(np.sort(got_idx, -1), np.sort(idx, -1))
+    order = np.argsort(got_idx[0])
+    assert np.allclose(r.expert_weights.cpu().numpy()[0][order], wts[0][np.argsort(idx[0])], rtol=0, atol=1e-5)
+    assert np.allclose(r.raw_scores.cpu().numpy(), raw, rtol=1e-4, atol=1e-6)
+    assert om.normwise_rel(y.cpu().numpy(), y_want) < 2e-5
+
+
+def test_route_only_matches_layer_record_and_invariants():
+    """The invariants of tests/test_k3ref_layers.py:113-127 on the sigmoid+bias router:
+    k distinct experts, weights renormalise to the scaling factor, selection follows the
+    corrected scores, weights come from the raw scores."""
+    from k3hip.moe import RoutedMoE
+    cfg, w, source, *_ = make_layer(3, 1024, 256, 64, 8, 0, 4, "sigmoid_bias", "silu", scaling=2.5)
+    moe = RoutedMoE(cfg, 0, w, source)
+    x = torch.randn(3, 1024, device=DEV).to(torch.bfloat16)
+    r = moe.route(x)
+    idx = r.expert_indices
+    assert all(len(set(row.tolist())) == 8 for row in idx)
+    assert torch.allclose(r.expert_weights.sum(-1), torch.full((3,), 2.5, device=idx.device), atol=1e-5)
+    assert torch.equal(idx.sort(-1).values, r.corrected_scores.topk(8, -1).indices.sort(-1).values)
+    raw_k = r.raw_scores.gather(1, idx)
+    assert torch.allclose(raw_k / raw_k.sum(-1, keepdim=True) * 2.5, r.expert_weights, atol=1e-6)
+    _, r2 = moe(x, return_router=True)
+    assert torch.equal(r2.expert_indices, idx) and torch.equal(r2.expert_weights, r.expert_weights)
+
+
+def test_layer_deterministic_and_graph_replay():
+    from k3hip.moe import RoutedMoE
+    cfg, w, source, *_ = make_layer(11, 2048, 512, 32, 8, 512, 8)
+    moe = RoutedMoE(cfg, 0, w, source)
+    xs = [torch.randn(1, 2048, device=DEV).to(torch.bfloat16) for _ in range(3)]
+    ref = [moe(x).clone() for x in xs]
+    for _ in range(5):
+        for x, r in zip(xs, ref):
+            assert torch.equal(moe(x), r)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        outs = [moe(x) for x in xs]
+    for _ in range(4):
+        g.replay()
+        torch.cuda.synchronize()
+        for o, r in zip(outs, ref):
+            assert torch.equal(o, r)
+        assert torch.equal(moe(xs[0]), ref[0])   # eager work between replays
+
+
+def test_layer_multi_token_and_unfused_expert():
+    from k3hip.moe import RoutedMoE
+    cfg, w, source, router_w, bias, experts, shared = make_layer(5, 1024, 256, 16, 4, 256)
+    moe = RoutedMoE(cfg, 0, w, source)
+    x32 = om.bf16_round(np.random.default_rng(1).standard_normal((3, 1024)).astype(np.float32))
+    y = moe(torch.from_numpy(x32).to(DEV).to(torch.bfloat16)).cpu().numpy()
+    for t in range(3):
+        want = oracle_layer(x32[t:t + 1], router_w, bias, experts, shared, cfg)[0]
+        assert om.normwise_rel(y[t:t + 1], want) < 2e-5
+    # the fused=False debug path: bf16-decoded weights, fp32 matmuls
+    h = torch.from_numpy(x32[:1]).to(DEV)
+    ref_moe = RoutedMoE(cfg, 0, w, source, fused=False)
+    a = ref_moe.expert_forward(h, 3).cpu().numpy()
+    b = moe.expert_forward(h, 3).cpu().numpy()
+    want = omoe.expert_ffn(x32[:1], *experts[3])[0]
+    assert om.normwise_rel(a, want) < 1e-4 and om.normwise_rel(b, want) < 1e-5
