@@ -1,0 +1,192 @@
+"""GPU parity of the latent-MLA absorbed decode kernels against the fp64 oracle.
+
+Tolerance: normwise max-relative error (max|got - want| / max|want|) <= 1e-3, the bar of
+the matvec gate; the hi/lo-split MFMA path is expected near 1e-5.  Cache and weights are
+bf16 (the benchmark's storage); the oracle reads the same bf16 values as float64.
+"""
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import mla as omla
+from oracle import mxfp4 as om
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+TOL = 1e-3
+
+
+def bf(a):
+    return om.bf16_round(np.asarray(a, np.float32))
+
+
+def make(seed, H, T, nope=128, v=128, cap=None, wstd=0.02):
+    rng = np.random.default_rng(seed)
+    q_nope = bf(rng.standard_normal((H, nope)))
+    q_rot = bf(rng.standard_normal((H, 64)))
+    w_uk = bf(rng.standard_normal((H, nope, 512)) * wstd)
+    w_uv = bf(rng.standard_normal((H, v, 512)) * wstd)
+    lat = bf(rng.standard_normal((T, 512)))
+    rot = bf(rng.standard_normal((T, 64)))
+    return q_nope, q_rot, w_uk, w_uv, lat, rot
+
+
+def to_dev(a, dtype=torch.bfloat16):
+    return torch.from_numpy(np.ascontiguousarray(a)).to(DEV).to(dtype)
+
+
+def run(q_nope, q_rot, w_uk, w_uv, lat, rot, scale, qdtype=torch.bfloat16, out_dtype=torch.float32, cap=None):
+    from k3hip.mla import mla_decode_absorbed
+    T = lat.shape[0]
+    if cap:  # cache rows inside a larger backing buffer (capacity > length)
+        lb = torch.zeros(cap, 512, dtype=torch.bfloat16, device=DEV)
+        rb = torch.zeros(cap, 64, dtype=torch.bfloat16, device=DEV)
+        lb[:T] = to_dev(lat)
+        rb[:T] = to_dev(rot)
+        ld, rd = lb[:T], rb[:T]
+    else:
+        ld, rd = to_dev(lat), to_dev(rot)
+    out = mla_decode_absorbed(to_dev(q_nope, qdtype), to_dev(q_rot, qdtype), to_dev(w_uk), to_dev(w_uv), ld, rd,
+                              scale, out_dtype=out_dtype)
+    torch.cuda.synchronize()
+    return out.float().cpu().numpy()
+
+
+@pytest.mark.parametrize("H,T", [(32, 1), (32, 5), (32, 31), (32, 32), (32, 33), (64, 100), (64, 257),
+                                 (8, 48), (96, 777), (64, 4096), (16, 4321)])
+def test_mla_decode_matches_oracle(H, T):
+    args = make(1000 + H + T, H, T)
+    scale = 192 ** -0.5
+    got = run(*args, scale)
+    want = omla.mla_decode_absorbed(*args, scale)[0]
+    rel = om.normwise_rel(got, want)
+    print(f"H={H} T={T} rel={rel:.3e}")
+    assert rel <= TOL, rel
+    assert rel <= 1e-4, f"hi/lo MFMA path should be near fp32: {rel:.3e}"
+
+
+def test_mla_decode_full_size_config():
+    """64 heads, 32768 cached tokens, kv_lora_rank 512 + rope 64, scale 1/sqrt(192)."""
+    args = make(1005, 64, 32768)
+    got = run(*args, 192 ** -0.5)
+    want = omla.mla_decode_absorbed(*args, 192 ** -0.5)[0]
+    rel = om.normwise_rel(got, want)
+    print(f"full size rel={rel:.3e}")
+    assert rel <= TOL
+
+
+def test_mla_decode_strided_cache_and_fp32_query_and_bf16_out():
+    args = list(make(7, 64, 600))
+    rng = np.random.default_rng(8)
+    args[0] = rng.standard_normal(args[0].shape).astype(np.float32)   # fp32 queries (not bf16-exact)
+    args[1] = rng.standard_normal(args[1].shape).astype(np.float32)
+    want = omla.mla_decode_absorbed(*args, 0.07)[0]
+    got = run(*args, 0.07, qdtype=torch.float32, cap=1024)
+    assert om.normwise_rel(got, want) <= 1e-4
+    got16 = run(*args, 0.07, qdtype=torch.float32, cap=1024, out_dtype=torch.bfloat16)
+    assert np.array_equal(got16, om.bf16_round(got.astype(np.float32))) or om.normwise_rel(got16, want) <= 4e-3
+
+
+def test_mla_decode_peaked_softmax():
+    """Large scores (scale 1): the softmax concentrates on a few tokens; the running max
+    must carry the rescaling exactly across tiles and splits."""
+    args = make(9, 32, 3000, wstd=0.2)
+    got = run(*args, 1.0)
+    want = omla.mla_decode_absorbed(*args, 1.0)[0]
+    assert om.normwise_rel(got, want) <= TOL
+
+
+def test_mla_decode_is_deterministic():
+    args = make(10, 64, 5000)
+    a = run(*args, 0.1)
+    b = run(*args, 0.1)
+    assert np.array_equal(a, b)
+
+
+def test_mla_decode_errors():
+    from k3hip.mla import mla_decode_absorbed
+    q = torch.zeros(32, 128, dtype=torch.bfloat16, device=DEV)
+    qr = torch.zeros(32, 64, dtype=torch.bfloat16, device=DEV)
+    wk = torch.zeros(32, 128, 512, dtype=torch.bfloat16, device=DEV)
+    wv = torch.zeros(32, 128, 512, dtype=torch.bfloat16, device=DEV)
+    lat = torch.zeros(10, 512, dtype=torch.bfloat16, device=DEV)
+    rot = torch.zeros(10, 64, dtype=torch.bfloat16, device=DEV)
+    with pytest.raises(ValueError):
+        mla_decode_absorbed(q, qr, wk, wv, lat[:0], rot[:0], 0.1)            # empty cache
+    with pytest.raises(ValueError):
+        mla_decode_absorbed(q, qr, wk, wv, lat, rot[:9], 0.1)                # T mismatch
+    with pytest.raises(TypeError):
+        mla_decode_absorbed(q, qr, wk, wv, lat.float(), rot.float(), 0.1)    # fp32 cache
+    with pytest.raises(ValueError):
+        mla_decode_absorbed(q, qr, wk[:, :, :256], wv[:, :, :256], lat[:, :256], rot, 0.1)  # r != 512
+
+
+# ------------------------------------------------------------------ layer gates N1 / N2
+
+@dataclass
+class Cfg:
+    hidden_size: int = 512
+    num_attention_heads: int = 8
+    q_lora_rank: int = 384
+    kv_lora_rank: int = 512
+    qk_nope_head_dim: int = 128
+    qk_rope_head_dim: int = 64
+    v_head_dim: int = 128
+    rms_norm_eps: float = 1e-5
+    mla_use_output_gate: bool = True
+
+    @property
+    def q_head_dim(self):
+        return self.qk_nope_head_dim + self.qk_rope_head_dim
+
+
+def test_mla_layer_incremental_decode_matches_one_shot_oracle():
+    """Gates N1/N2 (tests/test_mla_cache.py:229-255) restated: prefill, then decode token
+    by token through the HIP core; every step's output must match the fp64 one-shot layer.
+    The cache is bf16, so the oracle runs on the same bf16-rounded latents: its kv path is
+    re-derived from the cache the module actually stored."""
+    from k3hip.mla import MLAAttention
+    cfg = Cfg()
+    rng = np.random.default_rng(11)
+    w32 = omla.random_mla_weights(rng, cfg)
+    w32["kv_b_proj.weight"] = bf(w32["kv_b_proj.weight"])
+    wdev = {k: torch.from_numpy(v).to(DEV) for k, v in w32.items()}
+    attn = MLAAttention(cfg, wdev)
+    T, prefill = 40, 33
+    x = (rng.standard_normal((1, T, cfg.hidden_size)) * 0.5).astype(np.float32)
+    xd = torch.from_numpy(x).to(DEV)
+    out, cache = attn(xd[:, :prefill])
+    steps = [out.cpu().numpy()]
+    for t in range(prefill, T):
+        o, cache = attn(xd[:, t:t + 1], cache=cache)
+        steps.append(o.cpu().numpy())
+    inc = np.concatenate(steps, axis=1)[0]
+    assert cache.length == T
+    # oracle on the stored (bf16) latents: rebuild the per-step expectation from the core
+    lat = cache.latent[0, :T].float().cpu().numpy().astype(np.float64)
+    rot = cache.rot[0, :T].float().cpu().numpy().astype(np.float64)
+    w = {k: v.astype(np.float64) for k, v in w32.items()}
+    nh, nope, klr, vhd = cfg.num_attention_heads, 128, 512, 128
+    kb = w["kv_b_proj.weight"].reshape(nh, nope + vhd, klr)
+    rms = lambda a, g: g * a / np.sqrt((a * a).mean(-1, keepdims=True) + cfg.rms_norm_eps)  # noqa: E731
+    worst = 0.0
+    for t in range(prefill, T):
+        q = (rms(x[0, t].astype(np.float64) @ w["q_a_proj.weight"].T, w["q_a_layernorm.weight"])
+             @ w["q_b_proj.weight"].T).reshape(nh, cfg.q_head_dim)
+        o = omla.mla_decode_absorbed(q[:, :nope], q[:, nope:], kb[:, :nope], kb[:, nope:], lat[:t + 1],
+                                     rot[:t + 1], cfg.q_head_dim ** -0.5)[0].reshape(-1)
+        o = o / (1.0 + np.exp(-(x[0, t].astype(np.float64) @ w["g_proj.weight"].T)))
+        want = o @ w["o_proj.weight"].T
+        worst = max(worst, om.normwise_rel(inc[t], want))
+    print(f"worst decode-step rel {worst:.3e}")
+    assert worst <= TOL
+    # and the fp64 expanded one-shot layer (fp32 latents) within the bf16 cache's rounding
+    full = omla.mla_layer_expanded(cfg, w, x)[0]
+    assert om.normwise_rel(inc[prefill:], full[prefill:]) <= 2e-2
+    assert cache.bytes_per_token() == (512 + 64) * 2
+    assert cache.nbytes_used() == T * (512 + 64) * 2
