@@ -152,6 +152,55 @@ def bench_layer(torch, steps, warmup, dev):
     return sec, len(touched)
 
 
+MLA_H, MLA_T = 64, 32768
+MLA_BYTES = MLA_T * (512 + 64) * 2 + 2 * MLA_H * 128 * 512 * 2 + MLA_H * 192 * 2 + MLA_H * 128 * 4  # 54,575,104
+
+
+def bench_mla(torch, steps, warmup, dev):
+    """Latent-MLA absorbed decode: 64 heads over a 32768-token bf16 latent cache
+    (kv_lora_rank 512 + rope 64), W_UK / W_UV [64, 128, 512] bf16, scale 1/sqrt(192).
+    16 distinct caches and 8 weight sets rotate (737 MB) so the MALL cannot hold them."""
+    from k3hip.mla import mla_decode_absorbed
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(1005)
+    bf = torch.bfloat16
+    caches = [(torch.randn(MLA_T, 512, device=dev, generator=gen).to(bf),
+               torch.randn(MLA_T, 64, device=dev, generator=gen).to(bf)) for _ in range(16)]
+    weights = [((torch.randn(MLA_H, 128, 512, device=dev, generator=gen) * 0.02).to(bf),
+                (torch.randn(MLA_H, 128, 512, device=dev, generator=gen) * 0.02).to(bf)) for _ in range(8)]
+    q_nope = torch.randn(MLA_H, 128, device=dev, generator=gen).to(bf)
+    q_rot = torch.randn(MLA_H, 64, device=dev, generator=gen).to(bf)
+    scale = 192 ** -0.5
+
+    def step(i):
+        wk, wv = weights[i % 8]
+        lat, rot = caches[i % 16]
+        mla_decode_absorbed(q_nope, q_rot, wk, wv, lat, rot, scale)
+
+    sec, _ = graph_time(torch, step, steps, warmup)
+    del caches, weights
+    return sec
+
+
+def bench_read_ceiling(torch, nbytes, steps, dev):
+    """One streaming-read launch of nbytes (the library's calibration kernel), rotating
+    over >= 1.5 GB of buffers: the bandwidth a single launch of this size can reach."""
+    import ctypes
+    from k3hip import _lib
+    nbuf = max(4, min(64, -(-(3 << 29) // nbytes)))
+    bufs = [torch.empty(nbytes, dtype=torch.uint8, device=dev) for _ in range(nbuf)]
+    sink = torch.empty(4096, dtype=torch.uint8, device=dev)
+
+    def step(i):
+        st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+        _lib.call("k3_stream_read", ctypes.c_void_p(bufs[i % nbuf].data_ptr()), nbytes,
+                  ctypes.c_void_p(sink.data_ptr()), st)
+
+    sec, _ = graph_time(torch, step, steps, 8)
+    del bufs
+    return sec / steps
+
+
 def bench_cpu(sample_s=12.0):
     """torch-CPU restatement of the k3ref expert path (k3ref/layers.py:226-234 with the
     decode of k3ref/weights.py:29-37 on every access), timed on this host."""
@@ -182,7 +231,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=64)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
-    ap.add_argument("--workloads", default="expert,layer,gemv")
+    ap.add_argument("--workloads", default="expert,layer,gemv,mla,ceiling")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build runs on one GPU only (no multi-GPU path); use --gpus 1",
@@ -233,6 +282,26 @@ def main():
                              "bytes_per_layer": LAYER_BYTES, "experts": E_LAYER, "top_k": TOPK,
                              "shared_expert": "bf16", "distinct_experts_routed_first32": touched,
                              "launches_per_layer": 3}
+    if "mla" in work:
+        ms = min(K, 256)
+        msec = bench_mla(torch, ms, min(W, 32), dev)
+        mus = msec / ms * 1e6
+        mgbs = MLA_BYTES / (mus * 1e-6) / 1e9
+        line["mla_decode"] = {"us": round(mus, 2), "GB/s": round(mgbs, 1),
+                              "pct_hbm_peak": round(100 * mgbs / HBM_PEAK_GBS, 1), "bytes": MLA_BYTES,
+                              "heads": MLA_H, "tokens": MLA_T, "kv_lora_rank": 512, "rope": 64,
+                              "cache": "bf16", "launches": 4}
+    if "ceiling" in work:
+        ce = bench_read_ceiling(torch, EXPERT_BYTES, 256, dev)
+        cl = bench_read_ceiling(torch, LAYER_BYTES, 64, dev)
+        line["read_ceiling"] = {
+            "what": "single streaming-read launch of the same byte count (k3_stream_read)",
+            "expert_bytes_us": round(ce * 1e6, 3), "expert_bytes_GB/s": round(EXPERT_BYTES / ce / 1e9, 1),
+            "layer_bytes_us": round(cl * 1e6, 2), "layer_bytes_GB/s": round(LAYER_BYTES / cl / 1e9, 1)}
+        line["pct_of_measured_read"] = round(100 * gbs / (EXPERT_BYTES / ce / 1e9), 1)
+        if "moe_layer" in line:
+            line["moe_layer"]["pct_of_measured_read"] = round(
+                100 * line["moe_layer"]["GB/s"] / (LAYER_BYTES / cl / 1e9), 1)
     if "gemv" in work:
         gsec = bench_gemv(torch, K, W, dev)
         gus = gsec / K * 1e6

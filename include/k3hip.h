@@ -145,7 +145,7 @@ int64_t k3_mla_workspace_size(int64_t H, int64_t T);
  *   lat [T, r] rows ld_lat apart, rot [T, rope] rows ld_rot apart: the bf16 latent cache
  *   out [H, v] rows ld_out apart, out_dtype K3_F32 / K3_BF16
  * kv_lora_rank must be 512 and rope_dim 64 (Kimi-K3 and the benchmark shapes); nope <= 256;
- * v a multiple of 32; ld_lat and ld_rot multiples of 8; T >= 1.  fp32 accumulation, fp32
+ * v <= 1024; ld_lat and ld_rot multiples of 8; T >= 1.  fp32 accumulation, fp32
  * softmax, deterministic.
  * Replaces the absorbed attention core of MLAAttention.__call__
  * (air_llm/models/kimi_k3/attention_mla.py:193-212) for T == 1. */
@@ -155,6 +155,18 @@ int k3_mla_decode_absorbed(const void *q_nope, const void *q_rot, int64_t ld_q, 
                            int64_t kv_lora_rank, int64_t rope_dim, int64_t nope_dim, int64_t v_dim,
                            float scale, void *out, int out_dtype, int64_t ld_out, void *workspace,
                            int64_t workspace_bytes, void *stream);
+
+/* ---- HBM calibration ------------------------------------------------------------------- */
+
+/* Streaming read of `bytes` (multiple of 16) from src; sink is a >= 4096-byte device scratch
+ * word array that keeps the loads live.  No counterpart in the reference: the benchmark's
+ * measured bandwidth ceiling for one launch of a given size, and the known-size kernel the
+ * profiler's FETCH_SIZE counter is scaled by. */
+int k3_stream_read(const void *src, int64_t bytes, void *sink, void *stream);
+
+/* Streaming copy of `bytes` (multiple of 16) from src to dst.  No counterpart in the
+ * reference: the known-size kernel the profiler's WRITE_SIZE counter is scaled by. */
+int k3_stream_copy(void *dst, const void *src, int64_t bytes, void *stream);
 
 #ifdef __cplusplus
 }

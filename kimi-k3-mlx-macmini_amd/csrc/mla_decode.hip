@@ -9,7 +9,7 @@
 //     ctx = p @ lat                       [H, r]
 //     o   = ctx @ W_UV^T                  [H, v]
 // The reference upcasts the whole cache prefix to fp32 every step (attention_mla.py:85-87).
-// Here the cache stays bf16 and is read once; three stream-ordered launches:
+// Here the cache stays bf16 and is read once; four stream-ordered launches:
 //
 //   Q   qa[h] = q_nope[h] @ W_UK[h] in fp32, stored as a bf16 hi/lo pair
 //       (hi = rne(qa), lo = rne(qa - hi)), together with q_rot in columns 512..575, so the
@@ -21,8 +21,9 @@
 //       online softmax (base 2, running max and sum per head) turns them into P, split
 //       again into a bf16 hi/lo pair; ctx[32 x 512] += P_hi @ tile + P_lo @ tile on MFMA.
 //       The block writes its unnormalised (ctx, max, sum) record per head.
-//   M   per (head, 32 output rows): log-sum-exp merge of the split records in a fixed
-//       order, then o = W_UV[h] @ ctx in fp32.
+//   M   per (head, quarter of the latent columns): log-sum-exp merge of the split records
+//       in a fixed order into the normalised ctx.
+//   U   o = W_UV[h] @ ctx[h] in fp32, 32 output rows per block.
 //
 // Numerics: lat, rot, W_UK, W_UV and bf16 queries are exact in the MFMA inputs; the fp32
 // operands (qa, P) are carried as hi + lo bf16 pairs, so each product is represented to
@@ -40,21 +41,41 @@ constexpr int kK = kR + kRope;   // score contraction length
 constexpr int kQaLd = kK;        // row stride of the qa hi/lo arrays in the workspace
 constexpr int kLdsRow = kK + 8;  // padded LDS row (1168 B): conflict-free 16-byte row reads
 constexpr int kTile = 32;        // tokens per tile
-constexpr int kHG = 32;          // heads per attention block
+constexpr int kHG = 16;          // heads per attention block (one MFMA row tile)
 constexpr int kPRow = kTile + 8; // padded P row (bf16)
 constexpr int kSRow = kTile + 1; // padded score row (fp32)
 constexpr int kPartLd = 516;     // floats per (split, head) record: ctx[512], max, sum, pad
 constexpr int kMaxSplits = 1024;
 constexpr int kChunksPerRow = kK / 8;  // 16-byte chunks per token row (64 lat + 8 rot)
 constexpr int kPre = kTile * kChunksPerRow / 256;  // chunks per thread per tile (9)
+constexpr int kKSteps = kK / 32;                   // 18 MFMA k-steps over the score contraction
 
-constexpr size_t kAttnLds = (2 * kHG + kTile) * kLdsRow * 2 + 2 * kHG * kPRow * 2 +
-                            kHG * kSRow * 4 + 3 * kHG * 4;
+// tile, P hi/lo, two partial-score planes, running max / sum / rescale
+constexpr size_t kAttnLds = kTile * kLdsRow * 2 + 2 * kHG * kPRow * 2 + 2 * kHG * kSRow * 4 + 3 * kHG * 4;
 
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 
 __device__ __forceinline__ f32x4_t mfma_bf16(bf16x8 a, bf16x8 b, f32x4_t c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+
+// Reductions over the 16 lanes of a DPP row (lanes 16r .. 16r+15), result in every lane of
+// the row: quad swaps, then half-row and row mirrors.
+template <int CTRL>
+__device__ __forceinline__ float dpp_move(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, false));
+}
+__device__ __forceinline__ float row16_max(float v) {
+    v = fmaxf(v, dpp_move<0xb1>(v));   // quad_perm [1,0,3,2]
+    v = fmaxf(v, dpp_move<0x4e>(v));   // quad_perm [2,3,0,1]
+    v = fmaxf(v, dpp_move<0x141>(v));  // row_half_mirror
+    return fmaxf(v, dpp_move<0x140>(v));  // row_mirror
+}
+__device__ __forceinline__ float row16_sum(float v) {
+    v += dpp_move<0xb1>(v);
+    v += dpp_move<0x4e>(v);
+    v += dpp_move<0x141>(v);
+    return v + dpp_move<0x140>(v);
 }
 
 // fp32 -> (hi, lo) bf16 bit patterns with hi + lo == v to ~2^-17 relative
@@ -93,10 +114,18 @@ __global__ __launch_bounds__(256) void mla_qa_kernel(QaArgs a) {
     const int rc = tid & 15, ng = tid >> 4;
     float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
     const uint16_t *wrow = a.w_uk + static_cast<int64_t>(h) * a.nope * kR + quarter * 128 + rc * 8;
-    for (int n = ng; n < a.nope; n += 16) {
-        const uint4 w = *reinterpret_cast<const uint4 *>(wrow + static_cast<int64_t>(n) * kR);
-        const float qv = qn[n];
-        const uint32_t wd[4] = {w.x, w.y, w.z, w.w};
+    uint4 wv[16];  // nope <= 256: every load of this thread in flight at once
+#pragma unroll
+    for (int u = 0; u < 16; ++u) {
+        const int n = ng + 16 * u;
+        wv[u] = n < a.nope ? *reinterpret_cast<const uint4 *>(wrow + static_cast<int64_t>(n) * kR)
+                           : make_uint4(0u, 0u, 0u, 0u);
+    }
+#pragma unroll
+    for (int u = 0; u < 16; ++u) {
+        const int n = ng + 16 * u;
+        const float qv = n < a.nope ? qn[n] : 0.f;
+        const uint32_t wd[4] = {wv[u].x, wv[u].y, wv[u].z, wv[u].w};
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             acc[2 * j] = fmaf(qv, __uint_as_float(wd[j] << 16), acc[2 * j]);
@@ -136,127 +165,132 @@ struct AttnArgs {
     int swizzle;                    // XCD-aware block -> work mapping
 };
 
-__global__ __launch_bounds__(256) void mla_attn_kernel(AttnArgs a) {
+// Block: 16 heads x one split (tiles s, s + NS, ...); 4 waves; ~44 KB of LDS and <= 128
+// VGPRs + AGPRs per lane, so two blocks share a CU and hide each other's barriers.
+//   scores  wave (nt, kh): tokens 16 nt .. +16 of the tile, k-steps 9 kh .. +9; its qa
+//           operands (hi and lo) live in registers for the whole kernel
+//   softmax 16 threads per head, 2 tokens each, over the two k-half planes
+//   ctx     wave w: latent columns 128 w .. +128 (8 MFMA column tiles); the transposed tile
+//           operand comes from ds_read_b64_tr_b16 (two per MFMA)
+__global__ __launch_bounds__(256, 2) void mla_attn_kernel(AttnArgs a) {
     extern __shared__ uint4 smem[];
-    uint16_t *qa_s = reinterpret_cast<uint16_t *>(smem);          // [2][32][kLdsRow]
-    uint16_t *lat_s = qa_s + 2 * kHG * kLdsRow;                     // [32][kLdsRow]
-    uint16_t *p_s = lat_s + kTile * kLdsRow;                        // [2][32][kPRow]
-    float *s_s = reinterpret_cast<float *>(p_s + 2 * kHG * kPRow);  // [32][kSRow]
-    float *m_run = s_s + kHG * kSRow;
+    uint16_t *lat_s = reinterpret_cast<uint16_t *>(smem);                 // [32][kLdsRow]
+    uint16_t *p_s = lat_s + kTile * kLdsRow;                                // [2][16][kPRow]
+    float *s_s = reinterpret_cast<float *>(p_s + 2 * kHG * kPRow);          // [2][16][kSRow]
+    float *m_run = s_s + 2 * kHG * kSRow;
     float *l_run = m_run + kHG;
     float *alpha = l_run + kHG;
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     // blocks b, b+8, b+16, ... share an XCD (and its L2): give them consecutive work items,
-    // so the head groups of one token range read the same tiles through one L2
+    // so the head groups of one split read the same tiles through one L2
     const int b = blockIdx.x;
     const int w = a.swizzle ? (b & 7) * (static_cast<int>(gridDim.x) >> 3) + (b >> 3) : b;
     const int HGn = (a.H + kHG - 1) / kHG;
     const int hg = w % HGn, split = w / HGn;
     const int h0 = hg * kHG;
-    const int t0 = split * a.Ts;
-    const int t_end = min(a.T, t0 + a.Ts);
-    const int ntiles = (t_end - t0 + kTile - 1) / kTile;
+    // Split s owns the 32-token tiles s, s + NS, s + 2 NS, ...: blocks that run together
+    // read neighbouring tiles.
+    const int n_all = (a.T + kTile - 1) / kTile;
+    const int ntiles = (n_all - split + a.NS - 1) / a.NS;  // >= 1: NS <= n_all
+    auto tile_base = [&](int it) { return (split + it * a.NS) * kTile; };
 
     const auto rl = make_rsrc(a.lat, a.lat_bytes);
     const auto rr = make_rsrc(a.rot, a.rot_bytes);
-    uint4 pre[kPre];
-    auto load_tile = [&](int tb) {
+    // tile = 32 rows of 64 latent chunks + 32 rows of 8 rope chunks (16 B each): 8 latent
+    // loads and 1 rope load per thread, each a uniform instruction over the wave
+    auto load_tile = [&](uint4(&buf)[kPre], int tb) {
 #pragma unroll
-        for (int i = 0; i < kPre; ++i) {
+        for (int i = 0; i < kPre - 1; ++i) {
             const int c = tid + 256 * i;
-            const int tok = c / kChunksPerRow, cc = c % kChunksPerRow;
-            const int t = tb + tok;
-            if (cc < kR / 8)
-                pre[i] = buf_load16(rl, t < t_end ? static_cast<uint32_t>(t * a.ld_lat * 2 + cc * 16) : kOobOffset);
-            else
-                pre[i] = buf_load16(rr, t < t_end ? static_cast<uint32_t>(t * a.ld_rot * 2 + (cc - kR / 8) * 16)
-                                                  : kOobOffset);
+            const int t = tb + (c >> 6);
+            buf[i] = buf_load16(rl, t < a.T ? static_cast<uint32_t>(t * a.ld_lat * 2 + (c & 63) * 16) : kOobOffset);
         }
+        const int t = tb + (tid >> 3);
+        buf[kPre - 1] = buf_load16(rr, t < a.T ? static_cast<uint32_t>(t * a.ld_rot * 2 + (tid & 7) * 16) : kOobOffset);
     };
-    load_tile(t0);
+    uint4 pre0[kPre];
+    load_tile(pre0, tile_base(0));
 
-    // qa hi/lo of this block's heads into LDS (L2-resident: written by the Q launch)
-    for (int c = tid; c < 2 * kHG * kChunksPerRow; c += 256) {
-        const int hl = c / (kHG * kChunksPerRow), rem = c % (kHG * kChunksPerRow);
-        const int hh = rem / kChunksPerRow, cc = rem % kChunksPerRow;
-        const uint16_t *src = (hl ? a.qa_lo : a.qa_hi) + (h0 + hh) * kQaLd + cc * 8;
-        // heads past H (last group of a head count that is not a multiple of 32) score 0
-        *reinterpret_cast<uint4 *>(qa_s + (hl * kHG + hh) * kLdsRow + cc * 8) =
-            h0 + hh < a.H ? *reinterpret_cast<const uint4 *>(src) : make_uint4(0u, 0u, 0u, 0u);
+    // this wave's qa operands: head h0 + (lane % 16), k-steps 9 kh .. 9 kh + 8 (L2-resident)
+    const int r16 = lane & 15, q4 = lane >> 4;
+    const int nt = wave & 1, kh = wave >> 1;
+    bf16x8 qhi[kKSteps / 2], qlo[kKSteps / 2];
+    {
+        const bool hv = h0 + r16 < a.H;  // heads past H (last group) score 0
+        const uint16_t *qh = a.qa_hi + (h0 + r16) * kQaLd + kh * (kK / 2) + q4 * 8;
+        const uint16_t *ql = a.qa_lo + (h0 + r16) * kQaLd + kh * (kK / 2) + q4 * 8;
+#pragma unroll
+        for (int k = 0; k < kKSteps / 2; ++k) {
+            const uint4 z = make_uint4(0u, 0u, 0u, 0u);
+            qhi[k] = __builtin_bit_cast(bf16x8, hv ? *reinterpret_cast<const uint4 *>(qh + k * 32) : z);
+            qlo[k] = __builtin_bit_cast(bf16x8, hv ? *reinterpret_cast<const uint4 *>(ql + k * 32) : z);
+        }
     }
     if (tid < kHG) {
         m_run[tid] = -INFINITY;
         l_run[tid] = 0.f;
     }
 
-    f32x4_t cacc[2][8];
+    f32x4_t cacc[8];
 #pragma unroll
-    for (int m = 0; m < 2; ++m)
-#pragma unroll
-        for (int n = 0; n < 8; ++n) cacc[m][n] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    for (int n = 0; n < 8; ++n) cacc[n] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
-    const int r16 = lane & 15, q4 = lane >> 4;
-    for (int it = 0; it < ntiles; ++it) {
-        const int tb = t0 + it * kTile;
+    auto tile_step = [&](int it, uint4(&buf)[kPre]) {
+        const int tb = tile_base(it);
         __syncthreads();  // previous tile's LDS reads are done
 #pragma unroll
-        for (int i = 0; i < kPre; ++i) {
+        for (int i = 0; i < kPre - 1; ++i) {
             const int c = tid + 256 * i;
-            *reinterpret_cast<uint4 *>(lat_s + (c / kChunksPerRow) * kLdsRow + (c % kChunksPerRow) * 8) = pre[i];
+            *reinterpret_cast<uint4 *>(lat_s + (c >> 6) * kLdsRow + (c & 63) * 8) = buf[i];
         }
+        *reinterpret_cast<uint4 *>(lat_s + (tid >> 3) * kLdsRow + kR + (tid & 7) * 8) = buf[kPre - 1];
         __syncthreads();
-        if (it + 1 < ntiles) load_tile(tb + kTile);
+        if (it + 1 < ntiles) load_tile(buf, tile_base(it + 1));
 
-        // ---- scores: wave -> (head half mt, token half nt), K = 576 in 18 steps
+        // ---- partial scores over this wave's k half (hi and lo chains)
         {
-            const int mt = wave & 1, nt = wave >> 1;
-            const uint16_t *ahi = qa_s + (mt * 16 + r16) * kLdsRow + q4 * 8;
-            const uint16_t *alo = ahi + kHG * kLdsRow;
-            const uint16_t *bp = lat_s + (nt * 16 + r16) * kLdsRow + q4 * 8;
-            f32x4_t sacc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll 6
-            for (int kk = 0; kk < kK / 32; ++kk) {
-                const bf16x8 bv = *reinterpret_cast<const bf16x8 *>(bp + kk * 32);
-                sacc = mfma_bf16(*reinterpret_cast<const bf16x8 *>(ahi + kk * 32), bv, sacc);
-                sacc = mfma_bf16(*reinterpret_cast<const bf16x8 *>(alo + kk * 32), bv, sacc);
-            }
-            const int tok = nt * 16 + r16;
-            const bool valid = tb + tok < t_end;
+            const uint16_t *bp = lat_s + (nt * 16 + r16) * kLdsRow + kh * (kK / 2) + q4 * 8;
+            f32x4_t sh = {0.f, 0.f, 0.f, 0.f}, sl = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-            for (int i = 0; i < 4; ++i)
-                s_s[(mt * 16 + q4 * 4 + i) * kSRow + tok] = valid ? sacc[i] * a.scale_log2 : -INFINITY;
+            for (int k = 0; k < kKSteps / 2; ++k) {
+                const bf16x8 bv = *reinterpret_cast<const bf16x8 *>(bp + k * 32);
+                sh = mfma_bf16(qhi[k], bv, sh);
+                sl = mfma_bf16(qlo[k], bv, sl);
+            }
+            const f32x4_t st = sh + sl;
+            float *sp = s_s + kh * kHG * kSRow;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) sp[(q4 * 4 + i) * kSRow + nt * 16 + r16] = st[i];
         }
         __syncthreads();
 
-        // ---- online softmax: 8 threads per head, 4 tokens each
+        // ---- online softmax: 16 threads per head, 2 tokens each
         {
-            const int hh = tid >> 3, q = tid & 7;
-            float sv[4];
+            const int hh = tid >> 4, q = tid & 15;
+            float sv[2];
             float mx = -INFINITY;
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                sv[j] = s_s[hh * kSRow + q * 4 + j];
+            for (int j = 0; j < 2; ++j) {
+                const int tok = q * 2 + j;
+                const float v = (s_s[hh * kSRow + tok] + s_s[(kHG + hh) * kSRow + tok]) * a.scale_log2;
+                sv[j] = tb + tok < a.T ? v : -INFINITY;
                 mx = fmaxf(mx, sv[j]);
             }
-            mx = fmaxf(mx, __shfl_xor(mx, 1, 8));
-            mx = fmaxf(mx, __shfl_xor(mx, 2, 8));
-            mx = fmaxf(mx, __shfl_xor(mx, 4, 8));
+            mx = row16_max(mx);
             const float mold = m_run[hh];
             const float mnew = fmaxf(mold, mx);  // finite: every tile holds a valid token
             float ps = 0.f;
-            uint16_t *ph = p_s + hh * kPRow + q * 4;
+            uint16_t *ph = p_s + hh * kPRow + q * 2;
             uint16_t *pl = ph + kHG * kPRow;
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
+            for (int j = 0; j < 2; ++j) {
                 const float p = exp2f(sv[j] - mnew);
                 ps += p;
                 split_bf16(p, ph[j], pl[j]);
             }
-            ps += __shfl_xor(ps, 1, 8);
-            ps += __shfl_xor(ps, 2, 8);
-            ps += __shfl_xor(ps, 4, 8);
+            ps = row16_sum(ps);
             if (q == 0) {
                 const float al = exp2f(mold - mnew);
                 alpha[hh] = al;
@@ -266,55 +300,53 @@ __global__ __launch_bounds__(256) void mla_attn_kernel(AttnArgs a) {
         }
         __syncthreads();
 
-        // ---- ctx[32 x 512] += P @ tile: wave owns latent columns [128 wave, +128)
+        // ---- ctx[16 x 512] += P @ tile: wave owns latent columns [128 wave, +128)
         {
-            bf16x8 ph[2], pl[2];
+            const bf16x8 ph = *reinterpret_cast<const bf16x8 *>(p_s + r16 * kPRow + q4 * 8);
+            const bf16x8 pl = *reinterpret_cast<const bf16x8 *>(p_s + (kHG + r16) * kPRow + q4 * 8);
+            float al[4];
 #pragma unroll
-            for (int m = 0; m < 2; ++m) {
-                ph[m] = *reinterpret_cast<const bf16x8 *>(p_s + (m * 16 + r16) * kPRow + q4 * 8);
-                pl[m] = *reinterpret_cast<const bf16x8 *>(p_s + (kHG + m * 16 + r16) * kPRow + q4 * 8);
+            for (int i = 0; i < 4; ++i) al[i] = alpha[q4 * 4 + i];
+            if (!__all(al[0] == 1.f && al[1] == 1.f && al[2] == 1.f && al[3] == 1.f)) {
 #pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    const float al = alpha[m * 16 + q4 * 4 + i];
+                for (int n = 0; n < 8; ++n)
 #pragma unroll
-                    for (int n = 0; n < 8; ++n) cacc[m][n][i] *= al;
-                }
+                    for (int i = 0; i < 4; ++i) cacc[n][i] *= al[i];
             }
-            const uint16_t *col = lat_s + (q4 * 8) * kLdsRow + wave * 128 + r16;
+            // transposed operand: source lane s' of group g points at token 8g + s'/4,
+            // columns c0 + 4 (s' % 4) .. +3; a second read 4 tokens further down
+            typedef short s4_t __attribute__((ext_vector_type(4)));
+            const uint16_t *tsrc = lat_s + (q4 * 8 + (r16 >> 2)) * kLdsRow + wave * 128 + (r16 & 3) * 4;
 #pragma unroll
             for (int n = 0; n < 8; ++n) {
-                uint16_t bv[8];
-#pragma unroll
-                for (int i = 0; i < 8; ++i) bv[i] = col[i * kLdsRow + n * 16];
-                const bf16x8 bb = __builtin_bit_cast(bf16x8, bv);
-#pragma unroll
-                for (int m = 0; m < 2; ++m) {
-                    cacc[m][n] = mfma_bf16(ph[m], bb, cacc[m][n]);
-                    cacc[m][n] = mfma_bf16(pl[m], bb, cacc[m][n]);
-                }
+                typedef __attribute__((address_space(3))) s4_t *lds_s4;
+                const s4_t lo4 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4)(tsrc + n * 16));
+                const s4_t hi4 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4)(tsrc + n * 16 + 4 * kLdsRow));
+                const bf16x8 bb = __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo4, hi4, 0, 1, 2, 3, 4, 5, 6, 7));
+                cacc[n] = mfma_bf16(ph, bb, cacc[n]);
+                cacc[n] = mfma_bf16(pl, bb, cacc[n]);
             }
         }
-    }
+    };
+    for (int it = 0; it < ntiles; ++it) tile_step(it, pre0);
 
     // ---- split record: unnormalised ctx, running max and sum
     float *part = a.part + (static_cast<int64_t>(split) * a.H + h0) * kPartLd;
 #pragma unroll
-    for (int m = 0; m < 2; ++m)
+    for (int n = 0; n < 8; ++n)
 #pragma unroll
-        for (int n = 0; n < 8; ++n)
-#pragma unroll
-            for (int i = 0; i < 4; ++i)
-                if (h0 + m * 16 + q4 * 4 + i < a.H)
-                    part[(m * 16 + q4 * 4 + i) * kPartLd + wave * 128 + n * 16 + r16] = cacc[m][n][i];
+        for (int i = 0; i < 4; ++i)
+            if (h0 + q4 * 4 + i < a.H) part[(q4 * 4 + i) * kPartLd + wave * 128 + n * 16 + r16] = cacc[n][i];
     if (tid < kHG && h0 + tid < a.H) {
         part[tid * kPartLd + kR] = m_run[tid];
         part[tid * kPartLd + kR + 1] = l_run[tid];
     }
 }
 
-// ------------------------------------------------------------------ M: merge + W_UV
+// ------------------------------------------------------------------ M: merge, then W_UV
 struct MergeArgs {
     const float *part;
+    float *ctx;            // [H, 512] merged, normalised context
     const uint16_t *w_uv;  // [H, V, 512] bf16
     void *out;             // [H, V] rows of ld_out elements
     int64_t ld_out;
@@ -339,50 +371,109 @@ __device__ __forceinline__ float block_max256(float v, float *red) {
     return r;
 }
 
-// grid: H * (V / 32); block (h, vq) merges head h and produces o[h][32 vq .. +32)
-__global__ __launch_bounds__(256) void mla_merge_uv_kernel(MergeArgs a) {
+// grid: H * 4; block (h, quarter): ctx[h][128 quarter .. +128) = sum_s w_s ctx_s / L with
+// w_s = 2^(m_s - M).  Fixed order: 8 groups of splits (s = g mod 8), then the groups in order.
+// Every load of a thread is issued before the first is used: the records come from the
+// last-level cache, so the cost is round trips, not bytes.
+__global__ __launch_bounds__(256) void mla_merge_kernel(MergeArgs a) {
     __shared__ float wsplit[kMaxSplits];
-    __shared__ __align__(16) float ctx[2][kR];
+    __shared__ float csum[8][129];
     __shared__ float red[4];
-    const int vqn = a.V / 32;
-    const int h = blockIdx.x / vqn, vq = blockIdx.x % vqn;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int h = blockIdx.x >> 2, quarter = blockIdx.x & 3;
+    const int tid = threadIdx.x;
     const float *rec = a.part + static_cast<int64_t>(h) * kPartLd;
     const int64_t sstride = static_cast<int64_t>(a.H) * kPartLd;
 
+    // column loads first (16 splits per thread covers NS <= 128 in one batch)
+    const int c4 = tid & 31, grp = tid >> 5;
+    const float *col = rec + quarter * 128 + 4 * c4;
+    constexpr int kPer = 16;
+    float4 v[kPer];
+#pragma unroll
+    for (int u = 0; u < kPer; ++u) {
+        const int s = grp + 8 * u;
+        v[u] = s < a.NS ? *reinterpret_cast<const float4 *>(col + s * sstride) : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+    float mv[kMaxSplits / 256], lv[kMaxSplits / 256];
     float mx = -INFINITY;
-    for (int s = tid; s < a.NS; s += 256) mx = fmaxf(mx, rec[s * sstride + kR]);
+#pragma unroll
+    for (int j = 0; j < kMaxSplits / 256; ++j) {
+        const int s = tid + 256 * j;
+        mv[j] = s < a.NS ? rec[s * sstride + kR] : -INFINITY;
+        lv[j] = s < a.NS ? rec[s * sstride + kR + 1] : 0.f;
+        mx = fmaxf(mx, mv[j]);
+    }
     const float M = block_max256(mx, red);
     float ls = 0.f;
-    for (int s = tid; s < a.NS; s += 256) {
-        const float e = exp2f(rec[s * sstride + kR] - M);
-        wsplit[s] = e;
-        ls += e * rec[s * sstride + kR + 1];
+#pragma unroll
+    for (int j = 0; j < kMaxSplits / 256; ++j) {
+        const int s = tid + 256 * j;
+        if (s < a.NS) {
+            const float e = exp2f(mv[j] - M);
+            wsplit[s] = e;
+            ls += e * lv[j];
+        }
     }
     const float inv_l = 1.0f / block_sum256(ls, red);  // block_sum256 synchronises wsplit
 
-    {   // ctx = sum_s w_s ctx_s (two fixed halves of the splits, then their sum)
-        const int r4 = tid & 127, half = tid >> 7;
-        float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
-        for (int s = half; s < a.NS; s += 2) {
-            const float ws = wsplit[s];
-            const float4 v = *reinterpret_cast<const float4 *>(rec + s * sstride + 4 * r4);
-            acc.x = fmaf(ws, v.x, acc.x);
-            acc.y = fmaf(ws, v.y, acc.y);
-            acc.z = fmaf(ws, v.z, acc.z);
-            acc.w = fmaf(ws, v.w, acc.w);
-        }
-        *reinterpret_cast<float4 *>(&ctx[half][4 * r4]) = acc;
+    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+    for (int u = 0; u < kPer; ++u) {
+        const int s = grp + 8 * u;
+        const float ws = s < a.NS ? wsplit[s] : 0.f;
+        acc.x = fmaf(ws, v[u].x, acc.x);
+        acc.y = fmaf(ws, v[u].y, acc.y);
+        acc.z = fmaf(ws, v[u].z, acc.z);
+        acc.w = fmaf(ws, v[u].w, acc.w);
     }
+    for (int s0 = grp + 8 * kPer; s0 < a.NS; s0 += 8 * kPer) {  // NS > 128
+#pragma unroll
+        for (int u = 0; u < kPer; ++u) {
+            const int s = s0 + 8 * u;
+            v[u] = s < a.NS ? *reinterpret_cast<const float4 *>(col + s * sstride) : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+#pragma unroll
+        for (int u = 0; u < kPer; ++u) {
+            const int s = s0 + 8 * u;
+            const float ws = s < a.NS ? wsplit[s] : 0.f;
+            acc.x = fmaf(ws, v[u].x, acc.x);
+            acc.y = fmaf(ws, v[u].y, acc.y);
+            acc.z = fmaf(ws, v[u].z, acc.z);
+            acc.w = fmaf(ws, v[u].w, acc.w);
+        }
+    }
+    csum[grp][4 * c4] = acc.x;
+    csum[grp][4 * c4 + 1] = acc.y;
+    csum[grp][4 * c4 + 2] = acc.z;
+    csum[grp][4 * c4 + 3] = acc.w;
     __syncthreads();
-    float c8[8];
+    if (tid < 128) {
+        float r = 0.f;
+        for (int g = 0; g < 8; ++g) r += csum[g][tid];
+        a.ctx[h * kR + quarter * 128 + tid] = r * inv_l;
+    }
+}
+
+// grid: cdiv(H * V, 32); block: 32 output rows (8 per wave) of o[h][v] = W_UV[h][v] . ctx[h];
+// lane l covers columns 8l .. 8l+7, all 8 rows' weights in flight at once
+__global__ __launch_bounds__(256) void mla_uv_kernel(MergeArgs a) {
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int64_t rows = static_cast<int64_t>(a.H) * a.V;
+    const int64_t r0 = static_cast<int64_t>(blockIdx.x) * 32 + wave * 8;
+    uint4 w[8];
 #pragma unroll
-    for (int j = 0; j < 8; ++j) c8[j] = (ctx[0][lane * 8 + j] + ctx[1][lane * 8 + j]) * inv_l;
+    for (int u = 0; u < 8; ++u) {
+        const int64_t r = r0 + u;
+        w[u] = r < rows ? *reinterpret_cast<const uint4 *>(a.w_uv + r * kR + lane * 8) : make_uint4(0u, 0u, 0u, 0u);
+    }
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-        const int v = vq * 32 + wave * 8 + j;
-        const uint4 w = *reinterpret_cast<const uint4 *>(a.w_uv + (static_cast<int64_t>(h) * a.V + v) * kR + lane * 8);
-        const uint32_t wd[4] = {w.x, w.y, w.z, w.w};
+    for (int u = 0; u < 8; ++u) {
+        const int64_t r = r0 + u;
+        const int h = static_cast<int>(min(r, rows - 1) / a.V);
+        const float4 c0 = *reinterpret_cast<const float4 *>(a.ctx + h * kR + lane * 8);
+        const float4 c1 = *reinterpret_cast<const float4 *>(a.ctx + h * kR + lane * 8 + 4);
+        const float c8[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
+        const uint32_t wd[4] = {w[u].x, w[u].y, w[u].z, w[u].w};
         float acc = 0.f;
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
@@ -390,12 +481,12 @@ __global__ __launch_bounds__(256) void mla_merge_uv_kernel(MergeArgs a) {
             acc = fmaf(__uint_as_float(wd[q] & 0xffff0000u), c8[2 * q + 1], acc);
         }
         acc = wave_sum_to_lane63(acc);
-        if (lane == 63) {
-            const int64_t o = static_cast<int64_t>(h) * a.ld_out + v;
+        if (lane == 63 && r < rows) {
+            const int64_t oi = static_cast<int64_t>(h) * a.ld_out + (r - static_cast<int64_t>(h) * a.V);
             if (a.out_bf16)
-                static_cast<uint16_t *>(a.out)[o] = f32_to_bf16(acc);
+                static_cast<uint16_t *>(a.out)[oi] = f32_to_bf16(acc);
             else
-                static_cast<float *>(a.out)[o] = acc;
+                static_cast<float *>(a.out)[oi] = acc;
         }
     }
 }
@@ -411,7 +502,7 @@ void mla_splits(int64_t T, int *Ts, int *NS) {
 }
 
 struct MlaWs {
-    size_t qa_hi, qa_lo, part, total;
+    size_t qa_hi, qa_lo, ctx, part, total;
 };
 
 MlaWs mla_ws_layout(int64_t H, int64_t T) {
@@ -422,6 +513,7 @@ MlaWs mla_ws_layout(int64_t H, int64_t T) {
     size_t o = 0;
     L.qa_hi = o, o += up(static_cast<size_t>(H) * kQaLd * 2);
     L.qa_lo = o, o += up(static_cast<size_t>(H) * kQaLd * 2);
+    L.ctx = o, o += up(static_cast<size_t>(H) * kR * 4);
     L.part = o, o += up(static_cast<size_t>(NS) * H * kPartLd * 4);
     L.total = o;
     return L;
@@ -452,8 +544,8 @@ extern "C" int k3_mla_decode_absorbed(const void *q_nope, const void *q_rot, int
         return set_error(K3_ERR_SHAPE, "mla decode: kv_lora_rank=%lld rope=%lld; the kernels take 512 and 64",
                          (long long)kv_lora_rank, (long long)rope_dim);
     if (H <= 0 || H > 4096) return set_error(K3_ERR_SHAPE, "mla decode: H=%lld must be in 1..4096", (long long)H);
-    if (nope_dim <= 0 || nope_dim > 256 || v_dim <= 0 || v_dim % 32)
-        return set_error(K3_ERR_SHAPE, "mla decode: nope=%lld must be in 1..256 and v=%lld a multiple of 32",
+    if (nope_dim <= 0 || nope_dim > 256 || v_dim <= 0 || v_dim > 1024)
+        return set_error(K3_ERR_SHAPE, "mla decode: nope=%lld must be in 1..256 and v=%lld in 1..1024",
                          (long long)nope_dim, (long long)v_dim);
     if (T <= 0) return set_error(K3_ERR_SHAPE, "mla decode: empty cache (T=%lld)", (long long)T);
     if (ld_q < nope_dim || ld_lat < kR || ld_rot < kRope || ld_out < v_dim || ld_lat % 8 || ld_rot % 8)
@@ -502,17 +594,16 @@ extern "C" int k3_mla_decode_absorbed(const void *q_nope, const void *q_rot, int
     aa.scale_log2 = scale * 1.4426950408889634f;
     const int blocks = NS * static_cast<int>(cdiv(H, kHG));
     aa.swizzle = blocks % 8 == 0;
-    static_assert(kAttnLds <= 160 * 1024, "attention LDS");
-    rc = check_hip(hipFuncSetAttribute(reinterpret_cast<const void *>(&mla_attn_kernel),
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(kAttnLds)),
-                   "mla decode: raise LDS limit");
-    if (rc) return rc;
+    static_assert(kAttnLds <= 64 * 1024, "attention LDS: two blocks per CU");
     mla_attn_kernel<<<dim3(static_cast<unsigned>(blocks)), 256, kAttnLds, st>>>(aa);
     rc = check_hip(hipGetLastError(), "mla decode: attention launch");
     if (rc) return rc;
 
-    MergeArgs ma{part, static_cast<const uint16_t *>(w_uv), out, ld_out, static_cast<int>(H), NS,
-                 static_cast<int>(v_dim), out_dtype == K3_BF16};
-    mla_merge_uv_kernel<<<dim3(static_cast<unsigned>(H * (v_dim / 32))), 256, 0, st>>>(ma);
-    return check_hip(hipGetLastError(), "mla decode: merge launch");
+    MergeArgs ma{part, reinterpret_cast<float *>(ws + L.ctx), static_cast<const uint16_t *>(w_uv), out, ld_out,
+                 static_cast<int>(H), NS, static_cast<int>(v_dim), out_dtype == K3_BF16};
+    mla_merge_kernel<<<dim3(static_cast<unsigned>(H * 4)), 256, 0, st>>>(ma);
+    rc = check_hip(hipGetLastError(), "mla decode: merge launch");
+    if (rc) return rc;
+    mla_uv_kernel<<<dim3(static_cast<unsigned>(cdiv(H * v_dim, 32))), 256, 0, st>>>(ma);
+    return check_hip(hipGetLastError(), "mla decode: W_UV launch");
 }

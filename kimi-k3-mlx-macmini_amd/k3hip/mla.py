@@ -3,8 +3,8 @@ air_llm/models/kimi_k3/attention_mla.py (``MLACache``, ``MLAAttention``).
 
 ``mla_decode_absorbed(q_nope, q_rot, wk, wv, lat, rot, scale)`` is the attention core of
 ``MLAAttention.__call__`` for one decode token (``attention_mla.py:193-212``): it runs on
-the bf16 latent cache in place (three HIP launches: query absorption, split-T flash
-decoding on bf16 MFMA with hi/lo-split fp32 operands, log-sum-exp merge fused with the
+the bf16 latent cache in place (four HIP launches: query absorption, split-T flash
+decoding on bf16 MFMA with hi/lo-split fp32 operands, log-sum-exp merge of the splits, the
 W_UV absorption) and returns ``[H, v_head_dim]``.
 
 ``MLACache`` keeps the reference's surface (``latent``/``rot`` backing buffers with spare
