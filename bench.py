@@ -118,12 +118,25 @@ def bench_gemv(torch, steps, warmup, dev):
     return sec
 
 
+_EXPERTS = []
+
+
+def resident_experts(torch, dev):
+    """384 distinct MXFP4 experts (8.98 GB), built once and shared by the layer and
+    prefill workloads."""
+    if not _EXPERTS:
+        gen = torch.Generator(device=dev)
+        gen.manual_seed(1003)
+        _EXPERTS.extend((rand_mxfp4(torch, gen, I, H, dev), rand_mxfp4(torch, gen, I, H, dev),
+                         rand_mxfp4(torch, gen, H, I, dev)) for _ in range(E_LAYER))
+    return _EXPERTS
+
+
 def build_layer(torch, dev):
     from k3hip.moe import MoEConfig, RoutedMoE
     gen = torch.Generator(device=dev)
     gen.manual_seed(1003)
-    experts = [(rand_mxfp4(torch, gen, I, H, dev), rand_mxfp4(torch, gen, I, H, dev),
-                rand_mxfp4(torch, gen, H, I, dev)) for _ in range(E_LAYER)]
+    experts = resident_experts(torch, dev)
     w = {"gate.weight": (torch.randn(E_LAYER, H, device=dev, generator=gen) * 0.02).to(torch.bfloat16)}
     for name, shape in (("gate", (I, H)), ("up", (I, H)), ("down", (H, I))):
         w[f"shared_experts.{name}_proj.weight"] = (torch.randn(*shape, device=dev, generator=gen) * 0.02
@@ -148,8 +161,52 @@ def bench_layer(torch, steps, warmup, dev):
     # distinct experts the timed tokens routed to (evidence the MALL could not hold them)
     for i in range(min(steps, 32)):
         touched.update(moe.route(xs[i:i + 1]).expert_indices.view(-1).tolist())
-    del moe, experts
+    del moe
     return sec, len(touched)
+
+
+PF_T, PF_K = 2048, 8
+PF_FLOPS = 2 * PF_T * PF_K * 3 * H * I                                   # 1.443e12 useful
+
+
+def zipf_routing(T, E, k, s=1.1, seed=1004):
+    """k distinct experts per token, drawn without replacement with probability ~ r^-s over a
+    seeded permutation of the experts (Gumbel top-k); combine weights softmax(N(0,1))."""
+    import numpy as np
+    rng = np.random.default_rng(seed)
+    perm = rng.permutation(E)
+    logw = -s * np.log(np.arange(1, E + 1, dtype=np.float64))[np.argsort(perm)]
+    g = logw[None, :] - np.log(-np.log(rng.random((T, E))))
+    idx = np.argsort(-g, axis=1)[:, :k].astype(np.int32)
+    z = rng.standard_normal((T, k))
+    w = np.exp(z - z.max(axis=1, keepdims=True))
+    return idx, (w / w.sum(axis=1, keepdims=True)).astype(np.float32)
+
+
+def bench_prefill(torch, steps, warmup, dev):
+    """Grouped MoE prefill: 2048 bf16 tokens (hidden 7168), top-8 over the 384 resident
+    MXFP4 experts with Zipf(1.1) load; one step = the whole batch through the grouping
+    pass, both grouped GEMMs and the combine."""
+    import numpy as np
+    from k3hip.moe import moe_grouped_ffn
+    experts = resident_experts(torch, dev)
+    table = torch.tensor([[t.data_ptr() for pair in ex for t in pair] for ex in experts], dtype=torch.int64,
+                         device=dev)
+    idx_np, w_np = zipf_routing(PF_T, E_LAYER, PF_K)
+    idx = torch.from_numpy(idx_np).to(dev)
+    w = torch.from_numpy(w_np).to(dev)
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(1004)
+    x = torch.randn(PF_T, H, device=dev, generator=gen).to(torch.bfloat16)
+
+    def step(i):
+        moe_grouped_ffn(x, idx, w, table, I, validate=False)
+
+    sec, _ = graph_time(torch, step, steps, warmup)
+    counts = np.bincount(idx_np.ravel(), minlength=E_LAYER)
+    used = int((counts > 0).sum())
+    bytes_ = used * EXPERT_BYTES + PF_T * H * 2 + PF_T * H * 4
+    return sec / steps, bytes_, counts
 
 
 MLA_H, MLA_T = 64, 32768
@@ -231,7 +288,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=64)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
-    ap.add_argument("--workloads", default="expert,layer,gemv,mla,ceiling")
+    ap.add_argument("--workloads", default="expert,layer,prefill,gemv,mla,ceiling")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build runs on one GPU only (no multi-GPU path); use --gpus 1",
@@ -282,6 +339,16 @@ def main():
                              "bytes_per_layer": LAYER_BYTES, "experts": E_LAYER, "top_k": TOPK,
                              "shared_expert": "bf16", "distinct_experts_routed_first32": touched,
                              "launches_per_layer": 3}
+    if "prefill" in work:
+        pst, pbytes, counts = bench_prefill(torch, 8, 2, dev)
+        line["moe_prefill"] = {
+            "ms": round(pst * 1e3, 3), "GB/s": round(pbytes / pst / 1e9, 1),
+            "pct_hbm_peak": round(100 * pbytes / pst / 1e9 / HBM_PEAK_GBS, 1), "bytes": pbytes,
+            "useful_TFLOP/s": round(PF_FLOPS / pst / 1e12, 1),
+            "pct_bf16_mfma_peak": round(100 * PF_FLOPS / pst / 2.5e15, 1),
+            "tokens": PF_T, "top_k": PF_K, "experts": E_LAYER, "routing": "zipf(1.1), seeded",
+            "expert_load": {"max": int(counts.max()), "mean": round(float(counts.mean()), 1),
+                            "empty": int((counts == 0).sum())}}
     if "mla" in work:
         ms = min(K, 256)
         msec = bench_mla(torch, ms, min(W, 32), dev)

@@ -132,6 +132,27 @@ int k3_moe_layer_decode(const void *x, int x_dtype, const void *router_w, const 
                         int64_t n_experts, int64_t top_k, int act_kind, float beta,
                         float linear_beta, void *workspace, int64_t workspace_bytes, void *stream);
 
+/* ---- grouped routed experts for many tokens (prefill) ------------------------------------ */
+
+/* Workspace bytes k3_moe_grouped_ffn needs (grouping records, the bf16 hi/lo activations of
+ * every routed pair, fp32 per-pair expert outputs).  No initialisation. */
+int64_t k3_moe_grouped_workspace_size(int64_t T, int64_t top_k, int64_t n_experts, int64_t H, int64_t I);
+
+/* y[t] = sum_j w[t, j] * expert_{idx[t, j]}(x[t]) for T tokens at once:
+ *   x bf16 [T, H]; expert_idx int32 [T, top_k] (every id in 0..n_experts-1); expert_w f32
+ *   [T, top_k]; expert_table as in k3_moe_layer_decode (packed pointers 16-byte aligned,
+ *   scale pointers 2-byte aligned, E8M0 bytes 2..252); out [T, H] f32 or bf16.
+ * The (token, slot) pairs are grouped by expert on the device and each expert runs as a
+ * bf16-MFMA GEMM with M = its token count (weights decoded exactly in registers), so each
+ * expert's weights are read once per 32-token tile group.  Deterministic.  H and I must be
+ * multiples of 64.
+ * Replaces the per-expert dispatch loop of LatentMoE.__call__
+ * (air_llm/models/kimi_k3/moe.py:110-132; k3ref/layers.py:241-261) for prefill. */
+int k3_moe_grouped_ffn(const void *x, int x_dtype, const int32_t *expert_idx, const float *expert_w,
+                       const void *expert_table, void *out, int out_dtype, int64_t T, int64_t H,
+                       int64_t I, int64_t n_experts, int64_t top_k, int act_kind, float beta,
+                       float linear_beta, void *workspace, int64_t workspace_bytes, void *stream);
+
 /* ---- latent-MLA absorbed decode (one query token, batch 1) ------------------------------ */
 
 /* Workspace bytes k3_mla_decode_absorbed needs for H heads over T cached tokens (qa

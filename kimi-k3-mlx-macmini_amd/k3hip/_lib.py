@@ -45,13 +45,17 @@ SIGNATURES: dict[str, list] = {
     "k3_mla_workspace_size": [_I64, _I64],
     "k3_mla_decode_absorbed": [_P, _P, _I64, _I32, _P, _P, _P, _I64, _P, _I64, _I64, _I64, _I64, _I64, _I64,
                                _I64, _F32, _P, _I32, _I64, _P, _I64, _P],
+    "k3_moe_grouped_workspace_size": [_I64, _I64, _I64, _I64, _I64],
+    "k3_moe_grouped_ffn": [_P, _I32, _P, _P, _P, _P, _I32, _I64, _I64, _I64, _I64, _I64, _I32, _F32, _F32,
+                           _P, _I64, _P],
     "k3_stream_read": [_P, _I64, _P, _P],
     "k3_stream_copy": [_P, _P, _I64, _P],
 }
 _RESTYPE = {"k3_last_error": ctypes.c_char_p, "k3_version": ctypes.c_char_p,
             "k3_expert_ffn_workspace_size": ctypes.c_int64,
             "k3_moe_layer_workspace_size": ctypes.c_int64,
-            "k3_mla_workspace_size": ctypes.c_int64}
+            "k3_mla_workspace_size": ctypes.c_int64,
+            "k3_moe_grouped_workspace_size": ctypes.c_int64}
 
 
 class K3LibraryError(ImportError):

@@ -234,6 +234,22 @@ class RoutedMoE:
         u = xf @ self.sh_up.float().T
         return _act_torch(g, u, act, beta, lb) @ self.sh_down.float().T
 
+    def grouped_forward(self, x: torch.Tensor, router: RouterResult | None = None,
+                        out_dtype=torch.float32) -> torch.Tensor:
+        """Prefill form of __call__ for x [..., H] bf16: route every token (or take the given
+        RouterResult), then run the routed experts grouped by expert (moe_grouped_ffn); the
+        shared expert, if any, is a dense bf16 FFN through the BLAS library in fp32."""
+        orig = x.shape
+        flat = x.reshape(-1, orig[-1]).to(torch.bfloat16)
+        if router is None:
+            router = self.route(flat)
+        act, beta, lb = self._act()
+        y = moe_grouped_ffn(flat, router.expert_indices, router.expert_weights, self.expert_table(), self._I,
+                            act, beta, lb, out_dtype=torch.float32)
+        if self.sh_gate is not None:
+            y = y + self.shared_forward(flat)
+        return y.to(out_dtype).reshape(*orig[:-1], self._H)
+
     def __call__(self, x: torch.Tensor, return_router: bool = False, out_dtype=torch.float32):
         orig = x.shape
         flat = x.reshape(-1, orig[-1])
@@ -259,6 +275,43 @@ class RoutedMoE:
         r = RouterResult(*(torch.cat([getattr(rr, f) for rr in recs]) for f in
                            ("expert_indices", "expert_weights", "raw_scores", "corrected_scores")))
         return y, r
+
+
+def moe_grouped_ffn(x: torch.Tensor, expert_indices: torch.Tensor, expert_weights: torch.Tensor,
+                    table: torch.Tensor, intermediate: int, act: str = "silu", beta: float = 1.0,
+                    linear_beta: float | None = None, out_dtype: torch.dtype = torch.float32,
+                    validate: bool = True) -> torch.Tensor:
+    """Routed experts for many tokens at once (prefill): x [T, H] bf16, expert_indices
+    [T, k] (ids into the [E, 6] device pointer table), expert_weights [T, k] -> [T, H].
+
+    The per-expert loop of LatentMoE.__call__ (moe.py:120-127) becomes a device grouping
+    pass plus two grouped MFMA GEMMs and a fixed-order combine (k3_moe_grouped_ffn).
+    ``validate`` checks the ids on the device first (one small device->host copy)."""
+    if x.dim() != 2 or expert_indices.shape != expert_weights.shape or expert_indices.shape[0] != x.shape[0]:
+        raise ValueError(f"x [T, H] with expert_indices/expert_weights [T, k] expected; got {tuple(x.shape)}, "
+                         f"{tuple(expert_indices.shape)}, {tuple(expert_weights.shape)}")
+    if x.dtype != torch.bfloat16:
+        raise TypeError("the grouped path takes bf16 hidden states")
+    T.require_device(x, expert_indices, expert_weights, table)
+    n_tok, H = x.shape
+    k = expert_indices.shape[1]
+    E = table.shape[0]
+    idx = expert_indices.to(torch.int32).contiguous()
+    if validate and idx.numel():
+        lo, hi = (int(v) for v in torch.stack([idx.min(), idx.max()]).tolist())
+        if lo < 0 or hi >= E:
+            raise ValueError(f"expert ids {lo}..{hi} outside 0..{E - 1}")
+    w = expert_weights.to(torch.float32).contiguous()
+    x = T.contiguous_aligned(x)
+    out = torch.empty((n_tok, H), dtype=out_dtype, device=x.device)
+    if n_tok == 0:
+        return out
+    nbytes = int(_lib.lib().k3_moe_grouped_workspace_size(n_tok, k, E, H, intermediate))
+    ws = _workspace.get(x.device, nbytes, "moe_grouped")
+    _lib.call("k3_moe_grouped_ffn", T.ptr(x), T.dtype_code(x.dtype), T.ptr(idx), T.ptr(w), T.ptr(table),
+              T.ptr(out), T.dtype_code(out_dtype), n_tok, H, intermediate, E, k, _act_code(act), float(beta),
+              float(linear_beta or 0.0), T.ptr(ws), ws.numel(), T.stream(x))
+    return out
 
 
 def _act_torch(g, u, act, beta, lb):
