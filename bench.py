@@ -54,13 +54,31 @@ def rand_mxfp4(torch, gen, n, k, device):
     return p, s
 
 
+EAGER = False                   # --eager: launch every step directly (profiler counter runs)
+
+
 def graph_time(torch, fn, steps, warmup):
     """Capture `steps` calls of fn(i) into one graph and replay it; also replay a graph of
-    `warmup` calls first.  Returns seconds for the timed replay (synchronised both sides)."""
+    `warmup` calls first.  Returns seconds for the timed replay (synchronised both sides).
+    With --eager the steps are launched one by one instead (for per-dispatch profiler
+    counters); the timing then includes the host launch path."""
     stream = torch.cuda.current_stream()
     for i in range(3):
         fn(i)
     torch.cuda.synchronize()
+    if EAGER:
+        for i in range(warmup):
+            fn(i)
+        torch.cuda.synchronize()
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        t0 = time.perf_counter()
+        e0.record(stream)
+        for i in range(steps):
+            fn(i)
+        e1.record(stream)
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / 1e3, time.perf_counter() - t0
     if warmup:
         gw = torch.cuda.CUDAGraph()
         with torch.cuda.graph(gw):
@@ -258,6 +276,24 @@ def bench_read_ceiling(torch, nbytes, steps, dev):
     return sec / steps
 
 
+def bench_copy_ceiling(torch, nbytes, steps, dev):
+    """One streaming-copy launch of nbytes (k3_stream_copy) rotating over 16 source /
+    destination pairs: the known-size kernel the profiler's WRITE_SIZE counter is scaled by."""
+    import ctypes
+    from k3hip import _lib
+    src = [torch.empty(nbytes, dtype=torch.uint8, device=dev) for _ in range(16)]
+    dst = [torch.empty(nbytes, dtype=torch.uint8, device=dev) for _ in range(16)]
+
+    def step(i):
+        st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+        _lib.call("k3_stream_copy", ctypes.c_void_p(dst[i % 16].data_ptr()),
+                  ctypes.c_void_p(src[i % 16].data_ptr()), nbytes, st)
+
+    sec, _ = graph_time(torch, step, steps, 8)
+    del src, dst
+    return sec / steps
+
+
 def bench_cpu(sample_s=12.0):
     """torch-CPU restatement of the k3ref expert path (k3ref/layers.py:226-234 with the
     decode of k3ref/weights.py:29-37 on every access), timed on this host."""
@@ -289,7 +325,11 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--workloads", default="expert,layer,prefill,gemv,mla,ceiling")
+    ap.add_argument("--eager", action="store_true",
+                    help="launch steps one by one instead of replaying a HIP graph (profiler counter runs)")
     args = ap.parse_args()
+    global EAGER
+    EAGER = args.eager
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build runs on one GPU only (no multi-GPU path); use --gpus 1",
               file=sys.stderr)
@@ -361,10 +401,13 @@ def main():
     if "ceiling" in work:
         ce = bench_read_ceiling(torch, EXPERT_BYTES, 256, dev)
         cl = bench_read_ceiling(torch, LAYER_BYTES, 64, dev)
+        cc = bench_copy_ceiling(torch, EXPERT_BYTES, 64, dev)
         line["read_ceiling"] = {
             "what": "single streaming-read launch of the same byte count (k3_stream_read)",
             "expert_bytes_us": round(ce * 1e6, 3), "expert_bytes_GB/s": round(EXPERT_BYTES / ce / 1e9, 1),
-            "layer_bytes_us": round(cl * 1e6, 2), "layer_bytes_GB/s": round(LAYER_BYTES / cl / 1e9, 1)}
+            "layer_bytes_us": round(cl * 1e6, 2), "layer_bytes_GB/s": round(LAYER_BYTES / cl / 1e9, 1),
+            "copy_expert_bytes_us": round(cc * 1e6, 3),
+            "copy_expert_bytes_GB/s": round(2 * EXPERT_BYTES / cc / 1e9, 1)}
         line["pct_of_measured_read"] = round(100 * gbs / (EXPERT_BYTES / ce / 1e9), 1)
         if "moe_layer" in line:
             line["moe_layer"]["pct_of_measured_read"] = round(
