@@ -74,15 +74,16 @@ int k3_mxfp4_matvec_cfg(const void *x, int x_dtype, const void *packed, const vo
 
 /* ---- MoE expert FFN ---------------------------------------------------------------- */
 
-/* Workspace bytes k3_expert_ffn needs for intermediate size I.  The workspace must be
- * zero-filled once before its first use; the kernel leaves it ready for the next call.
- * One workspace per stream: calls that share a workspace must not overlap. */
+/* Workspace bytes k3_expert_ffn needs for intermediate size I (the fp32 act vector passed
+ * between its two launches).  Needs no initialisation.  Calls that share a workspace must
+ * not overlap (calls on one stream never do). */
 int64_t k3_expert_ffn_workspace_size(int64_t I);
 
-/* One routed expert at batch 1 in a single launch: out[H] = act(x Wg^T, x Wu^T) Wd^T with
- * gate/up packed [I, H/2] / scales [I, H/32] and down packed [H, I/2] / scales [H, I/32].
+/* One routed expert at batch 1, two stream-ordered launches (gate/up + act, then the down
+ * GEMV): out[H] = act(x Wg^T, x Wu^T) Wd^T with gate/up packed [I, H/2] / scales [I, H/32]
+ * and down packed [H, I/2] / scales [H, I/32].
  * act_kind K3_ACT_SILU (beta ignored) or K3_ACT_SITU (linear_beta <= 0 means None).
- * H and I must be multiples of 128.
+ * H and I must be multiples of 128, H <= 8192.
  * Replaces LatentMoE.expert_forward (air_llm/models/kimi_k3/moe.py:90-103) with the
  * k3ref semantics (k3ref/layers.py:226-234). */
 int k3_expert_ffn(const void *x, int x_dtype, const void *gate_packed, const void *gate_scales,

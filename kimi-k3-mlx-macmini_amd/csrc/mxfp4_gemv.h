@@ -17,12 +17,12 @@ struct GemvArgs {
     int64_t K;
     int x_bf16;
     int out_bf16;
-    int scales_vec;      // scales rows can be staged with 128-bit loads
 };
 
 constexpr size_t kGemvMaxLds = 160 * 1024;
 
 void gemv_default_cfg(int64_t N, int64_t K, int *rpw, int *gpl);
+int gemv_token_tile(int64_t K, int x_bf16);  // tokens per launch (0: K too long)
 int gemv_launch(const GemvArgs &a, int rpw, int gpl, hipStream_t st);
 int gemv_validate(const void *x, int x_dtype, const void *packed, const void *scales,
                   const void *out, int out_dtype, int64_t M, int64_t N, int64_t K);

@@ -1,9 +1,9 @@
-"""Caller-side workspaces for the persistent kernels.
+"""Caller-side workspaces for the multi-launch kernels.
 
-The C-ABI allocates nothing.  Kernels that synchronise across the grid keep a few
-counters at the head of their workspace; those must be zero before the first launch and
-the kernels leave them zero afterwards.  Concurrent launches must not share a workspace,
-so workspaces are kept per (device, stream).
+The C-ABI allocates nothing.  Intermediate records (the expert's act vector, router
+records, split-T partials, grouping lists) live in a workspace the caller passes in.
+Concurrent launches must not share a workspace, so workspaces are kept per (device,
+stream, user).
 """
 from __future__ import annotations
 
@@ -25,11 +25,6 @@ def get(device: torch.device, nbytes: int, tag: str = "") -> torch.Tensor:
             buf = torch.zeros(max(nbytes, 4096), dtype=torch.uint8, device=device)
             _cache[key] = buf
     return buf
-
-
-def error_flag(buf: torch.Tensor) -> int:
-    """The kernel-side error word (word 2 of the header); nonzero after a barrier timeout."""
-    return int(buf[8:12].view(torch.int32).item())
 
 
 def clear() -> None:

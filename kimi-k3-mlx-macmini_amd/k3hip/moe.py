@@ -2,9 +2,9 @@
 (air_llm/models/kimi_k3/moe.py:90-103, k3ref/layers.py:226-234).
 
 ``expert_ffn_fused(x, gate, up, down)`` runs one expert (``gate``/``up``/``down`` are the
-``(packed, scales)`` pairs an ``expert_source`` returns) in a single persistent HIP launch
-at batch 1: gate and up rows are reduced by the same wave so ``act = f(gate, up)`` never
-round-trips, and the down projection's weights stream while the grid waits for ``act``.
+``(packed, scales)`` pairs an ``expert_source`` returns) at batch 1 in two stream-ordered HIP
+launches: gate and up rows are reduced by the same wave, which applies the activation and
+writes ``act`` (fp32) to a workspace; the down projection is the batch-1 MXFP4 GEMV on it.
 """
 from __future__ import annotations
 

@@ -50,9 +50,8 @@ def test_expert_ffn_situ(beta, lbeta):
 
 
 def test_expert_ffn_repeated_calls_and_bf16_out():
-    """The workspace counters reset themselves: many back-to-back launches (and a graph
-    replay of them) give identical results, and no barrier timed out."""
-    from k3hip import _workspace
+    """Back-to-back launches sharing one workspace (and graph replays of them, with eager
+    work between the replays) give bit-identical results."""
     from k3hip.moe import expert_ffn_fused
     rng = np.random.default_rng(9)
     H, I = 7168, 2048
@@ -74,6 +73,4 @@ def test_expert_ffn_repeated_calls_and_bf16_out():
         torch.cuda.synchronize()
         for e in range(3):
             assert torch.equal(outs[e], ref[e])
-    for key, buf in _workspace._cache.items():
-        if key[2] == "expert_ffn":     # only the persistent kernel's workspaces carry the flag
-            assert _workspace.error_flag(buf) == 0
+        assert torch.equal(expert_ffn_fused(x, *experts[1]), ref[1])   # eager call between replays
