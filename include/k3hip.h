@@ -95,7 +95,10 @@ int k3_expert_ffn(const void *x, int x_dtype, const void *gate_packed, const voi
 /* ---- routed MoE layer at batch 1 ------------------------------------------------------ */
 
 /* Workspace bytes for k3_moe_layer_decode / k3_moe_route (pass shared_I = 0 without a
- * shared expert).  Needs no initialisation. */
+ * shared expert).  Its first 256 bytes hold a counter of finished router blocks (at that
+ * place for every shape): zero-fill them before the first call; every call returns them to
+ * zero.  The rest is rewritten by every call.  Calls that share a workspace must not
+ * overlap (calls on one stream never do). */
 int64_t k3_moe_layer_workspace_size(int64_t H, int64_t I, int64_t shared_I, int64_t n_experts,
                                     int64_t top_k);
 

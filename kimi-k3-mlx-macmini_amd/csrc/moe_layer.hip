@@ -1,21 +1,27 @@
 // Routed MoE layer decode at batch 1 (router + top-k + routed experts + shared expert +
-// weighted combine), four stream-ordered launches with no host synchronisation.
+// weighted combine), three stream-ordered launches with no host synchronisation.
 //
 // Reference: LatentMoE.route / __call__ / shared_forward (air_llm/models/kimi_k3/moe.py:65-132,
 // k3ref/layers.py:214-261).  The reference materialises the routing on the host
 // (np_indices, moe.py:135-138) and loops over experts serially with an mx.eval per expert.
 // Here the routing never leaves the GPU:
 //
-//   K1  router logits (bf16 [E, H] x bf16/fp32 x)          -> ws.logits[E]
-//       shared expert gate/up rows (bf16) + activation       -> ws.shared_act[Is]
-//   R   one block: softmax/sigmoid + rank-based top-k of the E logits, the router
-//       records for the caller, and the k selected experts' weight pointers
-//   K2  routed gate/up rows of the k selected experts       -> ws.act[k][I]
-//       (expert weights through a device table of pointers, so all E experts stay
-//       resident and each selected expert's bytes are read exactly once)
-//       shared down rows (bf16 [H, Is] x shared_act)        -> ws.yshared[H]
-//   K3  per output row: the k routed down rows (MXFP4) against ws.act[j], combined in a
-//       fixed order y = yshared + sum_j w_j * down_j      -> out[H]
+//   L1  router logits (bf16 [E, H] . x) and the shared expert's gate/up rows (bf16) with
+//       its activation.  The router rows run in the first blocks; each router block counts
+//       itself done on a workspace counter, and the last one computes softmax / sigmoid,
+//       the exact top-k (ties to the lower expert index), the router records and the
+//       selected experts' weight pointers -- while the shared stream is still running.
+//   L2  the shared expert's down rows (bf16 [H, Is] . shared act) in the first blocks, which
+//       need no routing, then the routed gate/up row pairs of the k selected experts (MXFP4,
+//       through the device pointer table, so every expert stays resident and each selected
+//       expert's bytes are read once) with their activation.
+//   L3  per block, RPW output rows and one wave per selected expert: the wave holds its
+//       expert's act in registers and reduces its down rows; the block combines
+//       y = shared + sum_j w_j * down_j in a fixed order.
+//
+// Every kernel issues its activation loads, then its whole weight stream, before it stages
+// anything into LDS or registers it consumes, and stages with unconditional stores, so the
+// in-order vmcnt waits never hold the staging behind the weight stream.
 #include <algorithm>
 
 #include "moe_common.h"
@@ -34,6 +40,7 @@ struct LayerWs {
     float *act;          // [k][I]
     float *yshared;      // [H]
     uint64_t *sel_ptrs;  // [k][6] weight pointers of the selected experts
+    uint32_t *counter;   // router blocks done in this launch (returns to 0 after each)
 };
 
 struct LayerArgs {
@@ -50,12 +57,14 @@ struct LayerArgs {
     int act_kind;
     float beta, lbeta;
     int out_bf16;
-    int k1_router_blocks;          // K1: blocks [0, k1_router_blocks) do router rows
-    int k2_routed_blocks;          // K2: blocks [0, k2_routed_blocks) do routed gate/up
+    int l1_router_blocks;          // L1: blocks [0, l1_router_blocks) do router rows
+    int l2_shared_blocks;          // L2: blocks [0, l2_shared_blocks) do shared down rows
 };
 
 constexpr int kMaxTopK = 16;
 constexpr int kMaxExperts = 1024;
+constexpr int kSharedDownRows = 2;  // shared down rows per wave (L2)
+constexpr int kRoutedPairs = 2;     // routed (gate, up) row pairs per wave (L2)
 
 // ------------------------------------------------------------------ bf16 row dots
 // 8 bf16 weights . 8 bf16 activations
@@ -91,67 +100,61 @@ __device__ __forceinline__ float dot_chunk(uint4 w, const uint4 *xl, int c, floa
     }
 }
 
-template <typename XT>
-__device__ __forceinline__ void stage_plain(uint4 *dst, const void *src, int n_elems) {
-    const int chunks = n_elems * static_cast<int>(sizeof(XT)) / 16;
-    const uint4 *s = static_cast<const uint4 *>(src);
-    for (int c = threadIdx.x; c < chunks; c += blockDim.x) dst[c] = s[c];
-}
-
-// NR bf16 weight rows (K elements each, K % 8 == 0) against an LDS activation row, in two
-// halves so callers can issue the weight stream before staging the activations:
-// bf16_rows_load issues every row's loads, bf16_rows_dot consumes them (wave totals land
-// in lane 63).  CH = chunks of 8 per lane (compile-time upper bound).
-template <int CH, int NR>
-__device__ __forceinline__ void bf16_rows_load(const __amdgpu_buffer_rsrc_t (&r)[NR], const uint32_t (&row_off)[NR],
-                                               int K, const bool (&valid)[NR], uint4 (&w)[NR][CH]) {
-    const int lane = threadIdx.x & 63;
-    const int nch = K >> 3;
+// Activation row staging in two halves: x_load issues XREG 16-byte loads per thread
+// (out-of-range chunks read zeros), x_store writes them all; callers issue their weight
+// stream between the two.  `swz` picks the swizzled MXFP4 group order (XTile) or the plain
+// chunk order of the bf16 rows.
+template <int XREG>
+__device__ __forceinline__ void x_load(uint4 (&xr)[XREG], const void *x, int nchunks) {
+    const auto rx = make_rsrc(x, static_cast<uint32_t>(nchunks * 16));
 #pragma unroll
-    for (int q = 0; q < NR; ++q)
-#pragma unroll
-        for (int u = 0; u < CH; ++u) {
-            const int c = u * 64 + lane;
-            w[q][u] = buf_load16(r[q], (valid[q] && c < nch) ? row_off[q] + c * 16u : kOobOffset);
-        }
-}
-
-template <typename XT, int CH, int NR>
-__device__ __forceinline__ void bf16_rows_dot(const uint4 (&w)[NR][CH], int K, const uint4 *xl, float (&out)[NR]) {
-    const int lane = threadIdx.x & 63;
-    const int nch = K >> 3;
-    float acc[NR][2];
-#pragma unroll
-    for (int q = 0; q < NR; ++q) acc[q][0] = acc[q][1] = 0.f;
-#pragma unroll
-    for (int u = 0; u < CH; ++u) {
-        const int c = u * 64 + lane;
-        if (c < nch) {
-#pragma unroll
-            for (int q = 0; q < NR; ++q) acc[q][u & 1] = dot_chunk<XT>(w[q][u], xl, c, acc[q][u & 1]);
-        }
+    for (int k = 0; k < XREG; ++k) {
+        const int c = threadIdx.x + 256 * k;
+        xr[k] = buf_load16(rx, c < nchunks ? static_cast<uint32_t>(c) * 16u : kOobOffset);
     }
-#pragma unroll
-    for (int q = 0; q < NR; ++q) out[q] = wave_sum_to_lane63(acc[q][0] + acc[q][1]);
 }
+template <typename XT, int XREG, bool SWZ>
+__device__ __forceinline__ void x_store(uint4 *xl, const uint4 (&xr)[XREG]) {
+    constexpr int CPG = XTile<XT>::kChunks;
+#pragma unroll
+    for (int k = 0; k < XREG; ++k) {
+        const int c = threadIdx.x + 256 * k;
+        xl[SWZ ? XTile<XT>::slot(c / CPG, c % CPG) : c] = xr[k];
+    }
+}
+template <typename XT>
+constexpr int x_regs() { return sizeof(XT) == 2 ? 4 : 8; }  // H <= 8192
 
-// A 64-bit pointer held in LDS or loaded per lane, made wave-uniform (SGPRs) so buffer
-// resources built from it need no waterfall loop.
+// A 64-bit pointer held in memory, made wave-uniform (SGPRs) so buffer resources built
+// from it need no waterfall loop.
 __device__ __forceinline__ const void *uniform_ptr(uint64_t p) {
     const uint32_t lo = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(p));
     const uint32_t hi = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(p >> 32));
     return reinterpret_cast<const void *>((static_cast<uint64_t>(hi) << 32) | lo);
 }
 
-// ------------------------------------------------------------------ routing
-// One block of E threads rounded up to a multiple of 64 (E <= 1024).
+// ------------------------------------------------------------------ routing (one block)
 // softmax:       scores = softmax(logits), selection on scores
 // sigmoid_bias:  scores = sigmoid(logits), selection on scores + bias, weights from scores
 // weights: optional renormalisation by (sum + 1e-20), then * scaling   (moe.py:65-76)
-// Top-k is exact and deterministic with ties to the lower expert index, in two levels:
+// Top-k is exact and deterministic with ties to the lower expert index: the order is the
+// strict total order on (selection score, -index), with NaN scores ranked as -inf, as one
+// 64-bit key per expert.  Two levels of parallel ranking (no sequential selection rounds):
 // every expert ranks itself inside its 64-expert group (64 broadcast LDS compares), the
-// group's best k become candidates, and each candidate ranks itself among all candidates.
-// The global top-k is always inside the union of the per-group top-k.
+// group's best k become candidates, and every candidate ranks itself among all candidates.
+// The global top-k is inside the union of the per-group top-k.
+// 64-bit order key of (selection score, expert): larger key = ranks first.  High word: the
+// float's bits mapped monotonically to unsigned (NaN mapped as -inf); low word: the
+// complement of the expert index, so ties go to the lower index.  Every live expert's key
+// is nonzero; 0 marks an empty slot.
+__device__ __forceinline__ uint64_t order_key(float v, int e) {
+    if (v != v) v = -INFINITY;
+    const uint32_t b = __float_as_uint(v);
+    const uint32_t mono = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+    return (static_cast<uint64_t>(mono) << 32) | (0xffffffffu - static_cast<uint32_t>(e));
+}
+__device__ __forceinline__ int key_expert(uint64_t k) { return static_cast<int>(0xffffffffu - static_cast<uint32_t>(k)); }
+
 __device__ __forceinline__ float block_reduce(float v, float *red, bool is_max) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
     v = is_max ? wave_max_all(v) : wave_sum_all(v);
@@ -163,76 +166,114 @@ __device__ __forceinline__ float block_reduce(float v, float *red, bool is_max) 
     return r;
 }
 
-// (value, index) order: larger value first, then lower index
-__device__ __forceinline__ bool outranks(float v, int j, float sel, int e) {
-    return v > sel || (v == sel && j < e);
-}
+constexpr int kMaxCand = kMaxExperts / 64 * kMaxTopK;
 
-__global__ __launch_bounds__(1024) void layer_route(LayerArgs a) {
-    __shared__ __align__(16) float sel_s[kMaxExperts];
-    __shared__ float cand_v[kMaxExperts / 64 * kMaxTopK];
-    __shared__ int cand_e[kMaxExperts / 64 * kMaxTopK];
-    __shared__ float cand_s[kMaxExperts / 64 * kMaxTopK];
-    __shared__ float red[16];
+// Called by all 256 threads of the last router block; logits are read with agent-coherent
+// loads (written by other blocks, possibly on other XCDs, in this launch).
+__device__ void route_block(const LayerArgs &a) {
+    constexpr int kPer = kMaxExperts / 256;  // experts per thread: e = t + 256 * m
+    __shared__ uint64_t key_s[kMaxExperts];
+    __shared__ uint64_t cand_k[kMaxCand];
+    __shared__ float cand_s[kMaxCand];
+    __shared__ float red[8];
     __shared__ int32_t idx_s[kMaxTopK];
     __shared__ float w_s[kMaxTopK];
-    const int e = threadIdx.x;
-    const int groups = blockDim.x >> 6;
-    const bool live = e < a.E;
-    const float l = live ? a.ws.logits[e] : -INFINITY;
-    float s;
-    if (a.route_kind == K3_ROUTE_SOFTMAX) {
-        const float mx = block_reduce(l, red, true);
-        const float ex = live ? expf(l - mx) : 0.f;
-        const float sum = block_reduce(ex, red, false);
-        s = ex / sum;
-    } else {
-        s = 1.0f / (1.0f + expf(-l));
+    const int t = threadIdx.x, lane = t & 63;
+    float l[kPer], s[kPer], sel[kPer];
+    uint64_t key[kPer];
+#pragma unroll
+    for (int m = 0; m < kPer; ++m) {
+        const int e = t + 256 * m;
+        l[m] = e < a.E ? __hip_atomic_load(a.ws.logits + e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : -INFINITY;
     }
-    const float sel = (a.route_kind == K3_ROUTE_SIGMOID_BIAS && a.router_bias && live) ? s + a.router_bias[e] : s;
-    sel_s[e] = live ? sel : -INFINITY;
-    for (int c = threadIdx.x; c < groups * a.k; c += blockDim.x) {
-        cand_v[c] = -INFINITY;
-        cand_e[c] = 0x7fffffff;
+    // every thread also loads the 6 table pointers of its experts now, alongside the logits,
+    // so that writing the selected experts' pointers needs no dependent load at the end
+    uint4 tab[kPer][3];
+    {
+        const auto rt = make_rsrc(a.table, a.table ? static_cast<uint32_t>(a.E) * 48u : 0u);
+#pragma unroll
+        for (int m = 0; m < kPer; ++m) {
+            const int e = t + 256 * m;
+#pragma unroll
+            for (int q = 0; q < 3; ++q) tab[m][q] = buf_load16(rt, e < a.E ? static_cast<uint32_t>(e) * 48u + q * 16u : kOobOffset);
+        }
+    }
+    if (a.route_kind == K3_ROUTE_SOFTMAX) {
+        float mx = -INFINITY;
+#pragma unroll
+        for (int m = 0; m < kPer; ++m) mx = fmaxf(mx, l[m]);
+        mx = block_reduce(mx, red, true);
+        float sum = 0.f;
+#pragma unroll
+        for (int m = 0; m < kPer; ++m) {
+            s[m] = t + 256 * m < a.E ? expf(l[m] - mx) : 0.f;
+            sum += s[m];
+        }
+        sum = block_reduce(sum, red, false);
+#pragma unroll
+        for (int m = 0; m < kPer; ++m) s[m] /= sum;
+    } else {
+#pragma unroll
+        for (int m = 0; m < kPer; ++m) s[m] = 1.0f / (1.0f + expf(-l[m]));
+    }
+    for (int c = t; c < kMaxCand; c += 256) cand_k[c] = 0;  // ranks below every expert
+#pragma unroll
+    for (int m = 0; m < kPer; ++m) {
+        const int e = t + 256 * m;
+        const bool live = e < a.E;
+        sel[m] = (a.route_kind == K3_ROUTE_SIGMOID_BIAS && a.router_bias && live) ? s[m] + a.router_bias[e] : s[m];
+        if (live) {
+            a.ws.scores[e] = s[m];
+            a.ws.corrected[e] = sel[m];
+        }
+        key[m] = live ? order_key(sel[m], e) : 0;
+        key_s[e] = key[m];
     }
     __syncthreads();
-    if (live) {
-        a.ws.scores[e] = s;
-        a.ws.corrected[e] = sel;
-        // rank inside the 64-expert group
-        const int g0 = e & ~63;
-        const float4 *s4 = reinterpret_cast<const float4 *>(sel_s + g0);
+    // level 1: rank inside the 64-expert group (all lanes of a wave share the group, so
+    // every LDS read is a broadcast); one 64-bit compare per pair
+#pragma unroll
+    for (int m = 0; m < kPer; ++m) {
+        const int e = t + 256 * m;
+        if (256 * m >= a.E) break;  // uniform: no expert of this or later rounds is live
+        const uint64_t *g = key_s + (e & ~63);
         int rank = 0;
 #pragma unroll
-        for (int j4 = 0; j4 < 16; ++j4) {
-            const float4 v = s4[j4];
-            const int j = g0 + j4 * 4;
-            rank += outranks(v.x, j, sel, e) + outranks(v.y, j + 1, sel, e) + outranks(v.z, j + 2, sel, e) +
-                    outranks(v.w, j + 3, sel, e);
-        }
-        if (rank < a.k) {
+        for (int j = 0; j < 64; ++j) rank += g[j] > key[m];
+        if (e < a.E && rank < a.k) {
             const int c = (e >> 6) * a.k + rank;
-            cand_v[c] = sel;
-            cand_e[c] = e;
-            cand_s[c] = s;
+            cand_k[c] = key[m];
+            cand_s[c] = s[m];
         }
     }
     __syncthreads();
-    const int nc = groups * a.k;
-    for (int c = threadIdx.x; c < nc; c += blockDim.x) {
-        const float v = cand_v[c];
-        const int ce = cand_e[c];
-        if (ce == 0x7fffffff) continue;
-        int rank = 0;
-        for (int d = 0; d < nc; ++d) rank += outranks(cand_v[d], cand_e[d], v, ce);
-        if (rank < a.k) {
-            idx_s[rank] = ce;
-            w_s[rank] = cand_s[c];
+    // level 2: every candidate ranks itself among all candidates
+    const int nc = (a.E + 63) / 64 * a.k;
+    if (nc <= 64) {
+        if (t < 64) {  // one candidate per lane of wave 0, 64 broadcast compares
+            const uint64_t kc = cand_k[lane];
+            int rank = 0;
+#pragma unroll
+            for (int d = 0; d < 64; ++d) rank += cand_k[d] > kc;
+            if (kc != 0 && rank < a.k) {
+                idx_s[rank] = key_expert(kc);
+                w_s[rank] = cand_s[lane];
+            }
+        }
+    } else {
+        for (int c = t; c < nc; c += 256) {
+            const uint64_t kc = cand_k[c];
+            if (kc == 0) continue;
+            int rank = 0;
+            for (int d = 0; d < nc; ++d) rank += cand_k[d] > kc;
+            if (rank < a.k) {
+                idx_s[rank] = key_expert(kc);
+                w_s[rank] = cand_s[c];
+            }
         }
     }
     __syncthreads();
-    if (threadIdx.x < 64) {
-        const int lane = threadIdx.x;
+    if (t < 64) {
         float wsum = lane < a.k ? w_s[lane] : 0.f;
         wsum = wave_sum_all(wsum);
         const float norm = (a.renorm && a.k > 1) ? 1.0f / (wsum + 1e-20f) : 1.0f;
@@ -241,92 +282,187 @@ __global__ __launch_bounds__(1024) void layer_route(LayerArgs a) {
             a.ws.topk_w[lane] = w_s[lane] * norm * a.scaling;
         }
     }
-    if (a.table && static_cast<int>(threadIdx.x) < a.k * 6) {
-        const int j = threadIdx.x / 6, q = threadIdx.x % 6;
-        a.ws.sel_ptrs[threadIdx.x] = a.table[static_cast<int64_t>(idx_s[j]) * 6 + q];
-    }
-}
-
-// ------------------------------------------------------------------ K1
-template <typename XT, int CHH>
-__global__ __launch_bounds__(256) void layer_k1(LayerArgs a) {
-    extern __shared__ uint4 smem[];
-    uint4 *xl = smem;
-    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
-    const uint32_t row_bytes = static_cast<uint32_t>(a.H) * 2u;
-    if (static_cast<int>(blockIdx.x) < a.k1_router_blocks) {
-        const int e = blockIdx.x * 4 + wave;
-        const __amdgpu_buffer_rsrc_t r[1] = {make_rsrc(a.router_w, static_cast<uint32_t>(a.E) * row_bytes)};
-        const uint32_t off[1] = {static_cast<uint32_t>(e) * row_bytes};
-        const bool v[1] = {e < a.E};
-        uint4 w[1][CHH];
-        bf16_rows_load<CHH, 1>(r, off, a.H, v, w);
-        stage_plain<XT>(xl, a.x, a.H);
-        __syncthreads();
-        float t[1];
-        bf16_rows_dot<XT, CHH, 1>(w, a.H, xl, t);
-        if (lane == 63 && e < a.E) a.ws.logits[e] = t[0];
-    } else {
-        const int i = (blockIdx.x - a.k1_router_blocks) * 4 + wave;
-        const __amdgpu_buffer_rsrc_t r[2] = {make_rsrc(a.sh_gate, static_cast<uint32_t>(a.Is) * row_bytes),
-                                             make_rsrc(a.sh_up, static_cast<uint32_t>(a.Is) * row_bytes)};
-        const uint32_t off[2] = {static_cast<uint32_t>(i) * row_bytes, static_cast<uint32_t>(i) * row_bytes};
-        const bool v[2] = {i < a.Is, i < a.Is};
-        uint4 w[2][CHH];
-        bf16_rows_load<CHH, 2>(r, off, a.H, v, w);
-        stage_plain<XT>(xl, a.x, a.H);
-        __syncthreads();
-        float gu[2];
-        bf16_rows_dot<XT, CHH, 2>(w, a.H, xl, gu);
-        if (lane == 63 && i < a.Is) a.ws.shared_act[i] = act_fn(gu[0], gu[1], a.act_kind, a.beta, a.lbeta);
-    }
-}
-
-// ------------------------------------------------------------------ K2
-constexpr int kK2Pairs = 2;  // routed (gate, up) row pairs per wave
-
-template <typename XT, int GA, int CHI>
-__global__ __launch_bounds__(256) void layer_k2(LayerArgs a) {
-    extern __shared__ uint4 smem[];
-    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
-    if (static_cast<int>(blockIdx.x) < a.k2_routed_blocks) {
-        // routed gate/up: kK2Pairs row pairs (slot j, row i) per wave
-        constexpr int CPGX = XTile<XT>::kChunks;
-        const int GH = a.H >> 5;
-        const uint32_t rowA = static_cast<uint32_t>(a.H >> 1);
-        uint4 wg_[kK2Pairs][GA], wu_[kK2Pairs][GA];
-        uint32_t sg_[kK2Pairs][GA], su_[kK2Pairs][GA];
-        int jj[kK2Pairs], ii[kK2Pairs];
-        bool vv[kK2Pairs];
+    if (a.table) {  // the owner of each selected expert writes its pointers
 #pragma unroll
-        for (int p = 0; p < kK2Pairs; ++p) {
-            const int pair = (blockIdx.x * 4 + wave) * kK2Pairs + p;
-            const int j = pair / a.I, i = pair % a.I;
-            const bool v = j < a.k;
-            jj[p] = j, ii[p] = i, vv[p] = v;
-            const uint64_t *t = a.ws.sel_ptrs + (v ? j : 0) * 6;
-            const auto rg = make_rsrc(uniform_ptr(t[0]), static_cast<uint32_t>(a.I) * rowA);
-            const auto rgs = make_rsrc(uniform_ptr(t[1]), static_cast<uint32_t>(a.I * GH));
-            const auto ru = make_rsrc(uniform_ptr(t[2]), static_cast<uint32_t>(a.I) * rowA);
-            const auto rus = make_rsrc(uniform_ptr(t[3]), static_cast<uint32_t>(a.I * GH));
-            const uint32_t so = static_cast<uint32_t>(i * GH);
-#pragma unroll
-            for (int u = 0; u < GA; ++u) {
-                const int g = u * 64 + lane;
-                const bool ok = v && g < GH;
-                const uint32_t off = ok ? static_cast<uint32_t>(i) * rowA + g * 16u : kOobOffset;
-                const uint32_t soff = ok ? scale_dword_off(so, g) : kOobOffset;
-                wg_[p][u] = buf_load16(rg, off);
-                wu_[p][u] = buf_load16(ru, off);
-                sg_[p][u] = buf_load4(rgs, soff);
-                su_[p][u] = buf_load4(rus, soff);
+        for (int m = 0; m < kPer; ++m) {
+            const int e = t + 256 * m;
+            for (int r = 0; r < a.k; ++r) {
+                if (idx_s[r] == e) {
+                    uint4 *dst = reinterpret_cast<uint4 *>(a.ws.sel_ptrs + r * 6);
+                    dst[0] = tab[m][0];
+                    dst[1] = tab[m][1];
+                    dst[2] = tab[m][2];
+                }
             }
         }
-        stage_x_tile<XT>(smem, a.x, GH * CPGX);  // after the weight stream is issued
-        __syncthreads();
-        float accg[kK2Pairs], accu[kK2Pairs];
+    }
+}
+
+// ------------------------------------------------------------------ L1
+// CHH: bf16 chunks (8 elements) per lane over H.
+template <typename XT, int CHH>
+__global__ __launch_bounds__(256) void layer_l1(LayerArgs a) {
+    extern __shared__ uint4 smem[];
+    __shared__ uint32_t last_s;
+    constexpr int XREG = x_regs<XT>();
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+    const uint32_t row_bytes = static_cast<uint32_t>(a.H) * 2u;
+    const int nch = a.H >> 3;
+    const int xchunks = a.H * static_cast<int>(sizeof(XT)) / 16;
+    uint4 xr[XREG];
+    x_load<XREG>(xr, a.x, xchunks);
+    if (static_cast<int>(blockIdx.x) < a.l1_router_blocks) {
+        const int e = blockIdx.x * 4 + wave;
+        const auto r = make_rsrc(a.router_w, static_cast<uint32_t>(a.E) * row_bytes);
+        uint4 w[CHH];
 #pragma unroll
-        for (int p = 0; p < kK2Pairs; ++p) accg[p] = accu[p] = 0.f;
+        for (int u = 0; u < CHH; ++u) {
+            const int c = u * 64 + lane;
+            w[u] = buf_load16(r, (e < a.E && c < nch) ? static_cast<uint32_t>(e) * row_bytes + c * 16u : kOobOffset);
+        }
+        x_store<XT, XREG, false>(smem, xr);
+        __syncthreads();
+        float acc0 = 0.f, acc1 = 0.f;
+#pragma unroll
+        for (int u = 0; u < CHH; ++u) {
+            const int c = u * 64 + lane;
+            if (c < nch) {
+                if (u & 1)
+                    acc1 = dot_chunk<XT>(w[u], smem, c, acc1);
+                else
+                    acc0 = dot_chunk<XT>(w[u], smem, c, acc0);
+            }
+        }
+        const float tot = wave_sum_to_lane63(acc0 + acc1);
+        if (lane == 63 && e < a.E)
+            __hip_atomic_store(a.ws.logits + e, tot, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __builtin_amdgcn_s_waitcnt(0);  // each wave's logit store is complete ...
+        __syncthreads();
+        if (threadIdx.x == 0) {         // ... before the block counts itself done
+            // modular, so that one block of every call routes even if the counter did not
+            // start at zero (the routing then reads this call's own pointer table either way)
+            const uint32_t old = __hip_atomic_fetch_add(a.ws.counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            last_s = (old + 1) % static_cast<uint32_t>(a.l1_router_blocks) == 0;
+            if (last_s) __hip_atomic_store(a.ws.counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        __syncthreads();
+        if (last_s) route_block(a);
+    } else {
+        // ~0.2 us head start for the router rows' loads (issued by the first blocks): the
+        // router blocks then finish early and the routing block runs under this stream
+        __builtin_amdgcn_s_sleep(8);
+        const int i = (blockIdx.x - a.l1_router_blocks) * 4 + wave;
+        const bool v = i < a.Is;
+        const auto rg = make_rsrc(a.sh_gate, static_cast<uint32_t>(a.Is) * row_bytes);
+        const auto ru = make_rsrc(a.sh_up, static_cast<uint32_t>(a.Is) * row_bytes);
+        uint4 wg[CHH], wu[CHH];
+#pragma unroll
+        for (int u = 0; u < CHH; ++u) {
+            const int c = u * 64 + lane;
+            const uint32_t off = (v && c < nch) ? static_cast<uint32_t>(i) * row_bytes + c * 16u : kOobOffset;
+            wg[u] = buf_load16(rg, off);
+            wu[u] = buf_load16(ru, off);
+        }
+        x_store<XT, XREG, false>(smem, xr);
+        __syncthreads();
+        float ag = 0.f, au = 0.f;
+#pragma unroll
+        for (int u = 0; u < CHH; ++u) {
+            const int c = u * 64 + lane;
+            if (c < nch) {
+                ag = dot_chunk<XT>(wg[u], smem, c, ag);
+                au = dot_chunk<XT>(wu[u], smem, c, au);
+            }
+        }
+        ag = wave_sum_to_lane63(ag);
+        au = wave_sum_to_lane63(au);
+        if (lane == 63 && v) a.ws.shared_act[i] = act_fn(ag, au, a.act_kind, a.beta, a.lbeta);
+    }
+}
+
+// ------------------------------------------------------------------ L2
+// GA: MXFP4 groups per lane over H.  CHI: bf16 chunks per lane over Is.
+template <typename XT, int GA, int CHI>
+__global__ __launch_bounds__(256) void layer_l2(LayerArgs a) {
+    extern __shared__ uint4 smem[];
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+    if (static_cast<int>(blockIdx.x) < a.l2_shared_blocks) {
+        // shared down: kSharedDownRows bf16 rows [H, Is] per wave against the fp32 shared act,
+        // which each lane holds in registers for its own chunks (L2-resident after the first
+        // waves)
+        const int n0 = (blockIdx.x * 4 + wave) * kSharedDownRows;
+        const uint32_t row_bytes = static_cast<uint32_t>(a.Is) * 2u;
+        const int nch = a.Is >> 3;
+        const auto ra = make_rsrc(a.ws.shared_act, static_cast<uint32_t>(a.Is) * 4u);
+        float4 av[CHI][2];
+#pragma unroll
+        for (int u = 0; u < CHI; ++u) {
+            const int c = u * 64 + lane;
+            const bool ok = c < nch;
+            av[u][0] = __builtin_bit_cast(float4, buf_load16(ra, ok ? c * 32u : kOobOffset));
+            av[u][1] = __builtin_bit_cast(float4, buf_load16(ra, ok ? c * 32u + 16u : kOobOffset));
+        }
+        const auto rr = make_rsrc(a.sh_down, static_cast<uint32_t>(a.H) * row_bytes);
+        uint4 w[kSharedDownRows][CHI];
+#pragma unroll
+        for (int r = 0; r < kSharedDownRows; ++r)
+#pragma unroll
+            for (int u = 0; u < CHI; ++u) {
+                const int c = u * 64 + lane, n = n0 + r;
+                w[r][u] = buf_load16(rr, (n < a.H && c < nch) ? static_cast<uint32_t>(n) * row_bytes + c * 16u
+                                                                : kOobOffset);
+            }
+#pragma unroll
+        for (int r = 0; r < kSharedDownRows; ++r) {
+            float acc = 0.f;
+#pragma unroll
+            for (int u = 0; u < CHI; ++u) acc = dot8(w[r][u], av[u][0], av[u][1], acc);
+            const float t = wave_sum_to_lane63(acc);
+            if (lane == 63 && n0 + r < a.H) a.ws.yshared[n0 + r] = t;
+        }
+        return;
+    }
+    // routed gate/up: kRoutedPairs (slot j, row i) pairs per wave
+    constexpr int CPGX = XTile<XT>::kChunks;
+    constexpr int XREG = x_regs<XT>();
+    const int GH = a.H >> 5;
+    const uint32_t rowA = static_cast<uint32_t>(a.H >> 1);
+    uint4 xr[XREG];
+    x_load<XREG>(xr, a.x, GH * CPGX);
+    uint4 wg[kRoutedPairs][GA], wu[kRoutedPairs][GA];
+    uint32_t sg[kRoutedPairs][GA], su[kRoutedPairs][GA];
+    int jj[kRoutedPairs], ii[kRoutedPairs];
+    bool vv[kRoutedPairs];
+#pragma unroll
+    for (int p = 0; p < kRoutedPairs; ++p) {
+        const int pair = ((blockIdx.x - a.l2_shared_blocks) * 4 + wave) * kRoutedPairs + p;
+        const int j = pair / a.I, i = pair % a.I;
+        const bool v = j < a.k;
+        jj[p] = j, ii[p] = i, vv[p] = v;
+        const uint64_t *t = a.ws.sel_ptrs + (v ? j : 0) * 6;
+        const auto rg = make_rsrc(uniform_ptr(t[0]), static_cast<uint32_t>(a.I) * rowA);
+        const auto rgs = make_rsrc(uniform_ptr(t[1]), static_cast<uint32_t>(a.I * GH));
+        const auto ru = make_rsrc(uniform_ptr(t[2]), static_cast<uint32_t>(a.I) * rowA);
+        const auto rus = make_rsrc(uniform_ptr(t[3]), static_cast<uint32_t>(a.I * GH));
+#pragma unroll
+        for (int u = 0; u < GA; ++u) {
+            const int g = u * 64 + lane;
+            const bool ok = v && g < GH;
+            const uint32_t off = ok ? static_cast<uint32_t>(i) * rowA + g * 16u : kOobOffset;
+            const uint32_t soff = ok ? static_cast<uint32_t>(i * GH + g) : kOobOffset;
+            wg[p][u] = buf_load16(rg, off);
+            wu[p][u] = buf_load16(ru, off);
+            sg[p][u] = __builtin_amdgcn_raw_buffer_load_b8(rgs, soff, 0, 0);
+            su[p][u] = __builtin_amdgcn_raw_buffer_load_b8(rus, soff, 0, 0);
+        }
+    }
+    x_store<XT, XREG, true>(smem, xr);
+    __syncthreads();
+    float accg[kRoutedPairs], accu[kRoutedPairs];
+#pragma unroll
+    for (int p = 0; p < kRoutedPairs; ++p) accg[p] = accu[p] = 0.f;
+#pragma unroll
+    for (int p = 0; p < kRoutedPairs; ++p) {
 #pragma unroll
         for (int u = 0; u < GA; ++u) {
             const int g = u * 64 + lane;
@@ -334,171 +470,98 @@ __global__ __launch_bounds__(256) void layer_k2(LayerArgs a) {
                 XChunk<XT> xc[CPGX];
 #pragma unroll
                 for (int q = 0; q < CPGX; ++q) xc[q] = reinterpret_cast<const XChunk<XT> *>(smem)[XTile<XT>::slot(g, q)];
-#pragma unroll
-                for (int p = 0; p < kK2Pairs; ++p) {
-                    const uint32_t so = static_cast<uint32_t>(ii[p] * GH);
-                    accg[p] = fmaf(group_dot(wg_[p][u], xc), e8m0_to_f32(scale_byte(sg_[p][u], so, g)), accg[p]);
-                    accu[p] = fmaf(group_dot(wu_[p][u], xc), e8m0_to_f32(scale_byte(su_[p][u], so, g)), accu[p]);
-                }
+                accg[p] = fmaf(group_dot(wg[p][u], xc), e8m0_to_f32(sg[p][u]), accg[p]);
+                accu[p] = fmaf(group_dot(wu[p][u], xc), e8m0_to_f32(su[p][u]), accu[p]);
             }
         }
+    }
 #pragma unroll
-        for (int p = 0; p < kK2Pairs; ++p) {
-            const float g = wave_sum_to_lane63(accg[p]);
-            const float u = wave_sum_to_lane63(accu[p]);
-            if (lane == 63 && vv[p])
-                a.ws.act[static_cast<int64_t>(jj[p]) * a.I + ii[p]] = act_fn(g, u, a.act_kind, a.beta, a.lbeta);
-        }
-    } else {
-        // shared down: bf16 [H, Is] rows against shared_act (fp32), 2 rows per wave
-        uint4 *al = smem;
-        const int n = ((blockIdx.x - a.k2_routed_blocks) * 4 + wave) * 2;
-        const uint32_t row_bytes = static_cast<uint32_t>(a.Is) * 2u;
-        const auto rr = make_rsrc(a.sh_down, static_cast<uint32_t>(a.H) * row_bytes);
-        const __amdgpu_buffer_rsrc_t r[2] = {rr, rr};
-        const uint32_t off[2] = {static_cast<uint32_t>(n) * row_bytes, static_cast<uint32_t>(n + 1) * row_bytes};
-        const bool v[2] = {n < a.H, n + 1 < a.H};
-        uint4 w[2][CHI];
-        bf16_rows_load<CHI, 2>(r, off, a.Is, v, w);
-        stage_plain<float>(al, a.ws.shared_act, a.Is);
-        __syncthreads();
-        float t[2];
-        bf16_rows_dot<float, CHI, 2>(w, a.Is, al, t);
-        if (lane == 63) {
-            if (v[0]) a.ws.yshared[n] = t[0];
-            if (v[1]) a.ws.yshared[n + 1] = t[1];
-        }
+    for (int p = 0; p < kRoutedPairs; ++p) {
+        const float g = wave_sum_to_lane63(accg[p]);
+        const float u = wave_sum_to_lane63(accu[p]);
+        if (lane == 63 && vv[p]) a.ws.act[static_cast<int64_t>(jj[p]) * a.I + ii[p]] = act_fn(g, u, a.act_kind, a.beta, a.lbeta);
     }
 }
 
-// ------------------------------------------------------------------ K3
-// Blocks of 8 waves; each wave owns RPW output rows and needs the KT routed down rows of
-// each (K = I, GB groups per lane).  Order of work per block:
-//   1. the k experts' act vectors (L2-resident, 8 KB each) are loaded into registers and
-//      the scale dwords are issued,
-//   2. the whole weight stream (KT x RPW rows) is issued,
-//   3. act goes to LDS (that wait covers only the loads of step 1),
-//   4. experts are consumed in issue order, so compute overlaps the stream's tail.
-constexpr int kK3Waves = 8;
-
+// ------------------------------------------------------------------ L3
+// Block: KT waves (wave j = selected expert j) x RPW output rows.  Each lane holds the act
+// values of its GB groups of expert j in registers (fp32, loaded from the workspace); the
+// block combines the experts' row totals in slot order.
 template <int KT, int RPW, int GB>
-__global__ __launch_bounds__(512) void layer_k3(LayerArgs a) {
-    extern __shared__ uint4 smem[];
-    __shared__ uint64_t tab_s[kMaxTopK][2];
-    __shared__ float w_s[kMaxTopK];
-    constexpr int NT = kK3Waves * 64;
-    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+__global__ __launch_bounds__(KT * 64) void layer_l3(LayerArgs a) {
+    __shared__ float ys[RPW][KT];
+    const int j = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+    const bool live = j < a.k;  // waves past top_k idle (KT rounds top_k up)
     const int GI = a.I >> 5;
     const uint32_t rowB = static_cast<uint32_t>(a.I >> 1);
-    if (static_cast<int>(threadIdx.x) < KT) {
-        tab_s[threadIdx.x][0] = a.ws.sel_ptrs[threadIdx.x * 6 + 4];
-        tab_s[threadIdx.x][1] = a.ws.sel_ptrs[threadIdx.x * 6 + 5];
-        w_s[threadIdx.x] = a.ws.topk_w[threadIdx.x];
+    const int n0 = blockIdx.x * RPW;
+    // 1. the expert's down-projection pointers, then its act for this lane's groups (8 chunks
+    //    of 4 floats per group)
+    const uint64_t *t = a.ws.sel_ptrs + (live ? j : 0) * 6;
+    const auto rd = make_rsrc(uniform_ptr(t[4]), static_cast<uint32_t>(a.H) * rowB);
+    const auto rds = make_rsrc(uniform_ptr(t[5]), static_cast<uint32_t>(a.H * GI));
+    const auto ra = make_rsrc(a.ws.act + static_cast<int64_t>(live ? j : 0) * a.I, static_cast<uint32_t>(a.I) * 4u);
+    float4 av[GB][8];
+#pragma unroll
+    for (int u = 0; u < GB; ++u) {
+        const int g = u * 64 + lane;
+#pragma unroll
+        for (int q = 0; q < 8; ++q)
+            av[u][q] = __builtin_bit_cast(float4, buf_load16(ra, (live && g < GI) ? static_cast<uint32_t>(g) * 128u + q * 16u
+                                                                                   : kOobOffset));
     }
-    // 1. act chunks into registers (one fp32 tile of GI*8 chunks per expert slot)
-    const int per = GI * 8;
-    constexpr int AREG = KT * 64 * 8 / NT;  // chunks per thread at I <= 2048 per GB
-    uint4 av[AREG * GB];
-    {
-        const auto ra = make_rsrc(a.ws.act, static_cast<uint32_t>(KT * per * 16));
+    // 2. the expert's down rows of this block, and their scale bytes
+    uint4 wd[RPW][GB];
+    uint32_t sd[RPW][GB];
 #pragma unroll
-        for (int b = 0; b < AREG * GB; ++b) {
-            const int c = b * NT + threadIdx.x;
-            av[b] = buf_load16(ra, c < KT * per ? static_cast<uint32_t>(c) * 16u : kOobOffset);
-        }
-    }
-    __syncthreads();  // tab_s
-    const int n0 = (blockIdx.x * kK3Waves + wave) * RPW;
-    uint4 wd[KT][RPW][GB];
-    uint32_t sd[KT][RPW][GB];
-#pragma unroll
-    for (int j = 0; j < KT; ++j) {
-        const auto rds = make_rsrc(uniform_ptr(tab_s[j][1]), static_cast<uint32_t>(a.H * GI));
-#pragma unroll
-        for (int r = 0; r < RPW; ++r)
-#pragma unroll
-            for (int u = 0; u < GB; ++u) {
-                const int n = n0 + r, g = u * 64 + lane;
-                const bool ok = n < a.H && g < GI;
-                sd[j][r][u] = buf_load4(rds, ok ? scale_dword_off(static_cast<uint32_t>(n * GI), g) : kOobOffset);
-            }
-    }
-    // 2. the weight stream
-#pragma unroll
-    for (int j = 0; j < KT; ++j) {
-        const auto rd = make_rsrc(uniform_ptr(tab_s[j][0]), static_cast<uint32_t>(a.H) * rowB);
-#pragma unroll
-        for (int r = 0; r < RPW; ++r)
-#pragma unroll
-            for (int u = 0; u < GB; ++u) {
-                const int n = n0 + r, g = u * 64 + lane;
-                const bool ok = n < a.H && g < GI;
-                wd[j][r][u] = buf_load16(rd, ok ? static_cast<uint32_t>(n) * rowB + g * 16u : kOobOffset);
-            }
-    }
-    // 3. act to LDS
-#pragma unroll
-    for (int b = 0; b < AREG * GB; ++b) {
-        const int c = b * NT + threadIdx.x;
-        if (c < KT * per) {
-            const int j = c / per, cc = c % per;
-            smem[j * per + XTile<float>::slot(cc >> 3, cc & 7)] = av[b];
-        }
-    }
-    __syncthreads();
-    // 4. consume in issue order
-    float y[RPW];
-#pragma unroll
-    for (int r = 0; r < RPW; ++r) y[r] = 0.f;
-#pragma unroll
-    for (int j = 0; j < KT; ++j) {
-        const uint4 *al = smem + j * per;
-        float acc[RPW];
-#pragma unroll
-        for (int r = 0; r < RPW; ++r) acc[r] = 0.f;
+    for (int r = 0; r < RPW; ++r)
 #pragma unroll
         for (int u = 0; u < GB; ++u) {
-            const int g = u * 64 + lane;
-            if (g < GI) {
-                float4 ac[8];
-#pragma unroll
-                for (int q = 0; q < 8; ++q) ac[q] = reinterpret_cast<const float4 *>(al)[XTile<float>::slot(g, q)];
-#pragma unroll
-                for (int r = 0; r < RPW; ++r) {
-                    const int n = n0 + r;
-                    acc[r] = fmaf(group_dot(wd[j][r][u], ac),
-                                  e8m0_to_f32(scale_byte(sd[j][r][u], static_cast<uint32_t>(n * GI), g)), acc[r]);
-                }
-            }
+            const int n = n0 + r, g = u * 64 + lane;
+            const bool ok = live && n < a.H && g < GI;
+            wd[r][u] = buf_load16(rd, ok ? static_cast<uint32_t>(n) * rowB + g * 16u : kOobOffset);
+            sd[r][u] = __builtin_amdgcn_raw_buffer_load_b8(rds, ok ? static_cast<uint32_t>(n * GI + g) : kOobOffset, 0, 0);
         }
+    // 3. row dots; wave totals to LDS
 #pragma unroll
-        for (int r = 0; r < RPW; ++r) y[r] = fmaf(w_s[j], wave_sum_to_lane63(acc[r]), y[r]);
+    for (int r = 0; r < RPW; ++r) {
+        float acc = 0.f;
+#pragma unroll
+        for (int u = 0; u < GB; ++u)
+            if (u * 64 + lane < GI) acc = fmaf(group_dot(wd[r][u], av[u]), e8m0_to_f32(sd[r][u]), acc);
+        const float tot = wave_sum_to_lane63(acc);
+        if (lane == 63) ys[r][j] = tot;
     }
-    if (lane == 63) {
-#pragma unroll
-        for (int r = 0; r < RPW; ++r) {
-            const int n = n0 + r;
-            if (n < a.H) {
-                const float v = y[r] + (a.sh_down ? a.ws.yshared[n] : 0.f);
-                if (a.out_bf16)
-                    static_cast<uint16_t *>(a.out)[n] = f32_to_bf16(v);
-                else
-                    static_cast<float *>(a.out)[n] = v;
-            }
+    __syncthreads();
+    // 4. combine in slot order with the shared expert's row
+    if (static_cast<int>(threadIdx.x) < RPW) {
+        const int r = threadIdx.x, n = n0 + r;
+        if (n < a.H) {
+            float y = 0.f;
+            for (int jj = 0; jj < a.k; ++jj) y = fmaf(a.ws.topk_w[jj], ys[r][jj], y);
+            if (a.sh_down) y += a.ws.yshared[n];
+            if (a.out_bf16)
+                static_cast<uint16_t *>(a.out)[n] = f32_to_bf16(y);
+            else
+                static_cast<float *>(a.out)[n] = y;
         }
     }
 }
 
 // ------------------------------------------------------------------ host side
 struct LayerWsLayout {
-    size_t logits, scores, corrected, idx, w, shared_act, act, yshared, ptrs, total;
+    size_t logits, scores, corrected, idx, w, shared_act, act, yshared, ptrs, counter, total;
 };
 
 static size_t up256(size_t v) { return (v + 255) & ~size_t(255); }
 
+// The router-block counter sits in the first 256 bytes for every shape, so workspaces
+// shared by layers of different shapes keep it at one place (zero between calls); the
+// records after it are rewritten by every call.
 static LayerWsLayout layer_ws_layout(int64_t H, int64_t I, int64_t Is, int64_t E, int64_t k) {
     LayerWsLayout L{};
     size_t o = 0;
+    L.counter = o, o += 256;
     L.logits = o, o += up256(E * 4);
     L.scores = o, o += up256(E * 4);
     L.corrected = o, o += up256(E * 4);
@@ -512,88 +575,65 @@ static LayerWsLayout layer_ws_layout(int64_t H, int64_t I, int64_t Is, int64_t E
     return L;
 }
 
-static int launch_route(const LayerArgs &a, hipStream_t st) {
-    const int threads = static_cast<int>(std::max<int64_t>(64, cdiv(a.E, 64) * 64));
-    layer_route<<<dim3(1), threads, 0, st>>>(a);
-    return check_hip(hipGetLastError(), "moe layer route");
+template <typename XT>
+static int launch_l1(LayerArgs &a, bool with_shared, hipStream_t st) {
+    const int chh = static_cast<int>(cdiv(a.H / 8, 64));
+    a.l1_router_blocks = static_cast<int>(cdiv(a.E, 4));
+    const int blocks = a.l1_router_blocks + (with_shared ? static_cast<int>(cdiv(a.Is, 4)) : 0);
+    const size_t lds = static_cast<size_t>(256) * x_regs<XT>() * 16;
+#define K3_L1(C) \
+    if (chh <= C) { \
+        layer_l1<XT, C><<<dim3(blocks), 256, lds, st>>>(a); \
+        return check_hip(hipGetLastError(), "moe layer L1"); \
+    }
+    K3_L1(4) K3_L1(8) K3_L1(12) K3_L1(16)
+#undef K3_L1
+    return set_error(K3_ERR_SHAPE, "moe layer: H=%d too wide", a.H);
 }
 
 template <typename XT>
 static int launch_layer(LayerArgs &a, hipStream_t st) {
     const int GH = a.H / 32, GI = a.I / 32;
-    const int chh = cdiv(a.H / 8, 64);        // bf16 chunks per lane over H
-    const int chi = cdiv(a.Is / 8, 64);       // over Is
-    const int ga = GH <= 128 ? 2 : (GH <= 256 ? 4 : 0);
+    const int chi = static_cast<int>(cdiv(a.Is / 8, 64));
+    const int ga = GH <= 64 ? 1 : (GH <= 128 ? 2 : (GH <= 256 ? 4 : 0));
     const int gb = GI <= 64 ? 1 : (GI <= 128 ? 2 : 0);
-    if (!ga || !gb || chh > 16 || (a.sh_down && chi > 8))
+    if (!ga || !gb || (a.sh_down && chi > 8))
         return set_error(K3_ERR_SHAPE, "moe layer: H=%d I=%d Is=%d outside the kernels' range", a.H, a.I, a.Is);
-    // K1
-    a.k1_router_blocks = static_cast<int>(cdiv(a.E, 4));
-    const int k1_blocks = a.k1_router_blocks + (a.sh_gate ? static_cast<int>(cdiv(a.Is, 4)) : 0);
-    const size_t lds1 = static_cast<size_t>(a.H) * sizeof(XT);
-#define K1(C) \
-    if (chh <= C) { layer_k1<XT, C><<<dim3(k1_blocks), 256, lds1, st>>>(a); } else
-    K1(4) K1(8) K1(12) K1(16) {}
-#undef K1
-    int rc = check_hip(hipGetLastError(), "moe layer K1");
+    int rc = launch_l1<XT>(a, a.sh_gate != nullptr, st);
     if (rc) return rc;
-    rc = launch_route(a, st);
-    if (rc) return rc;
-    // K2
-    a.k2_routed_blocks = static_cast<int>(cdiv(static_cast<int64_t>(a.k) * a.I, 4 * kK2Pairs));
-    const int k2_blocks = a.k2_routed_blocks + (a.sh_down ? static_cast<int>(cdiv(a.H, 8)) : 0);
-    const size_t lds2 = std::max<size_t>(static_cast<size_t>(GH) * XTile<XT>::kChunks * 16,
-                                         static_cast<size_t>(a.Is) * 4);
-#define K2(G_, C_) \
-    if (ga == G_ && chi <= C_) { layer_k2<XT, G_, C_><<<dim3(k2_blocks), 256, lds2, st>>>(a); } else
-    K2(2, 4) K2(2, 8) K2(4, 4) K2(4, 8) {}
-#undef K2
-    rc = check_hip(hipGetLastError(), "moe layer K2");
-    if (rc) return rc;
-    // K3: 4 rows per wave at I <= 2048, 2 rows per wave above (register budget)
-    const int rpw = gb == 1 ? 4 : 2;
-    const int k3_blocks = static_cast<int>(cdiv(a.H, kK3Waves * rpw));
-    const size_t lds3 = static_cast<size_t>(a.k) * a.I * 4;
-    const void *f3 = nullptr;
-#define K3SEL(KT_, GB_, R_) \
-    if (a.k == KT_ && gb == GB_) f3 = reinterpret_cast<const void *>(&layer_k3<KT_, R_, GB_>);
-    K3SEL(1, 1, 4) K3SEL(2, 1, 4) K3SEL(4, 1, 4) K3SEL(6, 1, 4) K3SEL(8, 1, 4)
-    K3SEL(1, 2, 2) K3SEL(2, 2, 2) K3SEL(4, 2, 2) K3SEL(8, 2, 2)
-#undef K3SEL
-    if (!f3) return set_error(K3_ERR_SHAPE, "moe layer: no combine kernel for top_k=%d, I=%d", a.k, a.I);
-    if (lds3 + 1024 > 64 * 1024) {
-        rc = check_hip(hipFuncSetAttribute(f3, hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds3)),
-                       "moe layer K3 LDS limit");
-        if (rc) return rc;
+    // L2
+    a.l2_shared_blocks = a.sh_down ? static_cast<int>(cdiv(a.H, 4 * kSharedDownRows)) : 0;
+    const int routed_blocks = static_cast<int>(cdiv(static_cast<int64_t>(a.k) * a.I, 4 * kRoutedPairs));
+    const size_t lds2 = static_cast<size_t>(256) * x_regs<XT>() * 16;
+    const dim3 g2(static_cast<unsigned>(a.l2_shared_blocks + routed_blocks));
+#define K3_L2(G_, C_) \
+    if (ga == G_ && (chi <= C_ || !a.sh_down)) { \
+        layer_l2<XT, G_, C_><<<g2, 256, lds2, st>>>(a); \
+    } else
+    K3_L2(1, 4) K3_L2(1, 8) K3_L2(2, 4) K3_L2(2, 8) K3_L2(4, 4) K3_L2(4, 8) {
+        return set_error(K3_ERR_SHAPE, "moe layer: no L2 kernel for H=%d Is=%d", a.H, a.Is);
     }
-#define K3RUN(KT_, GB_, R_) \
-    if (a.k == KT_ && gb == GB_) layer_k3<KT_, R_, GB_><<<dim3(k3_blocks), kK3Waves * 64, lds3, st>>>(a);
-    K3RUN(1, 1, 4) K3RUN(2, 1, 4) K3RUN(4, 1, 4) K3RUN(6, 1, 4) K3RUN(8, 1, 4)
-    K3RUN(1, 2, 2) K3RUN(2, 2, 2) K3RUN(4, 2, 2) K3RUN(8, 2, 2)
-#undef K3RUN
-    return check_hip(hipGetLastError(), "moe layer K3");
+#undef K3_L2
+    rc = check_hip(hipGetLastError(), "moe layer L2");
+    if (rc) return rc;
+    // L3: rows per block so each wave streams a few KiB of its expert's down rows
+    constexpr int R = 16;
+    const dim3 g3(static_cast<unsigned>(cdiv(a.H, R)));
+    const int kt = a.k <= 1 ? 1 : (a.k <= 2 ? 2 : (a.k <= 4 ? 4 : (a.k <= 8 ? 8 : 16)));
+#define K3_L3(KT_, GB_) \
+    if (kt == KT_ && gb == GB_) { \
+        layer_l3<KT_, R, GB_><<<g3, KT_ * 64, 0, st>>>(a); \
+        return check_hip(hipGetLastError(), "moe layer L3"); \
+    }
+    K3_L3(1, 1) K3_L3(2, 1) K3_L3(4, 1) K3_L3(8, 1) K3_L3(16, 1)
+    K3_L3(1, 2) K3_L3(2, 2) K3_L3(4, 2) K3_L3(8, 2) K3_L3(16, 2)
+#undef K3_L3
+    return set_error(K3_ERR_SHAPE, "moe layer: no combine kernel for top_k=%d", a.k);
 }
 
 }  // namespace k3
 
 using namespace k3;
-
-static int route_only(LayerArgs &a, int x_bf16, hipStream_t st) {
-    const int chh = static_cast<int>(cdiv(a.H / 8, 64));
-    if (chh > 16) return set_error(K3_ERR_SHAPE, "moe route: H=%d too wide", a.H);
-    a.k1_router_blocks = static_cast<int>(cdiv(a.E, 4));
-    const size_t lds1 = static_cast<size_t>(a.H) * (x_bf16 ? 2 : 4);
-#define K1(C) \
-    if (chh <= C) { \
-        if (x_bf16) layer_k1<uint16_t, C><<<dim3(a.k1_router_blocks), 256, lds1, st>>>(a); \
-        else layer_k1<float, C><<<dim3(a.k1_router_blocks), 256, lds1, st>>>(a); \
-    } else
-    K1(4) K1(8) K1(12) K1(16) {}
-#undef K1
-    int rc = check_hip(hipGetLastError(), "moe route K1");
-    if (rc) return rc;
-    return launch_route(a, st);
-}
 
 extern "C" int64_t k3_moe_layer_workspace_size(int64_t H, int64_t I, int64_t shared_I, int64_t n_experts,
                                                int64_t top_k) {
@@ -615,14 +655,12 @@ static int layer_impl(const void *x, int x_dtype, const void *router_w, const vo
     if (route_kind != K3_ROUTE_SOFTMAX && route_kind != K3_ROUTE_SIGMOID_BIAS)
         return set_error(K3_ERR_SHAPE, "moe layer: route_kind");
     if (act_kind != K3_ACT_SILU && act_kind != K3_ACT_SITU) return set_error(K3_ERR_SHAPE, "moe layer: act_kind");
-    if (H <= 0 || I <= 0 || H % 128 || I % 128 || (has_shared && (shared_I <= 0 || shared_I % 128)))
-        return set_error(K3_ERR_SHAPE, "moe layer: H, I and shared_I must be positive multiples of 128");
+    if (H <= 0 || I <= 0 || H % 128 || I % 128 || H > 8192 || (has_shared && (shared_I <= 0 || shared_I % 128)))
+        return set_error(K3_ERR_SHAPE,
+                         "moe layer: H, I and shared_I must be positive multiples of 128, H <= 8192");
     if (n_experts <= 0 || n_experts > kMaxExperts || top_k <= 0 || top_k > kMaxTopK || top_k > n_experts)
         return set_error(K3_ERR_SHAPE, "moe layer: n_experts must be in 1..%d and top_k in 1..min(%d, n_experts)",
                          kMaxExperts, kMaxTopK);
-    if (top_k * I * 4 > 160 * 1024)
-        return set_error(K3_ERR_SHAPE, "moe layer: top_k * I = %lld exceeds the combine kernel's LDS",
-                         (long long)(top_k * I));
     const LayerWsLayout L = layer_ws_layout(H, I, has_shared ? shared_I : 0, n_experts, top_k);
     if (workspace_bytes < static_cast<int64_t>(L.total))
         return set_error(K3_ERR_WORKSPACE, "moe layer: workspace %lld < %zu bytes", (long long)workspace_bytes, L.total);
@@ -650,6 +688,7 @@ static int layer_impl(const void *x, int x_dtype, const void *router_w, const vo
     a.ws.act = reinterpret_cast<float *>(w + L.act);
     a.ws.yshared = reinterpret_cast<float *>(w + L.yshared);
     a.ws.sel_ptrs = reinterpret_cast<uint64_t *>(w + L.ptrs);
+    a.ws.counter = reinterpret_cast<uint32_t *>(w + L.counter);
     a.H = static_cast<int>(H);
     a.I = static_cast<int>(I);
     a.Is = has_shared ? static_cast<int>(shared_I) : 0;
@@ -663,7 +702,8 @@ static int layer_impl(const void *x, int x_dtype, const void *router_w, const vo
     a.lbeta = linear_beta;
     a.out_bf16 = out_dtype == K3_BF16;
     auto st = static_cast<hipStream_t>(stream);
-    if (route_only_flag) return route_only(a, x_dtype == K3_BF16, st);
+    if (route_only_flag)
+        return x_dtype == K3_BF16 ? launch_l1<uint16_t>(a, false, st) : launch_l1<float>(a, false, st);
     return x_dtype == K3_BF16 ? launch_layer<uint16_t>(a, st) : launch_layer<float>(a, st);
 }
 
