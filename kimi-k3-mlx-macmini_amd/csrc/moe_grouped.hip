@@ -1,27 +1,46 @@
-// Grouped routed-expert FFN for many tokens (prefill): every routed (token, slot) pair is
-// grouped by expert, and each expert runs as a GEMM with M = its token count, so each
-// expert's MXFP4 weights stream from HBM once per 32-token tile group instead of once per
-// token.
+// Grouped routed-expert FFN for many tokens (prefill) on native MXFP4 MFMA: every routed
+// (token, slot) pair is grouped by expert and each expert runs as a GEMM with M = its token
+// count, so each expert's MXFP4 weights stream from HBM once per 64-row tile instead of
+// once per token.
 //
 // Reference: LatentMoE.__call__ (air_llm/models/kimi_k3/moe.py:110-132; k3ref
 // k3ref/layers.py:241-261): for each distinct routed expert, gather its tokens, run
 // expert_forward, scale by the gate weight and add into y.  The reference loops over
 // experts on the host; here:
 //
-//   count   block e counts the pairs routed to expert e                      -> counts[E]
-//   plan    one block: exclusive scan of the counts (segment bases) and the list of
-//           32-token tiles (expert, first row) of every non-empty expert
-//   place   block e writes its pairs, in (token, slot) order, into perm[base_e ...]
-//   gateup  block (tile, 128 intermediate rows): act = f(x W_gate^T, x W_up^T) for the
-//           tile's tokens; bf16 MFMA (v_mfma_f32_16x16x32_bf16) on x (bf16) and the MXFP4
-//           weights decoded in registers with their E8M0 scale folded in
-//           (v_cvt_scalef32_pk_bf16_fp4: E2M1 x 2^e is exact in bf16); act is stored as a
-//           bf16 hi/lo pair so the next product keeps fp32-class precision
-//   down    block (tile, 256 output rows): y_pair = act W_down^T (MFMAs on act_hi and
-//           act_lo) -> fp32 rows per (token, slot) pair
-//   combine y[t] = sum_slot w[t, slot] * y_pair[t, slot], slots in order
+//   count    block e counts the pairs routed to expert e                      -> counts[E]
+//   plan     one block: exclusive scan of the counts (segment bases) and the list of
+//            64-row tiles (expert, first row) of every non-empty expert
+//   place    block e writes its pairs, in (token, slot) order, into perm[base_e ...]
+//   quant_x  x (bf16) -> two E4M3 terms, one E8M0 scale per 32 elements per term:
+//            x = 2^e1 t1 + 2^e2 t2, exact for every element within 2^13 of its block's max
+//   gateup   block (tile, 128 intermediate indices): v_mfma_scale_f32_16x16x128_f8f6f4 with
+//            the expert's MXFP4 rows as the FP4 A operand and their E8M0 bytes as the A
+//            scales (no decode), the x terms as the FP8 B operand; act = f(gate, up) in
+//            fp32, split in registers into three E4M3 terms per 32 (about 12 bits)
+//   down     block (tile, 256 output rows): the same MFMA over the three act terms
+//            -> fp32 rows per (token, slot) pair
+//   combine  y[t] = sum_slot w[t, slot] * y_pair[t, slot], slots in order
 //
 // Deterministic: no atomics, fixed summation orders everywhere.
+//
+// Operand layout of v_mfma_scale_f32_16x16x128_f8f6f4 with FP4 A (cbsz 4) and FP8 E4M3 B
+// (blgp 0), as measured on gfx950:
+//   A   lane l: weight row l%16, the 32 elements of K block l/16 (of the instruction's 128),
+//       element j in nibble j, low nibble first -- the MXFP4 byte order, loaded verbatim
+//   B   lane l: column l%16; with g = l/16, bytes 0-15 hold elements 16(g%2)..16(g%2)+15 of
+//       K block g/2 and bytes 16-31 the same elements of K block 2+g/2
+//   scale_a / scale_b of lane l: row / column l%16, K block l/16; op_sel picks the byte
+//   C   lane l, register v: row 4(l/16)+v, column l%16
+// The 128-element dot is accumulated about 12 bits below its largest product (unbiased
+// rounding, measured), then added into the fp32 C.
+//
+// K runs in super-steps of 256: a lane's 32-byte A load covers blocks 2q, 2q+1 (q = l/16)
+// and MFMA m in {0, 1} uses block 2q+m, so MFMA m's K block q' is super-step block 2q'+m.
+// B rows are therefore stored in "MX-B" order: per super-step, sixteen 16-byte pieces
+// p = (m*2 + h)*4 + g, piece p holding elements 16(g%2)..+15 of block 4h + 2(g/2) + m.  The
+// B operand of (m, lane) is then pieces (m, h=0, g) and (m, h=1, g) of its row, and its
+// scale is byte 2g+m of the row's eight block scales (natural order).
 #include <algorithm>
 
 #include "k3_common.h"
@@ -30,14 +49,11 @@
 namespace k3 {
 namespace {
 
-constexpr int kMt = 32;           // tokens per tile (two MFMA row tiles)
-constexpr int kKs = 64;           // K per pipeline step (two MFMA k-steps)
-constexpr int kNg = 256;          // weight rows per block (gate/up: 128 + 128)
-constexpr int kThreads = 512;     // 8 waves: wave w owns weight rows [32 w, 32 w + 32)
-constexpr int kARow = kKs + 8;    // padded bf16 A row in LDS (144 B)
-constexpr int kBRow = 9;          // padded B row in LDS: 32 packed bytes + 4 pad, in dwords
+constexpr int kTM = 64;        // grouped rows (tokens) per tile: four 16-column B tiles
+constexpr int kSS = 256;       // K elements per super-step
+constexpr int kThreads = 256;  // 4 waves
 
-typedef float f32x4_t __attribute__((ext_vector_type(4)));
+typedef int i32x8 __attribute__((ext_vector_type(8)));
 
 struct GroupArgs {
     const int32_t *idx;    // [P] expert id of pair p = t * k + slot
@@ -51,7 +67,7 @@ struct GroupArgs {
     int max_tiles;
 };
 
-// Stable compaction of the pairs equal to `e` (wave ballots, block prefix over 8 waves).
+// Stable compaction of the pairs equal to `e` (wave ballots, block prefix over 4 waves).
 // Called by every thread of a 256-thread block; returns the block's total.
 template <bool WRITE>
 __device__ int scan_expert(const GroupArgs &g, int e, int32_t *out) {
@@ -88,7 +104,7 @@ __global__ __launch_bounds__(1024) void group_plan_kernel(GroupArgs g) {
     const int e = threadIdx.x;
     const int c = e < g.E ? g.counts[e] : 0;
     sc[e] = c;
-    st[e] = (c + kMt - 1) / kMt;
+    st[e] = (c + kTM - 1) / kTM;
     __syncthreads();
     for (int off = 1; off < 1024; off <<= 1) {  // inclusive Hillis-Steele scans
         const int a = e >= off ? sc[e - off] : 0, b = e >= off ? st[e - off] : 0;
@@ -99,223 +115,400 @@ __global__ __launch_bounds__(1024) void group_plan_kernel(GroupArgs g) {
     }
     if (e < g.E) {
         g.base[e] = sc[e] - c;
-        const int t0 = st[e] - (c + kMt - 1) / kMt;
-        for (int j = 0; j * kMt < c; ++j) {
+        const int t0 = st[e] - (c + kTM - 1) / kTM;
+        for (int j = 0; j * kTM < c; ++j) {
             if (t0 + j < g.max_tiles) {
                 g.tile_e[t0 + j] = e;
-                g.tile_m0[t0 + j] = j * kMt;
+                g.tile_m0[t0 + j] = j * kTM;
             }
         }
     }
     if (e == 1023) *g.n_tiles = min(st[1023], g.max_tiles);
 }
 
-// ------------------------------------------------------------------ grouped GEMMs
-struct GemmArgs {
-    const uint16_t *x;       // gate/up: [T, K] bf16 token rows
-    const uint16_t *a_hi;    // down: act hi [P, K] bf16, rows in grouped order
-    const uint16_t *a_lo;    // down: act lo
+// ------------------------------------------------------------------ E4M3 / E8M0 terms
+// Exponent e of the block scale 2^e for a block whose largest magnitude is amax, chosen so
+// amax / 2^e lies in [128, 256) (below E4M3's 448); clamped to the E8M0 range.
+__device__ __forceinline__ int block_exp(float amax) {
+    const int ea = static_cast<int>((__float_as_uint(amax) >> 23) & 0xffu) - 127;
+    return max(ea - 7, -127);
+}
+
+// E4M3 (OCP, bias 7) code of x, |x| < 256, rounded to nearest even; q receives its value.
+__device__ __forceinline__ uint32_t e4m3_rne(float x, float &q) {
+    const float a = fabsf(x);
+    uint32_t code;
+    float v;
+    if (a < 0.015625f) {  // subnormals: multiples of 2^-9 (rounding up to 8 gives 2^-6, code 8)
+        const float m = rintf(a * 512.f);
+        code = static_cast<uint32_t>(m);
+        v = m * 0.001953125f;
+    } else {              // normals: keep 3 mantissa bits, the carry runs into the exponent
+        uint32_t b = __float_as_uint(a);
+        b += 0x7ffffu + ((b >> 20) & 1u);
+        b &= 0xfff00000u;
+        v = __uint_as_float(b);
+        code = (b >> 20) - 960u;  // ((exp - 127 + 7) << 3) | mantissa
+    }
+    const uint32_t s = __float_as_uint(x) >> 31;
+    q = s ? -v : v;
+    return code | (s << 7);
+}
+
+// Byte offset, inside one row in MX-B order, of the 16-element half `half` of K block b.
+__device__ __forceinline__ uint32_t mxb_offset(uint32_t b, uint32_t half) {
+    const uint32_t bb = b & 7u, m = bb & 1u, h = bb >> 2, g = ((bb >> 1) & 1u) * 2u + half;
+    return (b >> 3) * kSS + ((m * 2u + h) * 4u + g) * 16u;
+}
+
+__device__ __forceinline__ float shfl_xor_f(float v, int m) { return __shfl_xor(v, m, 64); }
+
+// ------------------------------------------------------------------ quant_x
+struct QxArgs {
+    const uint16_t *x;    // [T, H] bf16
+    uint8_t *x8;          // [2][T][Hpad] E4M3 codes, MX-B order
+    uint8_t *xs;          // [2][T][Hpad / 32] E8M0
+    int T, H, Hpad;
+    uint32_t term, sterm; // bytes per term of x8 / xs
+};
+
+// One thread per 16-element half block; the two halves of a block are adjacent lanes.
+__global__ __launch_bounds__(256) void quant_x_kernel(QxArgs a) {
+    const int halves = a.H >> 4;
+    const int idx = blockIdx.x * 256 + threadIdx.x;
+    const bool ok = idx < a.T * halves;
+    const int t = ok ? idx / halves : 0, hh = ok ? idx % halves : 0;
+    float v[16];
+    if (ok) {
+        const uint4 *src = reinterpret_cast<const uint4 *>(a.x + static_cast<int64_t>(t) * a.H + hh * 16);
+        const uint4 u0 = src[0], u1 = src[1];
+        const uint32_t w[8] = {u0.x, u0.y, u0.z, u0.w, u1.x, u1.y, u1.z, u1.w};
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            v[2 * i] = __uint_as_float(w[i] << 16);
+            v[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) v[i] = 0.f;
+    }
+    const uint32_t row8 = static_cast<uint32_t>(t) * a.Hpad + mxb_offset(hh >> 1, hh & 1);
+    const uint32_t rows = static_cast<uint32_t>(t) * (a.Hpad >> 5) + (hh >> 1);
+#pragma unroll
+    for (int term = 0; term < 2; ++term) {
+        float amax = 0.f;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) amax = fmaxf(amax, fabsf(v[i]));
+        amax = fmaxf(amax, shfl_xor_f(amax, 1));
+        const int e = block_exp(amax);
+        uint32_t c[4] = {0u, 0u, 0u, 0u};
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            float q;
+            c[i >> 2] |= e4m3_rne(ldexpf(v[i], -e), q) << (8 * (i & 3));
+            v[i] -= ldexpf(q, e);
+        }
+        if (ok) {
+            *reinterpret_cast<uint4 *>(a.x8 + term * a.term + row8) = make_uint4(c[0], c[1], c[2], c[3]);
+            if ((hh & 1) == 0) a.xs[term * a.sterm + rows] = static_cast<uint8_t>(e + 127);
+        }
+    }
+}
+
+// ------------------------------------------------------------------ grouped MFMA GEMMs
+struct MxArgs {
+    const uint8_t *b8;       // B terms [TERMS][rows][Kpad], MX-B order
+    const uint8_t *bs;       // B scales [TERMS][rows][Kpad / 32]
+    uint32_t b_term, bs_term;
     const uint64_t *table;   // [E][6] expert pointers
     const int32_t *counts, *base, *perm, *tile_e, *tile_m0, *n_tiles;
-    uint16_t *act_hi, *act_lo;  // gate/up output [P, I]
+    uint8_t *a8, *as;        // gate/up output: act terms [3][P][Ipad], scales [3][P][Ipad / 32]
+    uint32_t a_term, as_term;
+    int Ipad;
     float *ypair;            // down output [P, H]: row = pair id
-    int K, N, top_k;         // K: reduction length; N: weight rows of one projection
-    int nt_per_tile;         // weight-row blocks per tile
-    int max_tiles;
-    int act_kind;
+    int K, Kpad, N;          // reduction length, its padded row length, weight rows of one projection
+    int top_k, max_tiles, act_kind;
     float beta, lbeta;
 };
 
-__device__ __forceinline__ f32x4_t mfma_bf16(bf16x8 a, bf16x8 b, f32x4_t c) {
-    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+template <int M>
+__device__ __forceinline__ f32x4 mfma_fp4_fp8(const uint4 &a, const uint4 &b0, const uint4 &b1, f32x4 c,
+                                              uint32_t sa, uint32_t sb) {
+    const i32x8 av = {static_cast<int>(a.x), static_cast<int>(a.y), static_cast<int>(a.z), static_cast<int>(a.w),
+                      0, 0, 0, 0};
+    const i32x8 bv = {static_cast<int>(b0.x), static_cast<int>(b0.y), static_cast<int>(b0.z), static_cast<int>(b0.w),
+                      static_cast<int>(b1.x), static_cast<int>(b1.y), static_cast<int>(b1.z), static_cast<int>(b1.w)};
+    return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(av, bv, c, 4, 0, M, static_cast<int>(sa), M,
+                                                            static_cast<int>(sb));
 }
 
-// 8 packed E2M1 codes (one dword) -> 8 bf16 scaled by 2^(e-127), exact for normal results
-__device__ __forceinline__ bf16x8 decode8(uint32_t w, float s) {
-    const bf16x2 a = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, s, 0);
-    const bf16x2 b = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, s, 1);
-    const bf16x2 c = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, s, 2);
-    const bf16x2 d = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, s, 3);
-    return bf16x8{a[0], a[1], b[0], b[1], c[0], c[1], d[0], d[1]};
-}
-
-// DOWN == false: gate/up + activation (weights rows 0..127 gate, 128..255 up of the same
-// 128 intermediate indices).  DOWN == true: 256 output rows of W_down, A = act hi/lo.
+// DOWN == false: gate/up + activation.  Wave w owns the 32 intermediate indices
+// [i0 + 32 w, +32): A tiles j = 0, 1 are their gate rows and j = 2, 3 their up rows, so the
+// activation of a (token, index) pair meets both products in one lane.
+// DOWN == true: wave w owns 64 output rows [n0 + 64 w, +64) of W_down, B = the act terms.
 template <bool DOWN>
-__global__ __launch_bounds__(kThreads) void grouped_gemm_kernel(GemmArgs a) {
-    constexpr int AH = DOWN ? 2 : 1;  // A planes (hi, lo)
-    __shared__ __align__(16) uint16_t a_s[2][AH][kMt * kARow];
-    __shared__ __align__(16) uint32_t b_s[2][kNg * kBRow];
-    __shared__ uint16_t sc_s[2][kNg];
-    __shared__ float g_s[DOWN ? 1 : kMt * 129];  // gate results for the epilogue
+__global__ __launch_bounds__(kThreads, 1) void mx_gemm_kernel(MxArgs a) {
+    constexpr int TERMS = DOWN ? 3 : 2;
+    // two LDS tiles of B: [buffer][ct][term][piece][column] 16-byte pieces, then
+    // [buffer][ct][term][column][block pair] scale pairs
+    extern __shared__ uint4 smem[];
+    constexpr int kXT = 4 * TERMS * 16 * 16;  // uint4 per tile
+    constexpr int kST = 4 * TERMS * 16 * 4;   // uint16 per scale tile
+    uint16_t *const ssm = reinterpret_cast<uint16_t *>(smem + 2 * kXT);
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int nb = static_cast<int>(gridDim.x);
     const int w = (nb & 7) == 0 ? (blockIdx.x & 7) * (nb >> 3) + (blockIdx.x >> 3) : blockIdx.x;
+    // Consecutive blocks on one XCD take consecutive tiles of one weight-row block, so the
+    // tiles of a hot expert stream the same weight rows together and share them in L2
+    // (ordering the weight-row blocks of one tile together instead, to share its B rows,
+    // measured 15% slower on the 2048-token Zipf prefill).
     const int tile = w % a.max_tiles, nt = w / a.max_tiles;
     if (tile >= *a.n_tiles) return;
     const int e = a.tile_e[tile], m0 = a.tile_m0[tile];
-    const int cnt = a.counts[e];
-    const int rows = min(kMt, cnt - m0);
+    const int rows = min(kTM, a.counts[e] - m0);
     const int pos0 = a.base[e] + m0;  // grouped row of the tile's first token
+    const int nct = (rows + 15) >> 4;
     const uint64_t *ptr = a.table + static_cast<int64_t>(e) * 6;
-    const int KG = a.K >> 5;          // scale groups per weight row
-    const uint32_t rowb = static_cast<uint32_t>(a.K >> 1);
+    const int KB = a.K >> 5;
+    const int NS = a.Kpad / kSS;
+    const int r16 = lane & 15, q = lane >> 4;
 
-    // ---- per-thread load assignments
-    // A: row r = c >> 3, 16-byte chunk c & 7 of the step's 128 bytes (threads 0..255 per plane)
-    const int ac = tid & 255, ar = ac >> 3, ach = ac & 7, aplane = DOWN ? (tid >> 8) : 0;
-    const bool a_thread = DOWN || tid < 256;
-    const uint16_t *arow = nullptr;
-    if (a_thread && ar < rows) {
-        if (DOWN) {
-            arow = (aplane ? a.a_lo : a.a_hi) + static_cast<int64_t>(pos0 + ar) * a.K;
-        } else {
-            const int pair = a.perm[pos0 + ar];
-            arow = a.x + static_cast<int64_t>(pair / a.top_k) * a.K;
-        }
+    // ---- A: four 16-row tiles per wave, 32 bytes + 2 scale bytes per lane per super-step,
+    // in a ring of four super-steps (loads run three super-steps ahead of their MFMAs)
+    const uint32_t rowA = static_cast<uint32_t>(a.K >> 1);
+    __amdgpu_buffer_rsrc_t ra[2], rsa[2];
+    {
+        const int p0 = DOWN ? 4 : 0;
+        ra[0] = make_rsrc(reinterpret_cast<const void *>(ptr[p0]), static_cast<uint32_t>(a.N) * rowA);
+        rsa[0] = make_rsrc(reinterpret_cast<const void *>(ptr[p0 + 1]), static_cast<uint32_t>(a.N * KB));
+        ra[1] = DOWN ? ra[0] : make_rsrc(reinterpret_cast<const void *>(ptr[2]), static_cast<uint32_t>(a.N) * rowA);
+        rsa[1] = DOWN ? rsa[0] : make_rsrc(reinterpret_cast<const void *>(ptr[3]), static_cast<uint32_t>(a.N * KB));
     }
-    // B: weight row br = tid >> 1 (of 256), 16-byte half bh of the step's 32 bytes
-    const int br = tid >> 1, bh = tid & 1;
-    int wrow;
-    const uint8_t *bp, *bs;
-    if (DOWN) {
-        wrow = nt * kNg + br;
-        bp = reinterpret_cast<const uint8_t *>(ptr[4]);
-        bs = reinterpret_cast<const uint8_t *>(ptr[5]);
-    } else {
-        wrow = nt * (kNg / 2) + (br & 127);
-        bp = reinterpret_cast<const uint8_t *>(ptr[br < 128 ? 0 : 2]);
-        bs = reinterpret_cast<const uint8_t *>(ptr[br < 128 ? 1 : 3]);
-    }
-    const bool b_ok = wrow < a.N;
-    const uint8_t *brow = bp + static_cast<int64_t>(b_ok ? wrow : 0) * rowb + bh * 16;
-    const uint8_t *srow = bs + static_cast<int64_t>(b_ok ? wrow : 0) * KG;
-
-    // three pipeline steps of operands in flight per thread: one step's MFMA work is far
-    // shorter than a memory round trip
-    constexpr int kDepth = 3;
-    uint4 ra[kDepth], rb[kDepth];
-    uint16_t rs[kDepth];
+    uint32_t aoff[4], asoff[4];
 #pragma unroll
-    for (int d = 0; d < kDepth; ++d) {
-        ra[d] = make_uint4(0u, 0u, 0u, 0u);
-        rb[d] = make_uint4(0u, 0u, 0u, 0u);
-        rs[d] = 0;
+    for (int j = 0; j < 4; ++j) {
+        const int row = DOWN ? nt * 256 + wave * 64 + j * 16 + r16 : nt * 128 + wave * 32 + (j & 1) * 16 + r16;
+        const bool ok = row < a.N;
+        aoff[j] = ok ? static_cast<uint32_t>(row) * rowA + 32u * q : kOobOffset;
+        asoff[j] = ok ? static_cast<uint32_t>(row * KB + 2 * q) : kOobOffset;
     }
-    auto load = [&](int ks, uint4 &va, uint4 &vb, uint16_t &vs) {
-        const int k0 = ks * kKs;
-        if (arow) va = *reinterpret_cast<const uint4 *>(arow + k0 + ach * 8);
-        if (b_ok) {
-            vb = *reinterpret_cast<const uint4 *>(brow + (k0 >> 1));
-            if (bh == 0) vs = *reinterpret_cast<const uint16_t *>(srow + (k0 >> 5));
+    constexpr int kRing = 4;
+    uint4 A[kRing][4][2];
+    uint16_t SA[kRing][4];  // widened only where used, so no VALU op waits on the load early
+    // Super-steps past the end load as zeros (block index >= KB), so every step issues the
+    // same loads and the waits stay exact.  Invalid offsets keep bit 31 set (every valid
+    // offset is below 2^31), OR-ed in without branches.
+    auto load_a = [&](int S, int slot) {
+        const uint32_t oob = S * 8 + 2 * q < KB ? 0u : kOobOffset;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const uint32_t off = (aoff[j] + S * 128u) | oob;
+            A[slot][j][0] = buf_load16(ra[j >> 1], off);
+            A[slot][j][1] = buf_load16(ra[j >> 1], off + 16u);
+            SA[slot][j] = __builtin_amdgcn_raw_buffer_load_b16(rsa[j >> 1], (asoff[j] + S * 8u) | oob, 0, 0);
         }
     };
-    auto store = [&](int buf, const uint4 &va, const uint4 &vb, uint16_t vs) {
-        if (a_thread) *reinterpret_cast<uint4 *>(&a_s[buf][aplane][ar * kARow + ach * 8]) = va;
-        uint32_t *bd = &b_s[buf][br * kBRow + bh * 4];
-        bd[0] = vb.x;
-        bd[1] = vb.y;
-        bd[2] = vb.z;
-        bd[3] = vb.w;
-        if (bh == 0) sc_s[buf][br] = vs;
+
+    // ---- B staging: thread (column c = tid & 15, piece p = tid >> 4) copies piece p of the
+    // four tile rows c, 16 + c, 32 + c, 48 + c, every term; (c, block pair g = (tid >> 4) & 3,
+    // tile tid >> 6) copies one scale pair per term.  Two register sets: loads run two
+    // super-steps ahead of their LDS stores.
+    const auto rb = make_rsrc(a.b8, a.b_term * TERMS);
+    const auto rbs = make_rsrc(a.bs, a.bs_term * TERMS);
+    const int sc_c = tid & 15, sp = tid >> 4;
+    const int sp_bb = 4 * ((sp >> 2) & 1) + 2 * ((sp & 3) >> 1) + (sp >> 3);  // block of piece sp
+    uint32_t boff[4];
+#pragma unroll
+    for (int ct = 0; ct < 4; ++ct) {
+        const int rr = ct * 16 + sc_c;
+        int brow = -1;
+        if (rr < rows) brow = DOWN ? pos0 + rr : a.perm[pos0 + rr] / a.top_k;
+        boff[ct] = brow >= 0 ? static_cast<uint32_t>(brow) * a.Kpad + sp * 16u : kOobOffset;
+    }
+    const int sg = sp & 3, sct = tid >> 6;
+    uint32_t bsoff;
+    {
+        const int rr = sct * 16 + sc_c;
+        int brow = -1;
+        if (rr < rows) brow = DOWN ? pos0 + rr : a.perm[pos0 + rr] / a.top_k;
+        bsoff = brow >= 0 ? static_cast<uint32_t>(brow) * (a.Kpad >> 5) + 2u * sg : kOobOffset;
+    }
+    // gate/up stages x two super-steps ahead (gathered token rows); down, whose act terms
+    // were written just before and sit in cache, one step ahead, to stay in registers
+    constexpr int XD = DOWN ? 1 : 2;
+    uint4 XR[XD][4][TERMS];
+    uint16_t XS[XD][TERMS];
+    auto load_x = [&](int S, int xs) {
+        const uint32_t poob = S >= 0 && S * 8 + sp_bb < KB ? 0u : kOobOffset;
+        const uint32_t soob = S >= 0 && S * 8 + 2 * sg < KB ? 0u : kOobOffset;
+#pragma unroll
+        for (int ct = 0; ct < 4; ++ct)
+#pragma unroll
+            for (int t = 0; t < TERMS; ++t)
+                XR[xs][ct][t] = buf_load16(rb, (boff[ct] + t * a.b_term + S * kSS) | poob);
+#pragma unroll
+        for (int t = 0; t < TERMS; ++t)
+            XS[xs][t] = __builtin_amdgcn_raw_buffer_load_b16(rbs, (bsoff + t * a.bs_term + S * 8u) | soob, 0, 0);
+    };
+    auto store_x = [&](int xs, int buf) {
+        uint4 *xt = smem + buf * kXT;
+        uint16_t *st = ssm + buf * kST;
+#pragma unroll
+        for (int ct = 0; ct < 4; ++ct)
+#pragma unroll
+            for (int t = 0; t < TERMS; ++t) xt[((ct * TERMS + t) * 16 + sp) * 16 + sc_c] = XR[xs][ct][t];
+#pragma unroll
+        for (int t = 0; t < TERMS; ++t) st[((sct * TERMS + t) * 16 + sc_c) * 4 + sg] = XS[xs][t];
     };
 
-    f32x4_t acc[2][2];  // [token tile][weight-row tile]
+    f32x4 acc[4][4];  // [A tile j][B tile ct]
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+    for (int j = 0; j < 4; ++j)
 #pragma unroll
-        for (int j = 0; j < 2; ++j) acc[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+        for (int ct = 0; ct < 4; ++ct) acc[j][ct] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-    const int r16 = lane & 15, q4 = lane >> 4;
-    const int nsteps = a.K / kKs;
-    auto step = [&](int ks, int d) {
-        const int buf = ks & 1;
-        store(buf, ra[d], rb[d], rs[d]);
-        __syncthreads();
-        if (ks + kDepth < nsteps) load(ks + kDepth, ra[d], rb[d], rs[d]);
+    // MFMAs of one super-step.  B fragments are read from LDS one 16-column tile ahead of
+    // their MFMAs, two sets live; the scheduling fences keep the compiler from hoisting all
+    // four tiles' fragments at once (which costs ~128 registers and forces reuse of
+    // registers whose loads are still in flight).
+    auto compute = [&](int slot, int buf) {
+        const uint4 *xt = smem + buf * kXT;
+        const uint16_t *st = ssm + buf * kST;
 #pragma unroll
-        for (int sub = 0; sub < 2; ++sub) {
-            bf16x8 bop[2];
+        for (int ct = 0; ct < 4; ++ct) {
+            if (ct < nct) {
 #pragma unroll
-            for (int j = 0; j < 2; ++j) {
-                const int row = wave * 32 + j * 16 + r16;
-                const uint32_t pk = b_s[buf][row * kBRow + sub * 4 + q4];
-                const uint32_t sb = (sc_s[buf][row] >> (8 * sub)) & 0xffu;
-                bop[j] = decode8(pk, e8m0_to_f32(sb));
-            }
+                for (int t = 0; t < TERMS; ++t) {
+                    const uint4 *xb = xt + (ct * TERMS + t) * 256;
+                    const uint32_t sb = st[((ct * TERMS + t) * 16 + r16) * 4 + q];
+                    const uint4 b00 = xb[0 * 64 + lane], b01 = xb[1 * 64 + lane];
+                    const uint4 b10 = xb[2 * 64 + lane], b11 = xb[3 * 64 + lane];
 #pragma unroll
-            for (int i = 0; i < 2; ++i) {
+                    for (int j = 0; j < 4; ++j)
+                        acc[j][ct] = mfma_fp4_fp8<0>(A[slot][j][0], b00, b01, acc[j][ct], SA[slot][j], sb);
 #pragma unroll
-                for (int pl = 0; pl < AH; ++pl) {
-                    const bf16x8 aop =
-                        *reinterpret_cast<const bf16x8 *>(&a_s[buf][pl][(i * 16 + r16) * kARow + sub * 32 + q4 * 8]);
-#pragma unroll
-                    for (int j = 0; j < 2; ++j) acc[i][j] = mfma_bf16(aop, bop[j], acc[i][j]);
+                    for (int j = 0; j < 4; ++j)
+                        acc[j][ct] = mfma_fp4_fp8<1>(A[slot][j][1], b10, b11, acc[j][ct], SA[slot][j], sb);
                 }
             }
         }
     };
+    // Super-step S: MFMAs on LDS tile S % 2 and A slot S % 4; then A(S + 4) into the freed
+    // slot, B(S + 1) from registers into the other LDS tile, B(S + 1 + XD) into the freed
+    // registers.  The loop starts at S = -4 with the MFMAs skipped, so the pipeline fills
+    // through the same instruction stream as the steady state (a separate prologue leaves
+    // the loop entry with a different set of loads in flight, and the compiler's waits at the
+    // loop head then cover the worse of the two).
+    auto step = [&](int S, int slot, int par) {
+        __syncthreads();  // tile S is stored and every wave is done with tile S - 1
+        if (S >= 0) compute(slot, par);
+        load_a(S + kRing, slot);
+        store_x((par ^ 1) % XD, par ^ 1);
+        load_x(S + 1 + XD, (par ^ 1) % XD);
+    };
 #pragma unroll
-    for (int d = 0; d < kDepth; ++d)
-        if (d < nsteps) load(d, ra[d], rb[d], rs[d]);
-    for (int ks = 0; ks < nsteps; ks += kDepth) {
-        step(ks, 0);
-        if (ks + 1 < nsteps) step(ks + 1, 1);
-        if (ks + 2 < nsteps) step(ks + 2, 2);
+    for (int xs = 0; xs < XD; ++xs) {
+#pragma unroll
+        for (int ct = 0; ct < 4; ++ct)
+#pragma unroll
+            for (int t = 0; t < TERMS; ++t) XR[xs][ct][t] = make_uint4(0u, 0u, 0u, 0u);
+#pragma unroll
+        for (int t = 0; t < TERMS; ++t) XS[xs][t] = 0;
+    }
+    // Unrolled over the four ring slots, so slot and LDS-tile indices are compile-time.
+    static_assert(kRing == 4, "the loop below is unrolled over the four ring slots");
+    for (int S = -kRing; S < NS; S += 4) {
+        step(S, 0, 0);
+        if (S + 1 < NS) step(S + 1, 1, 1);
+        if (S + 2 < NS) step(S + 2, 2, 0);
+        if (S + 3 < NS) step(S + 3, 3, 1);
     }
 
-    // ---- epilogues.  C layout: lane holds tokens 16 i + 4 q4 + v (v < 4), weight row 16 j + r16
+    // ---- epilogues (C: lane holds weight rows 4q + v of each A tile, column r16 of each B tile)
     if constexpr (DOWN) {
 #pragma unroll
-        for (int i = 0; i < 2; ++i)
+        for (int ct = 0; ct < 4; ++ct) {
+            const int rr = ct * 16 + r16;
+            if (ct < nct && rr < rows) {
+                const int pair = a.perm[pos0 + rr];
+                float *yrow = a.ypair + static_cast<int64_t>(pair) * a.N;
 #pragma unroll
-            for (int v = 0; v < 4; ++v) {
-                const int r = i * 16 + q4 * 4 + v;
-                if (r < rows) {
-                    const int pair = a.perm[pos0 + r];
-                    float *yrow = a.ypair + static_cast<int64_t>(pair) * a.N + nt * kNg + wave * 32;
-#pragma unroll
-                    for (int j = 0; j < 2; ++j)
-                        if (nt * kNg + wave * 32 + j * 16 + r16 < a.N) yrow[j * 16 + r16] = acc[i][j][v];
+                for (int j = 0; j < 4; ++j) {
+                    const int row = nt * 256 + wave * 64 + j * 16 + 4 * q;
+                    if (row < a.N) *reinterpret_cast<float4 *>(yrow + row) = __builtin_bit_cast(float4, acc[j][ct]);
                 }
             }
+        }
     } else {
-        __syncthreads();
-        if (wave < 4) {  // gate rows: publish to LDS
+        const int ib = nt * 128 + wave * 32;  // the wave's intermediate block
+        if (ib < a.N) {
+            const int blk = ib >> 5;
+            const uint32_t pbase = mxb_offset(blk, 0) + 4u * q;  // half 0; half 1 is 16 bytes on
 #pragma unroll
-            for (int i = 0; i < 2; ++i)
-#pragma unroll
-                for (int v = 0; v < 4; ++v)
+            for (int ct = 0; ct < 4; ++ct) {
+                if (ct < nct) {
+                    const int rr = ct * 16 + r16;
+                    const bool ok = rr < rows;
+                    float v[2][4];
+                    float amax = 0.f;
 #pragma unroll
                     for (int j = 0; j < 2; ++j)
-                        g_s[(i * 16 + q4 * 4 + v) * 129 + wave * 32 + j * 16 + r16] = acc[i][j][v];
-        }
-        __syncthreads();
-        if (wave >= 4) {  // up rows: combine with the gate of the same intermediate index
-            const int wl = wave - 4;
 #pragma unroll
-            for (int i = 0; i < 2; ++i)
+                        for (int i = 0; i < 4; ++i) {
+                            v[j][i] = act_fn(acc[j][ct][i], acc[j + 2][ct][i], a.act_kind, a.beta, a.lbeta);
+                            amax = fmaxf(amax, fabsf(v[j][i]));
+                        }
+                    const uint32_t pos = static_cast<uint32_t>(pos0 + rr);
 #pragma unroll
-                for (int v = 0; v < 4; ++v) {
-                    const int r = i * 16 + q4 * 4 + v;
-                    if (r >= rows) continue;
+                    for (int tt = 0; tt < 3; ++tt) {
+                        amax = fmaxf(amax, shfl_xor_f(amax, 16));
+                        amax = fmaxf(amax, shfl_xor_f(amax, 32));
+                        const int ex = block_exp(amax);
+                        uint32_t c[2] = {0u, 0u};
+                        amax = 0.f;
 #pragma unroll
-                    for (int j = 0; j < 2; ++j) {
-                        const int il = wl * 32 + j * 16 + r16;
-                        const int ii = nt * (kNg / 2) + il;
-                        if (ii < a.N) {
-                            const float act = act_fn(g_s[r * 129 + il], acc[i][j][v], a.act_kind, a.beta, a.lbeta);
-                            const uint16_t hi = f32_to_bf16(act);
-                            const int64_t o = static_cast<int64_t>(pos0 + r) * a.N + ii;
-                            a.act_hi[o] = hi;
-                            a.act_lo[o] = f32_to_bf16(act - bf16_to_f32(hi));
+                        for (int j = 0; j < 2; ++j)
+#pragma unroll
+                            for (int i = 0; i < 4; ++i) {
+                                float qv;
+                                c[j] |= e4m3_rne(ldexpf(v[j][i], -ex), qv) << (8 * i);
+                                v[j][i] -= ldexpf(qv, ex);
+                                amax = fmaxf(amax, fabsf(v[j][i]));
+                            }
+                        if (ok) {
+                            uint8_t *dst = a.a8 + tt * a.a_term + pos * static_cast<uint32_t>(a.Ipad) + pbase;
+                            *reinterpret_cast<uint32_t *>(dst) = c[0];
+                            *reinterpret_cast<uint32_t *>(dst + 16) = c[1];
+                            if (q == 0)
+                                a.as[tt * a.as_term + pos * static_cast<uint32_t>(a.Ipad >> 5) + blk] =
+                                    static_cast<uint8_t>(ex + 127);
                         }
                     }
                 }
+            }
         }
     }
+}
+
+// LDS of mx_gemm_kernel: two B tiles and their scale pairs
+constexpr size_t mx_lds_bytes(int terms) {
+    return 2 * (static_cast<size_t>(4 * terms * 16 * 16) * 16 + static_cast<size_t>(4 * terms * 16 * 4) * 2);
+}
+
+// Both GEMMs take more than the default 64 KB of dynamic LDS (gfx950 has 160 KB per CU).
+int mx_prepare() {
+    static const hipError_t rc = [] {
+        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(&mx_gemm_kernel<false>),
+                                           hipFuncAttributeMaxDynamicSharedMemorySize,
+                                           static_cast<int>(mx_lds_bytes(2)));
+        if (e == hipSuccess)
+            e = hipFuncSetAttribute(reinterpret_cast<const void *>(&mx_gemm_kernel<true>),
+                                    hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(mx_lds_bytes(3)));
+        return e;
+    }();
+    return check_hip(rc, "moe grouped: LDS size attribute");
 }
 
 // ------------------------------------------------------------------ combine
@@ -355,15 +548,18 @@ __global__ __launch_bounds__(256) void combine_kernel(CombineArgs a) {
 
 // ------------------------------------------------------------------ host side
 struct GroupedWs {
-    size_t counts, base, perm, tile_e, tile_m0, n_tiles, act_hi, act_lo, ypair, total;
+    size_t counts, base, perm, tile_e, tile_m0, n_tiles, x8, xs, a8, as, ypair, total;
     int max_tiles;
+    int64_t Hpad, Ipad;
 };
 
 GroupedWs grouped_ws_layout(int64_t T, int64_t k, int64_t E, int64_t H, int64_t I) {
     GroupedWs L{};
     auto up = [](size_t v) { return (v + 255) & ~size_t(255); };
     const int64_t P = T * k;
-    L.max_tiles = static_cast<int>(cdiv(P, kMt) + E);
+    L.Hpad = cdiv(H, kSS) * kSS;
+    L.Ipad = cdiv(I, kSS) * kSS;
+    L.max_tiles = static_cast<int>(cdiv(P, kTM) + E);
     size_t o = 0;
     L.counts = o, o += up(E * 4);
     L.base = o, o += up(E * 4);
@@ -371,8 +567,10 @@ GroupedWs grouped_ws_layout(int64_t T, int64_t k, int64_t E, int64_t H, int64_t 
     L.tile_e = o, o += up(static_cast<size_t>(L.max_tiles) * 4);
     L.tile_m0 = o, o += up(static_cast<size_t>(L.max_tiles) * 4);
     L.n_tiles = o, o += up(4);
-    L.act_hi = o, o += up(static_cast<size_t>(P) * I * 2);
-    L.act_lo = o, o += up(static_cast<size_t>(P) * I * 2);
+    L.x8 = o, o += up(static_cast<size_t>(2) * T * L.Hpad);
+    L.xs = o, o += up(static_cast<size_t>(2) * T * (L.Hpad / 32));
+    L.a8 = o, o += up(static_cast<size_t>(3) * P * L.Ipad);
+    L.as = o, o += up(static_cast<size_t>(3) * P * (L.Ipad / 32));
     L.ypair = o, o += up(static_cast<size_t>(P) * H * 4);
     L.total = o;
     return L;
@@ -399,12 +597,14 @@ extern "C" int k3_moe_grouped_ffn(const void *x, int x_dtype, const int32_t *exp
     if (act_kind != K3_ACT_SILU && act_kind != K3_ACT_SITU) return set_error(K3_ERR_SHAPE, "moe grouped: act_kind");
     if (T <= 0 || top_k <= 0 || top_k > 64 || n_experts <= 0 || n_experts > 1024)
         return set_error(K3_ERR_SHAPE, "moe grouped: T >= 1, 1 <= top_k <= 64, 1 <= n_experts <= 1024 required");
-    if (H <= 0 || I <= 0 || H % kKs || I % kKs || H % 4)
-        return set_error(K3_ERR_SHAPE, "moe grouped: H=%lld and I=%lld must be positive multiples of %d",
-                         (long long)H, (long long)I, kKs);
-    if (T * top_k >= (1ll << 30) || H * I / 2 >= (1ll << 31))
-        return set_error(K3_ERR_SHAPE, "moe grouped: problem too large");
+    if (H <= 0 || I <= 0 || H % 64 || I % 64)
+        return set_error(K3_ERR_SHAPE, "moe grouped: H=%lld and I=%lld must be positive multiples of 64",
+                         (long long)H, (long long)I);
     const GroupedWs L = grouped_ws_layout(T, top_k, n_experts, H, I);
+    const int64_t P = T * top_k;
+    if (P >= (1ll << 30) || H * I / 2 >= (1ll << 31) || 3 * P * L.Ipad >= (1ll << 31) ||
+        2 * T * L.Hpad >= (1ll << 31))
+        return set_error(K3_ERR_SHAPE, "moe grouped: problem too large");
     if (workspace_bytes < static_cast<int64_t>(L.total))
         return set_error(K3_ERR_WORKSPACE, "moe grouped: workspace %lld < %zu bytes", (long long)workspace_bytes,
                          L.total);
@@ -412,11 +612,10 @@ extern "C" int k3_moe_grouped_ffn(const void *x, int x_dtype, const int32_t *exp
         return set_error(K3_ERR_ALIGN, "moe grouped: x, out and workspace must be 16-byte aligned");
     auto st = static_cast<hipStream_t>(stream);
     char *ws = static_cast<char *>(workspace);
-    const int P = static_cast<int>(T * top_k);
 
     GroupArgs g{};
     g.idx = expert_idx;
-    g.P = P;
+    g.P = static_cast<int>(P);
     g.E = static_cast<int>(n_experts);
     g.counts = reinterpret_cast<int32_t *>(ws + L.counts);
     g.base = reinterpret_cast<int32_t *>(ws + L.base);
@@ -431,41 +630,65 @@ extern "C" int k3_moe_grouped_ffn(const void *x, int x_dtype, const int32_t *exp
     int rc = check_hip(hipGetLastError(), "moe grouped: grouping launches");
     if (rc) return rc;
 
-    GemmArgs ga{};
-    ga.x = static_cast<const uint16_t *>(x);
-    ga.table = static_cast<const uint64_t *>(expert_table);
-    ga.counts = g.counts;
-    ga.base = g.base;
-    ga.perm = g.perm;
-    ga.tile_e = g.tile_e;
-    ga.tile_m0 = g.tile_m0;
-    ga.n_tiles = g.n_tiles;
-    ga.act_hi = reinterpret_cast<uint16_t *>(ws + L.act_hi);
-    ga.act_lo = reinterpret_cast<uint16_t *>(ws + L.act_lo);
-    ga.ypair = reinterpret_cast<float *>(ws + L.ypair);
-    ga.top_k = static_cast<int>(top_k);
-    ga.max_tiles = L.max_tiles;
-    ga.act_kind = act_kind;
-    ga.beta = beta;
-    ga.lbeta = linear_beta;
+    QxArgs qa{};
+    qa.x = static_cast<const uint16_t *>(x);
+    qa.x8 = reinterpret_cast<uint8_t *>(ws + L.x8);
+    qa.xs = reinterpret_cast<uint8_t *>(ws + L.xs);
+    qa.T = static_cast<int>(T);
+    qa.H = static_cast<int>(H);
+    qa.Hpad = static_cast<int>(L.Hpad);
+    qa.term = static_cast<uint32_t>(T * L.Hpad);
+    qa.sterm = static_cast<uint32_t>(T * (L.Hpad / 32));
+    quant_x_kernel<<<dim3(static_cast<unsigned>(cdiv(T * (H / 16), 256))), 256, 0, st>>>(qa);
+    rc = check_hip(hipGetLastError(), "moe grouped: x quantization launch");
+    if (rc) return rc;
+
+    rc = mx_prepare();
+    if (rc) return rc;
+    MxArgs ma{};
+    ma.table = static_cast<const uint64_t *>(expert_table);
+    ma.counts = g.counts;
+    ma.base = g.base;
+    ma.perm = g.perm;
+    ma.tile_e = g.tile_e;
+    ma.tile_m0 = g.tile_m0;
+    ma.n_tiles = g.n_tiles;
+    ma.a8 = reinterpret_cast<uint8_t *>(ws + L.a8);
+    ma.as = reinterpret_cast<uint8_t *>(ws + L.as);
+    ma.a_term = static_cast<uint32_t>(P * L.Ipad);
+    ma.as_term = static_cast<uint32_t>(P * (L.Ipad / 32));
+    ma.Ipad = static_cast<int>(L.Ipad);
+    ma.ypair = reinterpret_cast<float *>(ws + L.ypair);
+    ma.top_k = static_cast<int>(top_k);
+    ma.max_tiles = L.max_tiles;
+    ma.act_kind = act_kind;
+    ma.beta = beta;
+    ma.lbeta = linear_beta;
     // gate/up: K = H, weight rows N = I, 128 intermediate indices per block
-    ga.K = static_cast<int>(H);
-    ga.N = static_cast<int>(I);
-    ga.nt_per_tile = static_cast<int>(cdiv(I, kNg / 2));
-    grouped_gemm_kernel<false><<<dim3(static_cast<unsigned>(L.max_tiles * ga.nt_per_tile)), kThreads, 0, st>>>(ga);
+    ma.b8 = qa.x8;
+    ma.bs = qa.xs;
+    ma.b_term = qa.term;
+    ma.bs_term = qa.sterm;
+    ma.K = static_cast<int>(H);
+    ma.Kpad = static_cast<int>(L.Hpad);
+    ma.N = static_cast<int>(I);
+    mx_gemm_kernel<false>
+        <<<dim3(static_cast<unsigned>(L.max_tiles * cdiv(I, 128))), kThreads, mx_lds_bytes(2), st>>>(ma);
     rc = check_hip(hipGetLastError(), "moe grouped: gate/up launch");
     if (rc) return rc;
-    // down: K = I, weight rows N = H, 256 output rows per block
-    ga.a_hi = ga.act_hi;
-    ga.a_lo = ga.act_lo;
-    ga.K = static_cast<int>(I);
-    ga.N = static_cast<int>(H);
-    ga.nt_per_tile = static_cast<int>(cdiv(H, kNg));
-    grouped_gemm_kernel<true><<<dim3(static_cast<unsigned>(L.max_tiles * ga.nt_per_tile)), kThreads, 0, st>>>(ga);
+    // down: K = I, weight rows N = H, 256 output rows per block, B = the act terms
+    ma.b8 = ma.a8;
+    ma.bs = ma.as;
+    ma.b_term = ma.a_term;
+    ma.bs_term = ma.as_term;
+    ma.K = static_cast<int>(I);
+    ma.Kpad = static_cast<int>(L.Ipad);
+    ma.N = static_cast<int>(H);
+    mx_gemm_kernel<true><<<dim3(static_cast<unsigned>(L.max_tiles * cdiv(H, 256))), kThreads, mx_lds_bytes(3), st>>>(ma);
     rc = check_hip(hipGetLastError(), "moe grouped: down launch");
     if (rc) return rc;
 
-    CombineArgs ca{ga.ypair, expert_w, out, static_cast<int>(T), static_cast<int>(H), static_cast<int>(top_k),
+    CombineArgs ca{ma.ypair, expert_w, out, static_cast<int>(T), static_cast<int>(H), static_cast<int>(top_k),
                    out_dtype == K3_BF16};
     combine_kernel<<<dim3(static_cast<unsigned>(T), static_cast<unsigned>(cdiv(H, 1024))), 256, 0, st>>>(ca);
     return check_hip(hipGetLastError(), "moe grouped: combine launch");

@@ -1,7 +1,10 @@
 """GPU parity of the grouped (prefill) routed-expert path against the fp64 oracle.
 
-Tolerance: normwise max-relative error <= 1e-3 (the matvec gate); the bf16 MFMA path with
-exact weight decode and hi/lo-split activations is expected near 1e-5.
+Tolerance: normwise max-relative error <= 1e-3 (the matvec gate).  The grouped path runs
+v_mfma_scale_f32_16x16x128_f8f6f4 on the MXFP4 weights as stored, with x split into two
+E4M3 terms (exact for bf16 x) and the activation into three (about 12 bits); the MFMA sums
+each 128-element dot about 12 bits below its largest product (unbiased, measured), so the
+path is expected within 5e-4 (observed 2.5e-5 .. 1.4e-4 on these cases).
 """
 from __future__ import annotations
 
@@ -15,6 +18,7 @@ from oracle import mxfp4 as om
 pytestmark = pytest.mark.gpu
 DEV = "cuda"
 TOL = 1e-3
+PATH_TOL = 5e-4  # expected level of the scaled-MFMA path (module docstring)
 
 
 def make_experts(rng, D, H, I):
@@ -90,7 +94,7 @@ def test_grouped_matches_oracle(T, H, I, E, k, D, routing, act):
     rel = om.normwise_rel(got, want)
     print(f"T={T} H={H} I={I} E={E} k={k} rel={rel:.3e}")
     assert rel <= TOL
-    assert rel <= 1e-4, f"hi/lo MFMA path should be near fp32: {rel:.3e}"
+    assert rel <= PATH_TOL, f"scaled-MFMA path above its expected error level: {rel:.3e}"
 
 
 def test_grouped_full_shape_sampled_tokens_and_determinism():
