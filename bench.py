@@ -4,11 +4,12 @@
 
 One JSON line on stdout.  The headline workload is one SwiGLU expert at batch 1
 (hidden 7168, intermediate 2048, MXFP4 weights with E8M0 scales in [118, 130], bf16 x):
-a step is one expert FFN launch on a different resident expert (64 experts rotate, 1.5 GB,
-so the 256 MB MALL cannot serve the weights).  `value` is algorithmic weight bytes per
-second over the K timed steps.  The same line carries the MoE-layer figure (384 resident
-experts, top-8 softmax routing, one bf16 shared expert, a fresh token per step), the
-single-projection GEMV figure, the roofline of the dominant kernel and a CPU baseline
+a step is one expert FFN (a gate/up + activation launch, then the down GEMV) on a different
+resident expert (64 experts rotate, 1.5 GB, so the 256 MB MALL cannot serve the weights).
+`value` is algorithmic weight bytes per second over the K timed steps.  The same line
+carries the MoE-layer figure (384 resident experts, top-8 softmax routing, one bf16 shared
+expert, a fresh token per step), the grouped-prefill, single-projection GEMV and MLA decode
+figures, the roofline of the expert step (its two launches) and a CPU baseline
 (torch-CPU restatement of the k3ref path timed on a bounded sample on this host).
 
 Synthetic, seeded data; weights are random-init with the benchmark shapes.  Steps are
@@ -307,11 +308,11 @@ def bench_cpu(sample_s=12.0):
 
 
 def traffic_from_profiles():
-    """HBM bytes per expert launch from the committed rocprofv3 --pmc summary, if any."""
+    """HBM bytes per expert step (both launches) from the committed rocprofv3 --pmc summary."""
     f = ROOT / "profiles" / "expert_ffn_b1_traffic.json"
     if f.exists():
         try:
-            return json.loads(f.read_text()).get("bytes_per_launch")
+            return json.loads(f.read_text()).get("bytes_per_step")
         except (ValueError, OSError):
             return None
     return None
@@ -366,8 +367,9 @@ def main():
         "pct_hbm_peak": round(100 * gbs / HBM_PEAK_GBS, 1),
         "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": traffic_from_profiles(),
-                     "kernel": "expert_ffn_kernel", "bytes_per_launch": EXPERT_BYTES,
-                     "avg_launch_us": round(per_step * 1e6, 3)},
+                     "kernel": "expert FFN step: expert_gateup_kernel then gemv_kernel (down)",
+                     "launches_per_step": 2, "bytes_per_step": EXPERT_BYTES,
+                     "avg_step_us": round(per_step * 1e6, 3)},
         "wall_s": round(wall, 4),
     }
     if "layer" in work:

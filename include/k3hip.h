@@ -138,8 +138,9 @@ int k3_moe_layer_decode(const void *x, int x_dtype, const void *router_w, const 
 
 /* ---- grouped routed experts for many tokens (prefill) ------------------------------------ */
 
-/* Workspace bytes k3_moe_grouped_ffn needs (grouping records, the bf16 hi/lo activations of
- * every routed pair, fp32 per-pair expert outputs).  No initialisation. */
+/* Workspace bytes k3_moe_grouped_ffn needs (grouping records, the E4M3 terms of x and of the
+ * activations of every routed pair with their E8M0 scales, fp32 per-pair expert outputs).
+ * No initialisation. */
 int64_t k3_moe_grouped_workspace_size(int64_t T, int64_t top_k, int64_t n_experts, int64_t H, int64_t I);
 
 /* y[t] = sum_j w[t, j] * expert_{idx[t, j]}(x[t]) for T tokens at once:
@@ -147,8 +148,10 @@ int64_t k3_moe_grouped_workspace_size(int64_t T, int64_t top_k, int64_t n_expert
  *   [T, top_k]; expert_table as in k3_moe_layer_decode (packed pointers 16-byte aligned,
  *   scale pointers 2-byte aligned, E8M0 bytes 2..252); out [T, H] f32 or bf16.
  * The (token, slot) pairs are grouped by expert on the device and each expert runs as a
- * bf16-MFMA GEMM with M = its token count (weights decoded exactly in registers), so each
- * expert's weights are read once per 32-token tile group.  Deterministic.  H and I must be
+ * GEMM with M = its token count on native MXFP4 MFMA (v_mfma_scale_f32_16x16x128_f8f6f4:
+ * the weights as stored, x as two E4M3 terms, the activation as three, all with E8M0
+ * scales per 32), so each expert's weights are read once per 64-token tile.  Normwise error
+ * about 1e-4 of fp64 (the MFMA's own accumulation).  Deterministic.  H and I must be
  * multiples of 64.
  * Replaces the per-expert dispatch loop of LatentMoE.__call__
  * (air_llm/models/kimi_k3/moe.py:110-132; k3ref/layers.py:241-261) for prefill. */
