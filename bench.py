@@ -104,6 +104,29 @@ def graph_time(torch, fn, steps, warmup):
     return e0.elapsed_time(e1) / 1e3, wall
 
 
+def step_stats(torch, fn, chunk=64, reps=16):
+    """Per-step time distribution: a graph of `chunk` calls (a whole expert / cache rotation)
+    replayed `reps` times, HIP events around each replay.  Returns {median, p10, p90} in us
+    of the per-step mean of each replay."""
+    import numpy as np
+    stream = torch.cuda.current_stream()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for i in range(chunk):
+            fn(i)
+    g.replay()
+    torch.cuda.synchronize()
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(reps + 1)]
+    ev[0].record(stream)
+    for r in range(reps):
+        g.replay()
+        ev[r + 1].record(stream)
+    torch.cuda.synchronize()
+    us = np.array([ev[r].elapsed_time(ev[r + 1]) * 1e3 / chunk for r in range(reps)])
+    return {"median": round(float(np.median(us)), 3), "p10": round(float(np.percentile(us, 10)), 3),
+            "p90": round(float(np.percentile(us, 90)), 3), "replays": reps, "steps_per_replay": chunk}
+
+
 # --------------------------------------------------------------------- workloads
 
 def bench_expert(torch, steps, warmup, dev):
@@ -119,8 +142,9 @@ def bench_expert(torch, steps, warmup, dev):
         outs[i & 1] = expert_ffn_fused(x, *experts[i % ROTATE])
 
     sec, wall = graph_time(torch, step, steps, warmup)
+    stats = None if EAGER else step_stats(torch, step, ROTATE)
     del experts
-    return sec, wall
+    return sec, wall, stats
 
 
 def bench_gemv(torch, steps, warmup, dev):
@@ -134,7 +158,7 @@ def bench_gemv(torch, steps, warmup, dev):
         mxfp4_matvec_fused(x, *ws[i % ROTATE], out_dtype=torch.bfloat16)
 
     sec, _ = graph_time(torch, step, steps, warmup)
-    return sec
+    return sec, None if EAGER else step_stats(torch, step, ROTATE)
 
 
 _EXPERTS = []
@@ -177,11 +201,12 @@ def bench_layer(torch, steps, warmup, dev):
         moe(xs[i:i + 1])
 
     sec, _ = graph_time(torch, step, steps, warmup)
+    stats = None if EAGER else step_stats(torch, step, min(64, steps))
     # distinct experts the timed tokens routed to (evidence the MALL could not hold them)
     for i in range(min(steps, 32)):
         touched.update(moe.route(xs[i:i + 1]).expert_indices.view(-1).tolist())
     del moe
-    return sec, len(touched)
+    return sec, len(touched), stats
 
 
 PF_T, PF_K = 2048, 8
@@ -254,8 +279,9 @@ def bench_mla(torch, steps, warmup, dev):
         mla_decode_absorbed(q_nope, q_rot, wk, wv, lat, rot, scale)
 
     sec, _ = graph_time(torch, step, steps, warmup)
+    stats = None if EAGER else step_stats(torch, step, 32)
     del caches, weights
-    return sec
+    return sec, stats
 
 
 def bench_read_ceiling(torch, nbytes, steps, dev):
@@ -346,7 +372,7 @@ def main():
     work = set(args.workloads.split(","))
     K, W = args.steps, args.warmup
 
-    sec, wall = bench_expert(torch, K, W, dev)
+    sec, wall, estats = bench_expert(torch, K, W, dev)
     per_step = sec / K
     gbs = EXPERT_BYTES / per_step / 1e9
     line = {
@@ -371,35 +397,37 @@ def main():
                      "launches_per_step": 2, "bytes_per_step": EXPERT_BYTES,
                      "avg_step_us": round(per_step * 1e6, 3)},
         "wall_s": round(wall, 4),
+        "step_us": estats,
     }
     if "layer" in work:
-        lsec, touched = bench_layer(torch, min(K, 256), min(W, 32), dev)
+        lsec, touched, lstats = bench_layer(torch, min(K, 256), min(W, 32), dev)
         lus = lsec / min(K, 256) * 1e6
         lgbs = LAYER_BYTES / (lus * 1e-6) / 1e9
         line["moe_layer"] = {"us_per_layer": round(lus, 2), "GB/s": round(lgbs, 1),
                              "pct_hbm_peak": round(100 * lgbs / HBM_PEAK_GBS, 1),
                              "bytes_per_layer": LAYER_BYTES, "experts": E_LAYER, "top_k": TOPK,
                              "shared_expert": "bf16", "distinct_experts_routed_first32": touched,
-                             "launches_per_layer": 3}
+                             "launches_per_layer": 3, "step_us": lstats}
     if "prefill" in work:
         pst, pbytes, counts = bench_prefill(torch, 8, 2, dev)
         line["moe_prefill"] = {
             "ms": round(pst * 1e3, 3), "GB/s": round(pbytes / pst / 1e9, 1),
             "pct_hbm_peak": round(100 * pbytes / pst / 1e9 / HBM_PEAK_GBS, 1), "bytes": pbytes,
             "useful_TFLOP/s": round(PF_FLOPS / pst / 1e12, 1),
-            "pct_bf16_mfma_peak": round(100 * PF_FLOPS / pst / 2.5e15, 1),
+            "mfma": "v_mfma_scale_f32_16x16x128_f8f6f4 (MXFP4 x E4M3 terms; issues at the FP8 rate)",
+            "pct_fp8_mfma_peak": round(100 * PF_FLOPS / pst / 5.0e15, 1),
             "tokens": PF_T, "top_k": PF_K, "experts": E_LAYER, "routing": "zipf(1.1), seeded",
             "expert_load": {"max": int(counts.max()), "mean": round(float(counts.mean()), 1),
                             "empty": int((counts == 0).sum())}}
     if "mla" in work:
         ms = min(K, 256)
-        msec = bench_mla(torch, ms, min(W, 32), dev)
+        msec, mstats = bench_mla(torch, ms, min(W, 32), dev)
         mus = msec / ms * 1e6
         mgbs = MLA_BYTES / (mus * 1e-6) / 1e9
         line["mla_decode"] = {"us": round(mus, 2), "GB/s": round(mgbs, 1),
                               "pct_hbm_peak": round(100 * mgbs / HBM_PEAK_GBS, 1), "bytes": MLA_BYTES,
                               "heads": MLA_H, "tokens": MLA_T, "kv_lora_rank": 512, "rope": 64,
-                              "cache": "bf16", "launches": 4}
+                              "cache": "bf16", "launches": 4, "step_us": mstats}
     if "ceiling" in work:
         ce = bench_read_ceiling(torch, EXPERT_BYTES, 256, dev)
         cl = bench_read_ceiling(torch, LAYER_BYTES, 64, dev)
@@ -415,10 +443,10 @@ def main():
             line["moe_layer"]["pct_of_measured_read"] = round(
                 100 * line["moe_layer"]["GB/s"] / (LAYER_BYTES / cl / 1e9), 1)
     if "gemv" in work:
-        gsec = bench_gemv(torch, K, W, dev)
+        gsec, gstats = bench_gemv(torch, K, W, dev)
         gus = gsec / K * 1e6
         line["gemv"] = {"us": round(gus, 3), "GB/s": round(GEMV_BYTES / (gus * 1e-6) / 1e9, 1),
-                        "shape": [I, H], "x": "bf16", "out": "bf16", "bytes": GEMV_BYTES}
+                        "shape": [I, H], "x": "bf16", "out": "bf16", "bytes": GEMV_BYTES, "step_us": gstats}
     if not args.no_cpu:
         cpu = bench_cpu(args.cpu_seconds)
         line["cpu_baseline"] = cpu

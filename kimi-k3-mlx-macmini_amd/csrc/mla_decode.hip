@@ -216,16 +216,18 @@ __global__ __launch_bounds__(256, 2) void mla_attn_kernel(AttnArgs a) {
     // this wave's qa operands: head h0 + (lane % 16), k-steps 9 kh .. 9 kh + 8 (L2-resident)
     const int r16 = lane & 15, q4 = lane >> 4;
     const int nt = wave & 1, kh = wave >> 1;
+    // heads past H (last group) load zeros (out-of-range buffer offsets) and score 0; no
+    // select on the loaded values, so nothing waits for these loads before the first tile
     bf16x8 qhi[kKSteps / 2], qlo[kKSteps / 2];
     {
-        const bool hv = h0 + r16 < a.H;  // heads past H (last group) score 0
-        const uint16_t *qh = a.qa_hi + (h0 + r16) * kQaLd + kh * (kK / 2) + q4 * 8;
-        const uint16_t *ql = a.qa_lo + (h0 + r16) * kQaLd + kh * (kK / 2) + q4 * 8;
+        const uint32_t qbytes = static_cast<uint32_t>(a.H) * kQaLd * 2;
+        const auto rqh = make_rsrc(a.qa_hi, qbytes), rql = make_rsrc(a.qa_lo, qbytes);
+        const uint32_t qoff = h0 + r16 < a.H ? static_cast<uint32_t>(((h0 + r16) * kQaLd + kh * (kK / 2) + q4 * 8) * 2)
+                                             : kOobOffset;
 #pragma unroll
         for (int k = 0; k < kKSteps / 2; ++k) {
-            const uint4 z = make_uint4(0u, 0u, 0u, 0u);
-            qhi[k] = __builtin_bit_cast(bf16x8, hv ? *reinterpret_cast<const uint4 *>(qh + k * 32) : z);
-            qlo[k] = __builtin_bit_cast(bf16x8, hv ? *reinterpret_cast<const uint4 *>(ql + k * 32) : z);
+            qhi[k] = __builtin_bit_cast(bf16x8, buf_load16(rqh, qoff + k * 64u));
+            qlo[k] = __builtin_bit_cast(bf16x8, buf_load16(rql, qoff + k * 64u));
         }
     }
     if (tid < kHG) {
