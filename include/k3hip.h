@@ -168,7 +168,8 @@ int64_t k3_mla_workspace_size(int64_t H, int64_t T);
 
 /* o[h] = W_UV[h] @ (softmax_t(scale * (q_nope[h] W_UK[h] . lat[t] + q_rot[h] . rot[t])) @ lat)
  * for every head h, over the T valid cache rows.
- *   q_nope [H, nope], q_rot [H, rope]: rows ld_q elements apart (q_dtype K3_BF16 / K3_F32)
+ *   q_nope [H, nope] rows ld_q elements apart, q_rot [H, rope] rows ld_q_rot apart
+ *   (q_dtype K3_BF16 / K3_F32, the same for both)
  *   w_uk [H, nope, r], w_uv [H, v, r]: bf16, the two halves of kv_b (attention_mla.py:155-158)
  *   lat [T, r] rows ld_lat apart, rot [T, rope] rows ld_rot apart: the bf16 latent cache
  *   out [H, v] rows ld_out apart, out_dtype K3_F32 / K3_BF16
@@ -177,8 +178,8 @@ int64_t k3_mla_workspace_size(int64_t H, int64_t T);
  * softmax, deterministic.
  * Replaces the absorbed attention core of MLAAttention.__call__
  * (air_llm/models/kimi_k3/attention_mla.py:193-212) for T == 1. */
-int k3_mla_decode_absorbed(const void *q_nope, const void *q_rot, int64_t ld_q, int q_dtype,
-                           const void *w_uk, const void *w_uv, const void *lat, int64_t ld_lat,
+int k3_mla_decode_absorbed(const void *q_nope, const void *q_rot, int64_t ld_q, int64_t ld_q_rot,
+                           int q_dtype, const void *w_uk, const void *w_uv, const void *lat, int64_t ld_lat,
                            const void *rot, int64_t ld_rot, int64_t T, int64_t H,
                            int64_t kv_lora_rank, int64_t rope_dim, int64_t nope_dim, int64_t v_dim,
                            float scale, void *out, int out_dtype, int64_t ld_out, void *workspace,

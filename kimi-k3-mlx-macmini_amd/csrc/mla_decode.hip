@@ -14,13 +14,16 @@
 //   Q   qa[h] = q_nope[h] @ W_UK[h] in fp32, stored as a bf16 hi/lo pair
 //       (hi = rne(qa), lo = rne(qa - hi)), together with q_rot in columns 512..575, so the
 //       score contraction is one K = 576 product against the [lat | rot] cache rows.
-//   A   split-T flash decoding.  A block owns 32 heads and a contiguous token range; it
-//       walks the range in 32-token tiles: the tile goes HBM -> registers (prefetched one
-//       tile ahead) -> LDS; scores S[32 heads x 32 tokens] come from bf16 MFMAs
-//       (v_mfma_f32_16x16x32_bf16) of the hi and the lo half of qa against the tile; an
-//       online softmax (base 2, running max and sum per head) turns them into P, split
-//       again into a bf16 hi/lo pair; ctx[32 x 512] += P_hi @ tile + P_lo @ tile on MFMA.
-//       The block writes its unnormalised (ctx, max, sum) record per head.
+//   A   split-T flash decoding.  A block owns 16 heads and a contiguous token range (one
+//       block per CU); its wave pairs are independent streams over interleaved 16-token
+//       steps, the two waves of a pair splitting the score contraction and the context
+//       columns in halves.  Cache rows go HBM -> registers (MFMA operand layout, a ring of
+//       buffers) -> a wave-private LDS copy for the transposed context operand.  Scores
+//       S^T[16 tokens x 16 heads] come from bf16 MFMAs (v_mfma_f32_16x16x32_bf16) of the
+//       rows against the hi and the lo half of qa; the pair adds its partials across one
+//       barrier; a base-2 softmax turns them into P, split again into a bf16 hi/lo pair;
+//       ctx^T += rows^T [P_hi; P_lo] on the same MFMA.  The streams merge in the block,
+//       which writes its unnormalised (ctx, max, sum) record per head.
 //   M   per (head, quarter of the latent columns): log-sum-exp merge of the split records
 //       in a fixed order into the normalised ctx.
 //   U   o = W_UV[h] @ ctx[h] in fp32, 32 output rows per block.
@@ -39,19 +42,10 @@ constexpr int kR = 512;          // kv_lora_rank (latent width)
 constexpr int kRope = 64;        // rope key width
 constexpr int kK = kR + kRope;   // score contraction length
 constexpr int kQaLd = kK;        // row stride of the qa hi/lo arrays in the workspace
-constexpr int kLdsRow = kK + 8;  // padded LDS row (1168 B): conflict-free 16-byte row reads
-constexpr int kTile = 32;        // tokens per tile
-constexpr int kHG = 16;          // heads per attention block (one MFMA row tile)
-constexpr int kPRow = kTile + 8; // padded P row (bf16)
-constexpr int kSRow = kTile + 1; // padded score row (fp32)
+constexpr int kHG = 16;          // heads per attention block (one MFMA tile)
 constexpr int kPartLd = 516;     // floats per (split, head) record: ctx[512], max, sum, pad
 constexpr int kMaxSplits = 1024;
-constexpr int kChunksPerRow = kK / 8;  // 16-byte chunks per token row (64 lat + 8 rot)
-constexpr int kPre = kTile * kChunksPerRow / 256;  // chunks per thread per tile (9)
-constexpr int kKSteps = kK / 32;                   // 18 MFMA k-steps over the score contraction
-
-// tile, P hi/lo, two partial-score planes, running max / sum / rescale
-constexpr size_t kAttnLds = kTile * kLdsRow * 2 + 2 * kHG * kPRow * 2 + 2 * kHG * kSRow * 4 + 3 * kHG * 4;
+constexpr int kKSteps = kK / 32; // 18 MFMA k-steps over the score contraction
 
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 
@@ -94,8 +88,8 @@ __device__ __forceinline__ float load_q(const QT *p) {
 
 // ------------------------------------------------------------------ Q: qa = q_nope @ W_UK
 struct QaArgs {
-    const void *q_nope, *q_rot;  // [H, ld_q] rows (bf16 or fp32)
-    int64_t ld_q;
+    const void *q_nope, *q_rot;  // [H, ld_q] and [H, ld_q_rot] rows (bf16 or fp32)
+    int64_t ld_q, ld_q_rot;
     const uint16_t *w_uk;        // [H, nope, 512] bf16
     uint16_t *qa_hi, *qa_lo;     // [H, 576]
     int H, nope;
@@ -144,7 +138,7 @@ __global__ __launch_bounds__(256) void mla_qa_kernel(QaArgs a) {
         a.qa_lo[h * kQaLd + quarter * 128 + tid] = lo;
     } else if (quarter == 0 && tid < 128 + kRope) {
         const int j = tid - 128;
-        const float v = load_q(static_cast<const QT *>(a.q_rot) + static_cast<int64_t>(h) * a.ld_q + j);
+        const float v = load_q(static_cast<const QT *>(a.q_rot) + static_cast<int64_t>(h) * a.ld_q_rot + j);
         uint16_t hi, lo;
         split_bf16(v, hi, lo);
         a.qa_hi[h * kQaLd + kR + j] = hi;
@@ -158,190 +152,306 @@ struct AttnArgs {
     const void *lat;                // [T, ld_lat] bf16
     const void *rot;                // [T, ld_rot] bf16
     uint32_t lat_bytes, rot_bytes;  // readable bytes from each base
-    int64_t ld_lat, ld_rot;         // elements between tokens
+    uint32_t lat_row_bytes, rot_row_bytes;  // bytes between tokens
     float *part;                    // [NS, H, kPartLd]
     int H, T, Ts, NS;
     float scale_log2;               // softmax scale * log2(e)
     int swizzle;                    // XCD-aware block -> work mapping
 };
 
-// Block: 16 heads x one split (tiles s, s + NS, ...); 4 waves; ~44 KB of LDS and <= 128
-// VGPRs + AGPRs per lane, so two blocks share a CU and hide each other's barriers.
-//   scores  wave (nt, kh): tokens 16 nt .. +16 of the tile, k-steps 9 kh .. +9; its qa
-//           operands (hi and lo) live in registers for the whole kernel
-//   softmax 16 threads per head, 2 tokens each, over the two k-half planes
-//   ctx     wave w: latent columns 128 w .. +128 (8 MFMA column tiles); the transposed tile
-//           operand comes from ds_read_b64_tr_b16 (two per MFMA)
-__global__ __launch_bounds__(256, 2) void mla_attn_kernel(AttnArgs a) {
-    extern __shared__ uint4 smem[];
-    uint16_t *lat_s = reinterpret_cast<uint16_t *>(smem);                 // [32][kLdsRow]
-    uint16_t *p_s = lat_s + kTile * kLdsRow;                                // [2][16][kPRow]
-    float *s_s = reinterpret_cast<float *>(p_s + 2 * kHG * kPRow);          // [2][16][kSRow]
-    float *m_run = s_s + 2 * kHG * kSRow;
-    float *l_run = m_run + kHG;
-    float *alpha = l_run + kHG;
+// Sum / max over the four 16-lane rows of the wave (lanes l, l^16, l^32, l^48), result in
+// every lane; the row pairs are combined in a fixed order, so the sum is deterministic.
+__device__ __forceinline__ float rows4_sum(float v) {
+    auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+    r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float rows4_max(float v) {
+    auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+    r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
 
+// bf16 pair (RNE, hardware conversion) of (a, b): low half a
+__device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
+    const bf16x2 v = {static_cast<__bf16>(a), static_cast<__bf16>(b)};
+    return __builtin_bit_cast(uint32_t, v);
+}
+
+// Block: 16 heads x one split of Ts tokens, run by P pairs of waves.  Pair p is one
+// flash-decoding stream over the 16-token steps p, p + P, p + 2P, ... of the split; its two
+// waves split the score contraction and the context columns in halves:
+//   wave j of the pair owns latent columns 256 j .. +256 and rope columns 32 j .. +32.
+// Per step and wave:
+//   load    its 9 column blocks of the 16 cache rows straight into MFMA operand layout
+//           (lane (token r16, group q4) holds 8 consecutive columns of its row per block),
+//           into a ring of RING register buffers, so RING - 1 steps are in flight
+//   scores  partial S^T[token][head] = rows . qa over its columns (A = cache rows, B = qa hi
+//           and lo, which stay in registers); the two partials meet through LDS across one
+//           block barrier, and both waves add them in the same order, so both hold
+//           identical scores.  Lane (head r16, q4) has tokens 4 q4 .. +3.
+//   softmax per lane over its 4 tokens, the max reduced over the 4 lane rows; identical in
+//           the two waves.  The max used for the exponentials moves only at the first step
+//           of a pass; a later score above it by more than kSlack restarts the pass (of the
+//           whole block, so every wave meets the same barriers).
+//   ctx     ctx^T[col][head] += rows^T . P on the 16x16x32 bf16 MFMA with k-slots 0..3 =
+//           P_hi and 4..7 = P_lo of the lane's own 4 tokens, so P needs no data movement;
+//           the transposed rows come from a wave-private LDS copy via ds_read_b64_tr_b16,
+//           duplicated into both k halves.  Lane (head r16, q4) accumulates ctx[head][256 j
+//           + 16 n + 4 q4 .. +3] for its 16 column tiles n.
+// The P streams meet once, in the final in-block merge.
+constexpr int kStepT = 16;              // tokens per step
+constexpr int kHalfK = 9;               // column blocks (of 32) per wave: 8 latent + 1 rope
+constexpr int kHalfCols = kR / 2;       // latent columns per wave
+constexpr int kCopyRow = kHalfCols + 8; // padded LDS row of the wave's copy (528 B)
+constexpr size_t kCopyBytes = kStepT * kCopyRow * 2;  // 8448 B per wave and slot
+constexpr float kSlack = 64.f;          // log2 headroom before the pass restarts
+constexpr int kMaxPairs = 4;
+
+template <int P>
+constexpr size_t attn_lds_bytes() {  // two copy slots per wave; the merge reuses them
+    return 2 * P * 2 * kCopyBytes;
+}
+
+template <int P, int RING>
+__global__ __launch_bounds__(128 * P, 1) void mla_attn_kernel(AttnArgs a) {
+    static_assert(P == 2 || P == 4, "pairs per block");
+    static_assert(attn_lds_bytes<P>() >= static_cast<size_t>(P / 2) * 2 * 16 * 64 * 16, "merge buffers fit");
+    extern __shared__ uint4 smem[];
+    __shared__ f32x4_t xs[kMaxPairs][2][2][64];  // partial scores: [pair][member][slot][lane]
+    __shared__ int req[2];                         // restart requests by step parity (pass number)
+    __shared__ float m_s[kMaxPairs][kHG], l_s[kMaxPairs][kHG];
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int pr = wave >> 1, j = wave & 1;
+    const int r16 = lane & 15, q4 = lane >> 4;
+    uint16_t *copy = reinterpret_cast<uint16_t *>(reinterpret_cast<char *>(smem) + wave * 2 * kCopyBytes);
+
     // blocks b, b+8, b+16, ... share an XCD (and its L2): give them consecutive work items,
-    // so the head groups of one split read the same tiles through one L2
+    // so the head groups of one split read the same rows through one L2
     const int b = blockIdx.x;
     const int w = a.swizzle ? (b & 7) * (static_cast<int>(gridDim.x) >> 3) + (b >> 3) : b;
     const int HGn = (a.H + kHG - 1) / kHG;
     const int hg = w % HGn, split = w / HGn;
     const int h0 = hg * kHG;
-    // Split s owns the 32-token tiles s, s + NS, s + 2 NS, ...: blocks that run together
-    // read neighbouring tiles.
-    const int n_all = (a.T + kTile - 1) / kTile;
-    const int ntiles = (n_all - split + a.NS - 1) / a.NS;  // >= 1: NS <= n_all
-    auto tile_base = [&](int it) { return (split + it * a.NS) * kTile; };
+    const int t_begin = split * a.Ts;
+    const int t_end = min(a.T, t_begin + a.Ts);
+    // every pair runs the block's step count (pair 0's): a step past a pair's tokens is all
+    // masked and adds nothing, and the barriers of all waves stay matched
+    const int nsteps = (t_end - t_begin + P * kStepT - 1) / (P * kStepT);
+
+    if (tid < 2) req[tid] = 0;
 
     const auto rl = make_rsrc(a.lat, a.lat_bytes);
     const auto rr = make_rsrc(a.rot, a.rot_bytes);
-    // tile = 32 rows of 64 latent chunks + 32 rows of 8 rope chunks (16 B each): 8 latent
-    // loads and 1 rope load per thread, each a uniform instruction over the wave
-    auto load_tile = [&](uint4(&buf)[kPre], int tb) {
+    // Steps past nsteps and rows past T load zeros (out-of-range offsets), so every step
+    // issues the same loads and the ring needs no guard; masked rows score -inf.
+    auto load = [&](uint4(&buf)[kHalfK], int st) {
+        const int t = t_begin + (st * P + pr) * kStepT + r16;
+        const bool ok = t < t_end;
+        const uint32_t ol = ok ? static_cast<uint32_t>(t) * a.lat_row_bytes + (j * kHalfCols + q4 * 8) * 2u : kOobOffset;
+        const uint32_t orr = ok ? static_cast<uint32_t>(t) * a.rot_row_bytes + (j * 32 + q4 * 8) * 2u : kOobOffset;
 #pragma unroll
-        for (int i = 0; i < kPre - 1; ++i) {
-            const int c = tid + 256 * i;
-            const int t = tb + (c >> 6);
-            buf[i] = buf_load16(rl, t < a.T ? static_cast<uint32_t>(t * a.ld_lat * 2 + (c & 63) * 16) : kOobOffset);
-        }
-        const int t = tb + (tid >> 3);
-        buf[kPre - 1] = buf_load16(rr, t < a.T ? static_cast<uint32_t>(t * a.ld_rot * 2 + (tid & 7) * 16) : kOobOffset);
+        for (int k = 0; k < kHalfK - 1; ++k) buf[k] = buf_load16(rl, ol + k * 64u);
+        buf[kHalfK - 1] = buf_load16(rr, orr);
     };
-    uint4 pre0[kPre];
-    load_tile(pre0, tile_base(0));
-
-    // this wave's qa operands: head h0 + (lane % 16), k-steps 9 kh .. 9 kh + 8 (L2-resident)
-    const int r16 = lane & 15, q4 = lane >> 4;
-    const int nt = wave & 1, kh = wave >> 1;
-    // heads past H (last group) load zeros (out-of-range buffer offsets) and score 0; no
-    // select on the loaded values, so nothing waits for these loads before the first tile
-    bf16x8 qhi[kKSteps / 2], qlo[kKSteps / 2];
+    // qa operands of head h0 + r16 over this wave's columns (heads past H load zeros),
+    // issued before the ring so that waiting for a ring buffer also covers them
+    bf16x8 qhi[kHalfK], qlo[kHalfK];
     {
         const uint32_t qbytes = static_cast<uint32_t>(a.H) * kQaLd * 2;
         const auto rqh = make_rsrc(a.qa_hi, qbytes), rql = make_rsrc(a.qa_lo, qbytes);
-        const uint32_t qoff = h0 + r16 < a.H ? static_cast<uint32_t>(((h0 + r16) * kQaLd + kh * (kK / 2) + q4 * 8) * 2)
-                                             : kOobOffset;
+        const uint32_t qrow = h0 + r16 < a.H ? static_cast<uint32_t>((h0 + r16) * kQaLd + q4 * 8) * 2 : kOobOffset;
 #pragma unroll
-        for (int k = 0; k < kKSteps / 2; ++k) {
-            qhi[k] = __builtin_bit_cast(bf16x8, buf_load16(rqh, qoff + k * 64u));
-            qlo[k] = __builtin_bit_cast(bf16x8, buf_load16(rql, qoff + k * 64u));
+        for (int k = 0; k < kHalfK; ++k) {
+            const uint32_t col = k < kHalfK - 1 ? j * kHalfCols + k * 32 : kR + j * 32;
+            qhi[k] = __builtin_bit_cast(bf16x8, buf_load16(rqh, qrow + col * 2));
+            qlo[k] = __builtin_bit_cast(bf16x8, buf_load16(rql, qrow + col * 2));
         }
     }
-    if (tid < kHG) {
-        m_run[tid] = -INFINITY;
-        l_run[tid] = 0.f;
-    }
+    uint4 buf[RING][kHalfK];
 
-    f32x4_t cacc[8];
-#pragma unroll
-    for (int n = 0; n < 8; ++n) cacc[n] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    __syncthreads();  // requests cleared
 
-    auto tile_step = [&](int it, uint4(&buf)[kPre]) {
-        const int tb = tile_base(it);
-        __syncthreads();  // previous tile's LDS reads are done
+    f32x4_t cacc[kHalfCols / 16];
 #pragma unroll
-        for (int i = 0; i < kPre - 1; ++i) {
-            const int c = tid + 256 * i;
-            *reinterpret_cast<uint4 *>(lat_s + (c >> 6) * kLdsRow + (c & 63) * 8) = buf[i];
+    for (int n = 0; n < kHalfCols / 16; ++n) cacc[n] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    float m_used = -INFINITY, l_run = 0.f;
+    int pass = 0;  // restarts so far (block-uniform)
+
+    // transposed-read source of this lane: row 4 q4 + r16 / 4, columns 4 (r16 % 4) .. +3
+    typedef short s4_t __attribute__((ext_vector_type(4)));
+    typedef __attribute__((address_space(3))) s4_t *lds_s4;
+    const uint16_t *tsrc = copy + (q4 * 4 + (r16 >> 2)) * kCopyRow + (r16 & 3) * 4;
+    uint16_t *tdst = copy + r16 * kCopyRow + q4 * 8;
+
+    // A step is split in two halves, software-pipelined one step apart: the front half of
+    // step st + 1 (LDS copy, score products, refill of its buffer) is issued before the back
+    // half of step st (exchange across the barrier, softmax, context products), so the
+    // score products run on the matrix cores while the wave waits at the barrier and works
+    // through the softmax.  The LDS copy has two slots (step parity): the front half writes
+    // one while the back half reads the other.
+    // A wave whose scores exceed its max by more than kSlack accumulates nothing from that
+    // step on and posts a restart request; every wave sees it after the next barrier and
+    // skips the rest of the pass too.
+    bool again = false;
+    f32x4_t mine = {0.f, 0.f, 0.f, 0.f};  // this wave's partial scores of the pending step
+    auto front = [&](uint4(&bf)[kHalfK], int st) -> f32x4_t {
+        // ---- partial scores over this wave's columns: hi and lo chains
+        f32x4_t s0 = {0.f, 0.f, 0.f, 0.f}, s1 = s0;
+#pragma unroll
+        for (int k = 0; k < kHalfK; ++k) {
+            const bf16x8 rk = __builtin_bit_cast(bf16x8, bf[k]);
+            s0 = mfma_bf16(rk, qhi[k], s0);
+            s1 = mfma_bf16(rk, qlo[k], s1);
         }
-        *reinterpret_cast<uint4 *>(lat_s + (tid >> 3) * kLdsRow + kR + (tid & 7) * 8) = buf[kPre - 1];
+        // ---- latent columns of the rows -> the wave's LDS copy slot st & 1 (read last by
+        // step st - 2, earlier in program order), then refill the buffer RING steps ahead
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        uint16_t *dst = tdst + (st & 1) * (kCopyBytes / 2);
+#pragma unroll
+        for (int k = 0; k < kHalfK - 1; ++k) *reinterpret_cast<uint4 *>(dst + k * 32) = bf[k];
+        load(bf, st + RING);
+        return s0 + s1;
+    };
+    auto back = [&](int st) {
+        // ---- exchange the partials with the pair partner (slots alternate by step, so a
+        // write never meets the partner's read of the previous step)
+        const int slot = st & 1;
+        xs[pr][j][slot][lane] = mine;
         __syncthreads();
-        if (it + 1 < ntiles) load_tile(buf, tile_base(it + 1));
+        again = again || req[slot] > pass;  // requests of step st - 1 are visible here
+        if (again) return;
+        const f32x4_t other = xs[pr][j ^ 1][slot][lane];
+        const f32x4_t sc = j == 0 ? mine + other : other + mine;
 
-        // ---- partial scores over this wave's k half (hi and lo chains)
-        {
-            const uint16_t *bp = lat_s + (nt * 16 + r16) * kLdsRow + kh * (kK / 2) + q4 * 8;
-            f32x4_t sh = {0.f, 0.f, 0.f, 0.f}, sl = {0.f, 0.f, 0.f, 0.f};
+        // ---- softmax weights of this lane's tokens 4 q4 .. +3 of head r16
+        const int tb = t_begin + (st * P + pr) * kStepT + q4 * 4;
+        float s[4];
+        float mt = -INFINITY;
 #pragma unroll
-            for (int k = 0; k < kKSteps / 2; ++k) {
-                const bf16x8 bv = *reinterpret_cast<const bf16x8 *>(bp + k * 32);
-                sh = mfma_bf16(qhi[k], bv, sh);
-                sl = mfma_bf16(qlo[k], bv, sl);
-            }
-            const f32x4_t st = sh + sl;
-            float *sp = s_s + kh * kHG * kSRow;
-#pragma unroll
-            for (int i = 0; i < 4; ++i) sp[(q4 * 4 + i) * kSRow + nt * 16 + r16] = st[i];
+        for (int v = 0; v < 4; ++v) {
+            s[v] = tb + v < t_end ? sc[v] * a.scale_log2 : -INFINITY;
+            mt = fmaxf(mt, s[v]);
         }
-        __syncthreads();
-
-        // ---- online softmax: 16 threads per head, 2 tokens each
-        {
-            const int hh = tid >> 4, q = tid & 15;
-            float sv[2];
-            float mx = -INFINITY;
-#pragma unroll
-            for (int j = 0; j < 2; ++j) {
-                const int tok = q * 2 + j;
-                const float v = (s_s[hh * kSRow + tok] + s_s[(kHG + hh) * kSRow + tok]) * a.scale_log2;
-                sv[j] = tb + tok < a.T ? v : -INFINITY;
-                mx = fmaxf(mx, sv[j]);
-            }
-            mx = row16_max(mx);
-            const float mold = m_run[hh];
-            const float mnew = fmaxf(mold, mx);  // finite: every tile holds a valid token
-            float ps = 0.f;
-            uint16_t *ph = p_s + hh * kPRow + q * 2;
-            uint16_t *pl = ph + kHG * kPRow;
-#pragma unroll
-            for (int j = 0; j < 2; ++j) {
-                const float p = exp2f(sv[j] - mnew);
-                ps += p;
-                split_bf16(p, ph[j], pl[j]);
-            }
-            ps = row16_sum(ps);
-            if (q == 0) {
-                const float al = exp2f(mold - mnew);
-                alpha[hh] = al;
-                l_run[hh] = l_run[hh] * al + ps;
-                m_run[hh] = mnew;
+        mt = rows4_max(mt);  // -inf only for a step past the pair's tokens
+        if (__any(mt > m_used + kSlack)) {
+            m_used = fmaxf(m_used, mt);
+            if (st != 0) {  // earlier steps used a smaller max: the block restarts
+                req[slot ^ 1] = pass + 1;
+                again = true;
+                return;
             }
         }
-        __syncthreads();
+        // p <= 2^kSlack; exponents below -126 flush to 0, far below the step's largest p.
+        // Before the pair's first token the max is -inf and every p is 0.
+        const float mref = m_used == -INFINITY ? 0.f : m_used;
+        uint32_t pw[4];
+#pragma unroll
+        for (int v = 0; v < 4; v += 2) {
+            const float p0 = __builtin_amdgcn_exp2f(s[v] - mref), p1 = __builtin_amdgcn_exp2f(s[v + 1] - mref);
+            l_run += p0 + p1;
+            const uint32_t hi = pack_bf16x2(p0, p1);
+            pw[v / 2] = hi;
+            pw[2 + v / 2] = pack_bf16x2(p0 - __uint_as_float(hi << 16), p1 - __uint_as_float(hi & 0xffff0000u));
+        }
+        const bf16x8 pb = __builtin_bit_cast(bf16x8, make_uint4(pw[0], pw[1], pw[2], pw[3]));
 
-        // ---- ctx[16 x 512] += P @ tile: wave owns latent columns [128 wave, +128)
-        {
-            const bf16x8 ph = *reinterpret_cast<const bf16x8 *>(p_s + r16 * kPRow + q4 * 8);
-            const bf16x8 pl = *reinterpret_cast<const bf16x8 *>(p_s + (kHG + r16) * kPRow + q4 * 8);
-            float al[4];
+        // ---- ctx^T += rows^T . [P_hi; P_lo] over this wave's columns; all transposed
+        // reads are issued before the first product, so their latencies overlap
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        const uint16_t *src = tsrc + slot * (kCopyBytes / 2);
+        s4_t t4[kHalfCols / 16];
 #pragma unroll
-            for (int i = 0; i < 4; ++i) al[i] = alpha[q4 * 4 + i];
-            if (!__all(al[0] == 1.f && al[1] == 1.f && al[2] == 1.f && al[3] == 1.f)) {
+        for (int n = 0; n < kHalfCols / 16; ++n) t4[n] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4)(src + n * 16));
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-                for (int n = 0; n < 8; ++n)
-#pragma unroll
-                    for (int i = 0; i < 4; ++i) cacc[n][i] *= al[i];
-            }
-            // transposed operand: source lane s' of group g points at token 8g + s'/4,
-            // columns c0 + 4 (s' % 4) .. +3; a second read 4 tokens further down
-            typedef short s4_t __attribute__((ext_vector_type(4)));
-            const uint16_t *tsrc = lat_s + (q4 * 8 + (r16 >> 2)) * kLdsRow + wave * 128 + (r16 & 3) * 4;
-#pragma unroll
-            for (int n = 0; n < 8; ++n) {
-                typedef __attribute__((address_space(3))) s4_t *lds_s4;
-                const s4_t lo4 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4)(tsrc + n * 16));
-                const s4_t hi4 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4)(tsrc + n * 16 + 4 * kLdsRow));
-                const bf16x8 bb = __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo4, hi4, 0, 1, 2, 3, 4, 5, 6, 7));
-                cacc[n] = mfma_bf16(ph, bb, cacc[n]);
-                cacc[n] = mfma_bf16(pl, bb, cacc[n]);
-            }
+        for (int n = 0; n < kHalfCols / 16; ++n) {
+            const bf16x8 ra = __builtin_bit_cast(bf16x8, __builtin_shufflevector(t4[n], t4[n], 0, 1, 2, 3, 0, 1, 2, 3));
+            cacc[n] = mfma_bf16(ra, pb, cacc[n]);
         }
     };
-    for (int it = 0; it < ntiles; ++it) tile_step(it, pre0);
+    // The max used by the exponentials (per head) is set by the first step of a pass and
+    // only moves when a score exceeds it by more than kSlack (log2 units).  Then the block
+    // restarts the pass from its first step, the triggering pair with its larger max, so the
+    // accumulators are never rescaled inside the loop.  A restarted pass does not trigger
+    // again on the steps before the trigger, so a block makes at most nsteps + 1 passes.
+    // The trip loop runs whole trips of RING steps (steps past the split are all masked)
+    // and has no other exit, so the waits at its top see the ring in steady-state order.
+    for (;;) {
+        // in buffer order (the trip loop waits for buffer r behind the loads of the others)
+#pragma unroll
+        for (int r = 0; r < RING; ++r) {
+            load(buf[r], r);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        again = false;
+        mine = front(buf[0], 0);
+        for (int st = 0; st < nsteps; st += RING) {
+#pragma unroll
+            for (int r = 0; r < RING; ++r) {
+                const f32x4_t next = front(buf[(r + 1) % RING], st + r + 1);
+                back(st + r);
+                mine = next;
+            }
+        }
+        __syncthreads();  // publishes a request made in the last step
+        if (max(req[0], req[1]) <= pass) break;  // block-uniform
+        ++pass;
+#pragma unroll
+        for (int n = 0; n < kHalfCols / 16; ++n) cacc[n] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+        l_run = 0.f;
+    }
 
-    // ---- split record: unnormalised ctx, running max and sum
-    float *part = a.part + (static_cast<int64_t>(split) * a.H + h0) * kPartLd;
+    // ---- in-block merge of the P streams: common max, then a fixed pairwise tree
+    const float l_tot = rows4_sum(l_run);
+    if (j == 0 && q4 == 0) {
+        m_s[pr][r16] = m_used;
+        l_s[pr][r16] = l_tot;
+    }
+    __syncthreads();  // every stream is done with its LDS copies
+    float M = -INFINITY;
 #pragma unroll
-    for (int n = 0; n < 8; ++n)
+    for (int v = 0; v < P; ++v) M = fmaxf(M, m_s[v][r16]);  // finite: the split has a token
+    const float f = m_used == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m_used - M);
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
-            if (h0 + q4 * 4 + i < a.H) part[(q4 * 4 + i) * kPartLd + wave * 128 + n * 16 + r16] = cacc[n][i];
-    if (tid < kHG && h0 + tid < a.H) {
-        part[tid * kPartLd + kR] = m_run[tid];
-        part[tid * kPartLd + kR + 1] = l_run[tid];
+    for (int n = 0; n < kHalfCols / 16; ++n) cacc[n] *= f;
+    float4 *xb = reinterpret_cast<float4 *>(smem);  // [P / 2][2][16][64] float4
+#pragma unroll
+    for (int half = P / 2; half >= 1; half /= 2) {
+        if (pr >= half && pr < 2 * half) {
+#pragma unroll
+            for (int n = 0; n < kHalfCols / 16; ++n)
+                xb[(((pr - half) * 2 + j) * 16 + n) * 64 + lane] = make_float4(cacc[n][0], cacc[n][1], cacc[n][2], cacc[n][3]);
+        }
+        __syncthreads();
+        if (pr < half) {
+#pragma unroll
+            for (int n = 0; n < kHalfCols / 16; ++n) {
+                const float4 o = xb[((pr * 2 + j) * 16 + n) * 64 + lane];
+                cacc[n] += f32x4_t{o.x, o.y, o.z, o.w};
+            }
+        }
+        __syncthreads();
+    }
+    if (pr == 0 && h0 + r16 < a.H) {
+        float *rec = a.part + (static_cast<int64_t>(split) * a.H + h0 + r16) * kPartLd;
+#pragma unroll
+        for (int n = 0; n < kHalfCols / 16; ++n)
+            *reinterpret_cast<float4 *>(rec + j * kHalfCols + n * 16 + q4 * 4) =
+                make_float4(cacc[n][0], cacc[n][1], cacc[n][2], cacc[n][3]);
+        if (j == 0 && q4 == 0) {
+            float L = 0.f;
+#pragma unroll
+            for (int v = 0; v < P; ++v) {
+                const float mv = m_s[v][r16];
+                L += mv == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mv - M) * l_s[v][r16];
+            }
+            rec[kR] = M;
+            rec[kR + 1] = L;
+        }
     }
 }
 
@@ -494,11 +604,16 @@ __global__ __launch_bounds__(256) void mla_uv_kernel(MergeArgs a) {
 }
 
 // ------------------------------------------------------------------ host side
-// Tokens per split: at least 128 (the qa tile staged per block is amortised over >= 4
-// tiles), otherwise enough that one split per 128 tokens-of-work keeps ~256 blocks busy.
-void mla_splits(int64_t T, int *Ts, int *NS) {
-    int64_t ts = std::max<int64_t>(128, cdiv(T, 128));
-    ts = cdiv(ts, kTile) * kTile;
+constexpr int kPairs = 2;  // streams (wave pairs) per attention block: one wave per SIMD
+constexpr int kRing = 2;   // register buffers per wave (deeper rings measured no faster)
+
+// One attention block per CU: about 256 blocks of (head group, split); a split is a
+// multiple of 16 kPairs tokens, so every step of every stream lies inside it.
+void mla_splits(int64_t H, int64_t T, int *Ts, int *NS) {
+    const int64_t hgn = cdiv(H, kHG);
+    const int64_t want = std::max<int64_t>(1, 256 / hgn);
+    int64_t ts = cdiv(T, want);
+    ts = cdiv(ts, kStepT * kPairs) * kStepT * kPairs;
     *Ts = static_cast<int>(ts);
     *NS = static_cast<int>(cdiv(T, ts));
 }
@@ -509,7 +624,7 @@ struct MlaWs {
 
 MlaWs mla_ws_layout(int64_t H, int64_t T) {
     int Ts, NS;
-    mla_splits(std::max<int64_t>(T, 1), &Ts, &NS);
+    mla_splits(H, std::max<int64_t>(T, 1), &Ts, &NS);
     MlaWs L{};
     auto up = [](size_t v) { return (v + 255) & ~size_t(255); };
     size_t o = 0;
@@ -531,8 +646,8 @@ extern "C" int64_t k3_mla_workspace_size(int64_t H, int64_t T) {
     return static_cast<int64_t>(mla_ws_layout(H, T).total);
 }
 
-extern "C" int k3_mla_decode_absorbed(const void *q_nope, const void *q_rot, int64_t ld_q, int q_dtype,
-                                      const void *w_uk, const void *w_uv, const void *lat, int64_t ld_lat,
+extern "C" int k3_mla_decode_absorbed(const void *q_nope, const void *q_rot, int64_t ld_q, int64_t ld_q_rot,
+                                      int q_dtype, const void *w_uk, const void *w_uv, const void *lat, int64_t ld_lat,
                                       const void *rot, int64_t ld_rot, int64_t T, int64_t H, int64_t kv_lora_rank,
                                       int64_t rope_dim, int64_t nope_dim, int64_t v_dim, float scale, void *out,
                                       int out_dtype, int64_t ld_out, void *workspace, int64_t workspace_bytes,
@@ -550,7 +665,8 @@ extern "C" int k3_mla_decode_absorbed(const void *q_nope, const void *q_rot, int
         return set_error(K3_ERR_SHAPE, "mla decode: nope=%lld must be in 1..256 and v=%lld in 1..1024",
                          (long long)nope_dim, (long long)v_dim);
     if (T <= 0) return set_error(K3_ERR_SHAPE, "mla decode: empty cache (T=%lld)", (long long)T);
-    if (ld_q < nope_dim || ld_lat < kR || ld_rot < kRope || ld_out < v_dim || ld_lat % 8 || ld_rot % 8)
+    if (ld_q < nope_dim || ld_q_rot < rope_dim || ld_lat < kR || ld_rot < kRope || ld_out < v_dim || ld_lat % 8 ||
+        ld_rot % 8)
         return set_error(K3_ERR_SHAPE, "mla decode: row strides too small, or cache strides not multiples of 8");
     if (!aligned16(lat) || !aligned16(rot) || !aligned16(w_uk) || !aligned16(w_uv) || !aligned16(workspace))
         return set_error(K3_ERR_ALIGN, "mla decode: cache, weights and workspace must be 16-byte aligned");
@@ -562,7 +678,7 @@ extern "C" int k3_mla_decode_absorbed(const void *q_nope, const void *q_rot, int
         return set_error(K3_ERR_WORKSPACE, "mla decode: workspace %lld < %zu bytes", (long long)workspace_bytes,
                          L.total);
     int Ts, NS;
-    mla_splits(T, &Ts, &NS);
+    mla_splits(H, T, &Ts, &NS);
     if (NS > kMaxSplits) return set_error(K3_ERR_SHAPE, "mla decode: T=%lld needs too many splits", (long long)T);
     auto st = static_cast<hipStream_t>(stream);
     char *ws = static_cast<char *>(workspace);
@@ -570,7 +686,7 @@ extern "C" int k3_mla_decode_absorbed(const void *q_nope, const void *q_rot, int
     uint16_t *qa_lo = reinterpret_cast<uint16_t *>(ws + L.qa_lo);
     float *part = reinterpret_cast<float *>(ws + L.part);
 
-    QaArgs qa{q_nope, q_rot, ld_q, static_cast<const uint16_t *>(w_uk), qa_hi, qa_lo, static_cast<int>(H),
+    QaArgs qa{q_nope, q_rot, ld_q, ld_q_rot, static_cast<const uint16_t *>(w_uk), qa_hi, qa_lo, static_cast<int>(H),
               static_cast<int>(nope_dim)};
     if (q_dtype == K3_BF16)
         mla_qa_kernel<uint16_t><<<dim3(static_cast<unsigned>(H * 4)), 256, 0, st>>>(qa);
@@ -586,8 +702,8 @@ extern "C" int k3_mla_decode_absorbed(const void *q_nope, const void *q_rot, int
     aa.rot = rot;
     aa.lat_bytes = static_cast<uint32_t>(lat_bytes);
     aa.rot_bytes = static_cast<uint32_t>(rot_bytes);
-    aa.ld_lat = ld_lat;
-    aa.ld_rot = ld_rot;
+    aa.lat_row_bytes = static_cast<uint32_t>(ld_lat * 2);
+    aa.rot_row_bytes = static_cast<uint32_t>(ld_rot * 2);
     aa.part = part;
     aa.H = static_cast<int>(H);
     aa.T = static_cast<int>(T);
@@ -596,8 +712,14 @@ extern "C" int k3_mla_decode_absorbed(const void *q_nope, const void *q_rot, int
     aa.scale_log2 = scale * 1.4426950408889634f;
     const int blocks = NS * static_cast<int>(cdiv(H, kHG));
     aa.swizzle = blocks % 8 == 0;
-    static_assert(kAttnLds <= 64 * 1024, "attention LDS: two blocks per CU");
-    mla_attn_kernel<<<dim3(static_cast<unsigned>(blocks)), 256, kAttnLds, st>>>(aa);
+    constexpr auto attn = &mla_attn_kernel<kPairs, kRing>;
+    constexpr size_t lds = attn_lds_bytes<kPairs>();
+    static const hipError_t lds_rc = hipFuncSetAttribute(reinterpret_cast<const void *>(attn),
+                                                         hipFuncAttributeMaxDynamicSharedMemorySize,
+                                                         static_cast<int>(lds));  // may exceed the 64 KB default
+    rc = check_hip(lds_rc, "mla decode: attention LDS size");
+    if (rc) return rc;
+    attn<<<dim3(static_cast<unsigned>(blocks)), 128 * kPairs, lds, st>>>(aa);
     rc = check_hip(hipGetLastError(), "mla decode: attention launch");
     if (rc) return rc;
 

@@ -146,15 +146,17 @@ def mla_decode_absorbed(q_nope: torch.Tensor, q_rot: torch.Tensor, wk: torch.Ten
     qdt = torch.bfloat16 if (q_nope.dtype == torch.bfloat16 and q_rot.dtype == torch.bfloat16) else torch.float32
     q_nope = q_nope.to(qdt)
     q_rot = q_rot.to(qdt)
-    if (q_nope.stride(1) != 1 or q_rot.stride(1) != 1 or q_nope.stride(0) != q_rot.stride(0)):
-        q = torch.cat([q_nope, q_rot], dim=1).contiguous()
-        q_nope, q_rot = q[:, :nope], q[:, nope:]
+    if q_nope.stride(1) != 1:
+        q_nope = q_nope.contiguous()
+    if q_rot.stride(1) != 1:
+        q_rot = q_rot.contiguous()
     V = wv.shape[1]
     out = torch.empty((H, V), dtype=out_dtype, device=lat.device)
     ntok = lat.shape[0]
     ws_bytes = int(_lib.lib().k3_mla_workspace_size(H, ntok))
     ws = _workspace.get(lat.device, ws_bytes, "mla")
-    _lib.call("k3_mla_decode_absorbed", T.ptr(q_nope), T.ptr(q_rot), q_nope.stride(0), T.dtype_code(qdt),
+    _lib.call("k3_mla_decode_absorbed", T.ptr(q_nope), T.ptr(q_rot), q_nope.stride(0), q_rot.stride(0),
+              T.dtype_code(qdt),
               T.ptr(wk), T.ptr(wv), T.ptr(lat), lat.stride(0), T.ptr(rot), rot.stride(0), ntok, H, r,
               q_rot.shape[1], nope, V, float(scale), T.ptr(out), T.dtype_code(out_dtype), out.stride(0),
               T.ptr(ws), ws.numel(), T.stream(lat))

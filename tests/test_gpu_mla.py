@@ -101,6 +101,24 @@ def test_mla_decode_peaked_softmax():
     assert om.normwise_rel(got, want) <= TOL
 
 
+def test_mla_decode_rising_scores_restart_passes():
+    """Scores that climb by 80..170 (log2 units) every 96 tokens, for half of the heads:
+    a later step of a split exceeds the max its pass started with by far more than the
+    kernel's headroom, so the split's pass restarts with the larger max (several times per
+    split); the other heads fall instead.  The rope column 0 carries the ramp."""
+    H, T = 64, 20000
+    q_nope, q_rot, w_uk, w_uv, lat, rot = make(11, H, T)
+    q_rot[:, 0] = np.linspace(-2.0, 2.0, H).astype(np.float32)
+    rot[:, 0] = (800.0 * ((np.arange(T) // 96) % 4)).astype(np.float32)
+    args = (q_nope, bf(q_rot), w_uk, w_uv, lat, bf(rot))
+    scale = 192 ** -0.5
+    got = run(*args, scale)
+    want = omla.mla_decode_absorbed(*args, scale)[0]
+    rel = om.normwise_rel(got, want)
+    print(f"rising scores rel={rel:.3e}")
+    assert rel <= 1e-4, rel
+
+
 def test_mla_decode_is_deterministic():
     args = make(10, 64, 5000)
     a = run(*args, 0.1)
