@@ -43,7 +43,6 @@ constexpr int kRope = 64;        // rope key width
 constexpr int kK = kR + kRope;   // score contraction length
 constexpr int kQaLd = kK;        // row stride of the qa hi/lo arrays in the workspace
 constexpr int kHG = 16;          // heads per attention block (one MFMA tile)
-constexpr int kPartLd = 516;     // floats per (split, head) record: ctx[512], max, sum, pad
 constexpr int kMaxSplits = 1024;
 constexpr int kKSteps = kK / 32; // 18 MFMA k-steps over the score contraction
 
@@ -153,7 +152,8 @@ struct AttnArgs {
     const void *rot;                // [T, ld_rot] bf16
     uint32_t lat_bytes, rot_bytes;  // readable bytes from each base
     uint32_t lat_row_bytes, rot_row_bytes;  // bytes between tokens
-    float *part;                    // [NS, H, kPartLd]
+    float *part;                    // [NS, H, 512] unnormalised context per split and head
+    float2 *ml;                     // [NS, H] (running max, running sum) per split and head
     int H, T, Ts, NS;
     float scale_log2;               // softmax scale * log2(e)
     int swizzle;                    // XCD-aware block -> work mapping
@@ -209,6 +209,14 @@ constexpr int kCopyRow = kHalfCols + 8; // padded LDS row of the wave's copy (52
 constexpr size_t kCopyBytes = kStepT * kCopyRow * 2;  // 8448 B per wave and slot
 constexpr float kSlack = 64.f;          // log2 headroom before the pass restarts
 constexpr int kMaxPairs = 4;
+#ifndef MLA_TRB
+#define MLA_TRB 16
+#endif
+#ifndef MLA_OCC
+#define MLA_OCC 1
+#endif
+constexpr int kTrBatch = MLA_TRB;       // transposed reads issued ahead of their products
+constexpr int kCsRow = kR + 4;          // padded LDS row of the merged context (floats)
 
 template <int P>
 constexpr size_t attn_lds_bytes() {  // two copy slots per wave; the merge reuses them
@@ -216,13 +224,14 @@ constexpr size_t attn_lds_bytes() {  // two copy slots per wave; the merge reuse
 }
 
 template <int P, int RING>
-__global__ __launch_bounds__(128 * P, 1) void mla_attn_kernel(AttnArgs a) {
+__global__ __launch_bounds__(128 * P, MLA_OCC) void mla_attn_kernel(AttnArgs a) {
     static_assert(P == 2 || P == 4, "pairs per block");
     static_assert(attn_lds_bytes<P>() >= static_cast<size_t>(P / 2) * 2 * 16 * 64 * 16, "merge buffers fit");
+    static_assert(attn_lds_bytes<P>() >= static_cast<size_t>(kHG) * kCsRow * 4, "context staging fits");
     extern __shared__ uint4 smem[];
-    __shared__ f32x4_t xs[kMaxPairs][2][2][64];  // partial scores: [pair][member][slot][lane]
+    __shared__ f32x4_t xs[P][2][2][64];  // partial scores: [pair][member][slot][lane]
     __shared__ int req[2];                         // restart requests by step parity (pass number)
-    __shared__ float m_s[kMaxPairs][kHG], l_s[kMaxPairs][kHG];
+    __shared__ float m_s[P][kHG], l_s[P][kHG];
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int pr = wave >> 1, j = wave & 1;
@@ -363,14 +372,18 @@ __global__ __launch_bounds__(128 * P, 1) void mla_attn_kernel(AttnArgs a) {
         // reads are issued before the first product, so their latencies overlap
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
         const uint16_t *src = tsrc + slot * (kCopyBytes / 2);
-        s4_t t4[kHalfCols / 16];
 #pragma unroll
-        for (int n = 0; n < kHalfCols / 16; ++n) t4[n] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4)(src + n * 16));
-        __builtin_amdgcn_sched_barrier(0);
+        for (int n0 = 0; n0 < kHalfCols / 16; n0 += kTrBatch) {
+            s4_t t4[kTrBatch];
 #pragma unroll
-        for (int n = 0; n < kHalfCols / 16; ++n) {
-            const bf16x8 ra = __builtin_bit_cast(bf16x8, __builtin_shufflevector(t4[n], t4[n], 0, 1, 2, 3, 0, 1, 2, 3));
-            cacc[n] = mfma_bf16(ra, pb, cacc[n]);
+            for (int n = 0; n < kTrBatch; ++n)
+                t4[n] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4)(src + (n0 + n) * 16));
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int n = 0; n < kTrBatch; ++n) {
+                const bf16x8 ra = __builtin_bit_cast(bf16x8, __builtin_shufflevector(t4[n], t4[n], 0, 1, 2, 3, 0, 1, 2, 3));
+                cacc[n0 + n] = mfma_bf16(ra, pb, cacc[n0 + n]);
+            }
         }
     };
     // The max used by the exponentials (per head) is set by the first step of a pass and
@@ -436,29 +449,37 @@ __global__ __launch_bounds__(128 * P, 1) void mla_attn_kernel(AttnArgs a) {
         }
         __syncthreads();
     }
-    if (pr == 0 && h0 + r16 < a.H) {
-        float *rec = a.part + (static_cast<int64_t>(split) * a.H + h0 + r16) * kPartLd;
+    // ---- the merged context goes out through LDS, so that each store of a wave writes
+    // 1 KB of one record row (the merge buffers are free after the last barrier)
+    float *cs = reinterpret_cast<float *>(smem);  // [16][kCsRow]
+    if (pr == 0) {
 #pragma unroll
         for (int n = 0; n < kHalfCols / 16; ++n)
-            *reinterpret_cast<float4 *>(rec + j * kHalfCols + n * 16 + q4 * 4) =
+            *reinterpret_cast<float4 *>(cs + r16 * kCsRow + j * kHalfCols + n * 16 + q4 * 4) =
                 make_float4(cacc[n][0], cacc[n][1], cacc[n][2], cacc[n][3]);
-        if (j == 0 && q4 == 0) {
+        if (j == 0 && q4 == 0 && h0 + r16 < a.H) {
             float L = 0.f;
 #pragma unroll
             for (int v = 0; v < P; ++v) {
                 const float mv = m_s[v][r16];
                 L += mv == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mv - M) * l_s[v][r16];
             }
-            rec[kR] = M;
-            rec[kR + 1] = L;
+            a.ml[static_cast<int64_t>(split) * a.H + h0 + r16] = make_float2(M, L);
         }
+    }
+    __syncthreads();
+    float *rec = a.part + (static_cast<int64_t>(split) * a.H + h0) * kR;
+    for (int f = tid; f < kHG * kR / 4; f += 128 * P) {
+        const int row = f / (kR / 4), c4 = f % (kR / 4);
+        if (h0 + row < a.H)
+            *reinterpret_cast<float4 *>(rec + row * kR + c4 * 4) = *reinterpret_cast<const float4 *>(cs + row * kCsRow + c4 * 4);
     }
 }
 
 // ------------------------------------------------------------------ M: merge, then W_UV
 struct MergeArgs {
-    const float *part;
-    float *ctx;            // [H, 512] merged, normalised context
+    const float *part;     // [NS, H, 512]
+    const float2 *ml;      // [NS, H]
     const uint16_t *w_uv;  // [H, V, 512] bf16
     void *out;             // [H, V] rows of ld_out elements
     int64_t ld_out;
@@ -483,135 +504,135 @@ __device__ __forceinline__ float block_max256(float v, float *red) {
     return r;
 }
 
-// grid: H * 4; block (h, quarter): ctx[h][128 quarter .. +128) = sum_s w_s ctx_s / L with
-// w_s = 2^(m_s - M).  Fixed order: 8 groups of splits (s = g mod 8), then the groups in order.
-// Every load of a thread is issued before the first is used: the records come from the
-// last-level cache, so the cost is round trips, not bytes.
-__global__ __launch_bounds__(256) void mla_merge_kernel(MergeArgs a) {
-    __shared__ float wsplit[kMaxSplits];
-    __shared__ float csum[8][129];
-    __shared__ float red[4];
-    const int h = blockIdx.x >> 2, quarter = blockIdx.x & 3;
-    const int tid = threadIdx.x;
-    const float *rec = a.part + static_cast<int64_t>(h) * kPartLd;
-    const int64_t sstride = static_cast<int64_t>(a.H) * kPartLd;
+constexpr int kMergeChunk = 64;  // splits whose record columns are in flight at once
+constexpr int kMergeRows = 64;   // W_UV rows per merge block (16 per wave)
 
-    // column loads first (16 splits per thread covers NS <= 128 in one batch)
-    const int c4 = tid & 31, grp = tid >> 5;
-    const float *col = rec + quarter * 128 + 4 * c4;
-    constexpr int kPer = 16;
-    float4 v[kPer];
+// grid: H * cdiv(V, kMergeRows); block (h, vb): every block of head h merges the split
+// records of h into ctx[h], then computes o[h][v] = W_UV[h][v] . ctx[h] for its rows.  All
+// loads of a chunk of 64 splits are issued at once, behind the W_UV rows and the split
+// maxima, so the block waits for memory about once per chunk.
+//   merge:  thread t owns columns 4 (t % 128) .. +3 of the splits s = t / 128 (mod 2);
+//           ctx = sum_s 2^(m_s - M) ctx_s / L with M = max_s m_s, L = sum_s 2^(m_s - M) l_s,
+//           summed in split order within each half, then half 0 + half 1
+//   W_UV:   wave w, rows vb * kMergeRows + 8 w .. +8; lane l covers columns 8 l .. +8
+__global__ __launch_bounds__(256) void mla_merge_uv_kernel(MergeArgs a) {
+    __shared__ float4 half1[kR / 4];
+    __shared__ float ctx[kR];
+    __shared__ float wsplit[kMaxSplits];
+    __shared__ float red[4];
+    const int vb_n = (a.V + kMergeRows - 1) / kMergeRows;
+    const int h = blockIdx.x / vb_n, vb = blockIdx.x % vb_n;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int c4 = tid & 127, g = tid >> 7;
+
+    // W_UV rows of this block
+    const int r0 = vb * kMergeRows + wave * (kMergeRows / 4);
+    uint4 w[kMergeRows / 4];
 #pragma unroll
-    for (int u = 0; u < kPer; ++u) {
-        const int s = grp + 8 * u;
-        v[u] = s < a.NS ? *reinterpret_cast<const float4 *>(col + s * sstride) : make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int u = 0; u < kMergeRows / 4; ++u) {
+        const int v = r0 + u;
+        w[u] = v < a.V ? *reinterpret_cast<const uint4 *>(a.w_uv + (static_cast<int64_t>(h) * a.V + v) * kR + lane * 8)
+                       : make_uint4(0u, 0u, 0u, 0u);
     }
-    float mv[kMaxSplits / 256], lv[kMaxSplits / 256];
+    // split maxima and sums
+    float2 mlv[kMaxSplits / 256];
+#pragma unroll
+    for (int q = 0; q < kMaxSplits / 256; ++q) {
+        const int sidx = tid + 256 * q;
+        mlv[q] = sidx < a.NS ? a.ml[static_cast<int64_t>(sidx) * a.H + h] : make_float2(-INFINITY, 0.f);
+    }
+    // record columns of the first chunk
+    const float *col = a.part + static_cast<int64_t>(h) * kR + 4 * c4;
+    const int64_t sstride = static_cast<int64_t>(a.H) * kR;
+    auto load_chunk = [&](float4(&c)[kMergeChunk / 2], int s0) {
+#pragma unroll
+        for (int u = 0; u < kMergeChunk / 2; ++u) {
+            const int sidx = s0 + 2 * u + g;
+            c[u] = sidx < a.NS ? *reinterpret_cast<const float4 *>(col + sidx * sstride) : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+    };
+    float4 c[kMergeChunk / 2];
+    load_chunk(c, 0);
+
     float mx = -INFINITY;
 #pragma unroll
-    for (int j = 0; j < kMaxSplits / 256; ++j) {
-        const int s = tid + 256 * j;
-        mv[j] = s < a.NS ? rec[s * sstride + kR] : -INFINITY;
-        lv[j] = s < a.NS ? rec[s * sstride + kR + 1] : 0.f;
-        mx = fmaxf(mx, mv[j]);
-    }
-    const float M = block_max256(mx, red);
+    for (int q = 0; q < kMaxSplits / 256; ++q) mx = fmaxf(mx, mlv[q].x);
+    const float M = block_max256(mx, red);  // finite: every split has a token
     float ls = 0.f;
 #pragma unroll
-    for (int j = 0; j < kMaxSplits / 256; ++j) {
-        const int s = tid + 256 * j;
-        if (s < a.NS) {
-            const float e = exp2f(mv[j] - M);
-            wsplit[s] = e;
-            ls += e * lv[j];
+    for (int q = 0; q < kMaxSplits / 256; ++q) {
+        const int sidx = tid + 256 * q;
+        if (sidx < a.NS) {
+            const float e = exp2f(mlv[q].x - M);
+            wsplit[sidx] = e;
+            ls += e * mlv[q].y;
         }
     }
     const float inv_l = 1.0f / block_sum256(ls, red);  // block_sum256 synchronises wsplit
 
     float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int s0 = 0;;) {
 #pragma unroll
-    for (int u = 0; u < kPer; ++u) {
-        const int s = grp + 8 * u;
-        const float ws = s < a.NS ? wsplit[s] : 0.f;
-        acc.x = fmaf(ws, v[u].x, acc.x);
-        acc.y = fmaf(ws, v[u].y, acc.y);
-        acc.z = fmaf(ws, v[u].z, acc.z);
-        acc.w = fmaf(ws, v[u].w, acc.w);
-    }
-    for (int s0 = grp + 8 * kPer; s0 < a.NS; s0 += 8 * kPer) {  // NS > 128
-#pragma unroll
-        for (int u = 0; u < kPer; ++u) {
-            const int s = s0 + 8 * u;
-            v[u] = s < a.NS ? *reinterpret_cast<const float4 *>(col + s * sstride) : make_float4(0.f, 0.f, 0.f, 0.f);
+        for (int u = 0; u < kMergeChunk / 2; ++u) {
+            const int sidx = s0 + 2 * u + g;
+            const float ws = sidx < a.NS ? wsplit[sidx] : 0.f;
+            acc.x = fmaf(ws, c[u].x, acc.x);
+            acc.y = fmaf(ws, c[u].y, acc.y);
+            acc.z = fmaf(ws, c[u].z, acc.z);
+            acc.w = fmaf(ws, c[u].w, acc.w);
         }
-#pragma unroll
-        for (int u = 0; u < kPer; ++u) {
-            const int s = s0 + 8 * u;
-            const float ws = s < a.NS ? wsplit[s] : 0.f;
-            acc.x = fmaf(ws, v[u].x, acc.x);
-            acc.y = fmaf(ws, v[u].y, acc.y);
-            acc.z = fmaf(ws, v[u].z, acc.z);
-            acc.w = fmaf(ws, v[u].w, acc.w);
-        }
+        s0 += kMergeChunk;
+        if (s0 >= a.NS) break;
+        load_chunk(c, s0);
     }
-    csum[grp][4 * c4] = acc.x;
-    csum[grp][4 * c4 + 1] = acc.y;
-    csum[grp][4 * c4 + 2] = acc.z;
-    csum[grp][4 * c4 + 3] = acc.w;
+    if (g == 1) half1[c4] = acc;
     __syncthreads();
-    if (tid < 128) {
-        float r = 0.f;
-        for (int g = 0; g < 8; ++g) r += csum[g][tid];
-        a.ctx[h * kR + quarter * 128 + tid] = r * inv_l;
+    if (g == 0) {
+        const float4 o = half1[c4];
+        *reinterpret_cast<float4 *>(ctx + 4 * c4) =
+            make_float4((acc.x + o.x) * inv_l, (acc.y + o.y) * inv_l, (acc.z + o.z) * inv_l, (acc.w + o.w) * inv_l);
     }
-}
+    __syncthreads();
 
-// grid: cdiv(H * V, 32); block: 32 output rows (8 per wave) of o[h][v] = W_UV[h][v] . ctx[h];
-// lane l covers columns 8l .. 8l+7, all 8 rows' weights in flight at once
-__global__ __launch_bounds__(256) void mla_uv_kernel(MergeArgs a) {
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int64_t rows = static_cast<int64_t>(a.H) * a.V;
-    const int64_t r0 = static_cast<int64_t>(blockIdx.x) * 32 + wave * 8;
-    uint4 w[8];
+    const float4 c0 = *reinterpret_cast<const float4 *>(ctx + lane * 8);
+    const float4 c1 = *reinterpret_cast<const float4 *>(ctx + lane * 8 + 4);
+    const float c8[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
 #pragma unroll
-    for (int u = 0; u < 8; ++u) {
-        const int64_t r = r0 + u;
-        w[u] = r < rows ? *reinterpret_cast<const uint4 *>(a.w_uv + r * kR + lane * 8) : make_uint4(0u, 0u, 0u, 0u);
-    }
-#pragma unroll
-    for (int u = 0; u < 8; ++u) {
-        const int64_t r = r0 + u;
-        const int h = static_cast<int>(min(r, rows - 1) / a.V);
-        const float4 c0 = *reinterpret_cast<const float4 *>(a.ctx + h * kR + lane * 8);
-        const float4 c1 = *reinterpret_cast<const float4 *>(a.ctx + h * kR + lane * 8 + 4);
-        const float c8[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
+    for (int u = 0; u < kMergeRows / 4; ++u) {
+        const int v = r0 + u;
         const uint32_t wd[4] = {w[u].x, w[u].y, w[u].z, w[u].w};
-        float acc = 0.f;
+        float o = 0.f;
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
-            acc = fmaf(__uint_as_float(wd[q] << 16), c8[2 * q], acc);
-            acc = fmaf(__uint_as_float(wd[q] & 0xffff0000u), c8[2 * q + 1], acc);
+            o = fmaf(__uint_as_float(wd[q] << 16), c8[2 * q], o);
+            o = fmaf(__uint_as_float(wd[q] & 0xffff0000u), c8[2 * q + 1], o);
         }
-        acc = wave_sum_to_lane63(acc);
-        if (lane == 63 && r < rows) {
-            const int64_t oi = static_cast<int64_t>(h) * a.ld_out + (r - static_cast<int64_t>(h) * a.V);
+        o = wave_sum_to_lane63(o);
+        if (lane == 63 && v < a.V) {
+            const int64_t oi = static_cast<int64_t>(h) * a.ld_out + v;
             if (a.out_bf16)
-                static_cast<uint16_t *>(a.out)[oi] = f32_to_bf16(acc);
+                static_cast<uint16_t *>(a.out)[oi] = f32_to_bf16(o);
             else
-                static_cast<float *>(a.out)[oi] = acc;
+                static_cast<float *>(a.out)[oi] = o;
         }
     }
 }
 
 // ------------------------------------------------------------------ host side
-constexpr int kPairs = 2;  // streams (wave pairs) per attention block: one wave per SIMD
-constexpr int kRing = 2;   // register buffers per wave (deeper rings measured no faster)
+#ifndef MLA_P
+#define MLA_P 2
+#endif
+#ifndef MLA_RING
+#define MLA_RING 2
+#endif
+constexpr int kPairs = MLA_P;
+constexpr int kRing = MLA_RING;
 
 // One attention block per CU: about 256 blocks of (head group, split); a split is a
 // multiple of 16 kPairs tokens, so every step of every stream lies inside it.
 void mla_splits(int64_t H, int64_t T, int *Ts, int *NS) {
     const int64_t hgn = cdiv(H, kHG);
-    const int64_t want = std::max<int64_t>(1, 256 / hgn);
+    const int64_t want = std::max<int64_t>(1, 256 * MLA_OCC / hgn);
     int64_t ts = cdiv(T, want);
     ts = cdiv(ts, kStepT * kPairs) * kStepT * kPairs;
     *Ts = static_cast<int>(ts);
@@ -619,7 +640,7 @@ void mla_splits(int64_t H, int64_t T, int *Ts, int *NS) {
 }
 
 struct MlaWs {
-    size_t qa_hi, qa_lo, ctx, part, total;
+    size_t qa_hi, qa_lo, ml, part, total;
 };
 
 MlaWs mla_ws_layout(int64_t H, int64_t T) {
@@ -630,8 +651,8 @@ MlaWs mla_ws_layout(int64_t H, int64_t T) {
     size_t o = 0;
     L.qa_hi = o, o += up(static_cast<size_t>(H) * kQaLd * 2);
     L.qa_lo = o, o += up(static_cast<size_t>(H) * kQaLd * 2);
-    L.ctx = o, o += up(static_cast<size_t>(H) * kR * 4);
-    L.part = o, o += up(static_cast<size_t>(NS) * H * kPartLd * 4);
+    L.ml = o, o += up(static_cast<size_t>(NS) * H * 8);
+    L.part = o, o += up(static_cast<size_t>(NS) * H * kR * 4);
     L.total = o;
     return L;
 }
@@ -685,6 +706,7 @@ extern "C" int k3_mla_decode_absorbed(const void *q_nope, const void *q_rot, int
     uint16_t *qa_hi = reinterpret_cast<uint16_t *>(ws + L.qa_hi);
     uint16_t *qa_lo = reinterpret_cast<uint16_t *>(ws + L.qa_lo);
     float *part = reinterpret_cast<float *>(ws + L.part);
+    float2 *ml = reinterpret_cast<float2 *>(ws + L.ml);
 
     QaArgs qa{q_nope, q_rot, ld_q, ld_q_rot, static_cast<const uint16_t *>(w_uk), qa_hi, qa_lo, static_cast<int>(H),
               static_cast<int>(nope_dim)};
@@ -705,6 +727,7 @@ extern "C" int k3_mla_decode_absorbed(const void *q_nope, const void *q_rot, int
     aa.lat_row_bytes = static_cast<uint32_t>(ld_lat * 2);
     aa.rot_row_bytes = static_cast<uint32_t>(ld_rot * 2);
     aa.part = part;
+    aa.ml = ml;
     aa.H = static_cast<int>(H);
     aa.T = static_cast<int>(T);
     aa.Ts = Ts;
@@ -723,11 +746,8 @@ extern "C" int k3_mla_decode_absorbed(const void *q_nope, const void *q_rot, int
     rc = check_hip(hipGetLastError(), "mla decode: attention launch");
     if (rc) return rc;
 
-    MergeArgs ma{part, reinterpret_cast<float *>(ws + L.ctx), static_cast<const uint16_t *>(w_uv), out, ld_out,
-                 static_cast<int>(H), NS, static_cast<int>(v_dim), out_dtype == K3_BF16};
-    mla_merge_kernel<<<dim3(static_cast<unsigned>(H * 4)), 256, 0, st>>>(ma);
-    rc = check_hip(hipGetLastError(), "mla decode: merge launch");
-    if (rc) return rc;
-    mla_uv_kernel<<<dim3(static_cast<unsigned>(cdiv(H * v_dim, 32))), 256, 0, st>>>(ma);
-    return check_hip(hipGetLastError(), "mla decode: W_UV launch");
+    MergeArgs ma{part, ml, static_cast<const uint16_t *>(w_uv), out, ld_out, static_cast<int>(H), NS,
+                 static_cast<int>(v_dim), out_dtype == K3_BF16};
+    mla_merge_uv_kernel<<<dim3(static_cast<unsigned>(H * cdiv(v_dim, kMergeRows))), 256, 0, st>>>(ma);
+    return check_hip(hipGetLastError(), "mla decode: merge and W_UV launch");
 }
