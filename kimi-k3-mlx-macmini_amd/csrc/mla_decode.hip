@@ -209,13 +209,7 @@ constexpr int kCopyRow = kHalfCols + 8; // padded LDS row of the wave's copy (52
 constexpr size_t kCopyBytes = kStepT * kCopyRow * 2;  // 8448 B per wave and slot
 constexpr float kSlack = 64.f;          // log2 headroom before the pass restarts
 constexpr int kMaxPairs = 4;
-#ifndef MLA_TRB
-#define MLA_TRB 16
-#endif
-#ifndef MLA_OCC
-#define MLA_OCC 1
-#endif
-constexpr int kTrBatch = MLA_TRB;       // transposed reads issued ahead of their products
+constexpr int kTrBatch = 16;            // transposed reads issued ahead of their products
 constexpr int kCsRow = kR + 4;          // padded LDS row of the merged context (floats)
 
 template <int P>
@@ -224,7 +218,7 @@ constexpr size_t attn_lds_bytes() {  // two copy slots per wave; the merge reuse
 }
 
 template <int P, int RING>
-__global__ __launch_bounds__(128 * P, MLA_OCC) void mla_attn_kernel(AttnArgs a) {
+__global__ __launch_bounds__(128 * P, 1) void mla_attn_kernel(AttnArgs a) {
     static_assert(P == 2 || P == 4, "pairs per block");
     static_assert(attn_lds_bytes<P>() >= static_cast<size_t>(P / 2) * 2 * 16 * 64 * 16, "merge buffers fit");
     static_assert(attn_lds_bytes<P>() >= static_cast<size_t>(kHG) * kCsRow * 4, "context staging fits");
@@ -619,20 +613,14 @@ __global__ __launch_bounds__(256) void mla_merge_uv_kernel(MergeArgs a) {
 }
 
 // ------------------------------------------------------------------ host side
-#ifndef MLA_P
-#define MLA_P 2
-#endif
-#ifndef MLA_RING
-#define MLA_RING 2
-#endif
-constexpr int kPairs = MLA_P;
-constexpr int kRing = MLA_RING;
+constexpr int kPairs = 2;  // streams (wave pairs) per attention block: one wave per SIMD
+constexpr int kRing = 2;   // register buffers per wave (deeper rings measured no faster)
 
 // One attention block per CU: about 256 blocks of (head group, split); a split is a
 // multiple of 16 kPairs tokens, so every step of every stream lies inside it.
 void mla_splits(int64_t H, int64_t T, int *Ts, int *NS) {
     const int64_t hgn = cdiv(H, kHG);
-    const int64_t want = std::max<int64_t>(1, 256 * MLA_OCC / hgn);
+    const int64_t want = std::max<int64_t>(1, 256 / hgn);
     int64_t ts = cdiv(T, want);
     ts = cdiv(ts, kStepT * kPairs) * kStepT * kPairs;
     *Ts = static_cast<int>(ts);
