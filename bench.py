@@ -427,7 +427,7 @@ def main():
         line["mla_decode"] = {"us": round(mus, 2), "GB/s": round(mgbs, 1),
                               "pct_hbm_peak": round(100 * mgbs / HBM_PEAK_GBS, 1), "bytes": MLA_BYTES,
                               "heads": MLA_H, "tokens": MLA_T, "kv_lora_rank": 512, "rope": 64,
-                              "cache": "bf16", "launches": 4, "step_us": mstats}
+                              "cache": "bf16", "launches": 3, "step_us": mstats}
     if "ceiling" in work:
         ce = bench_read_ceiling(torch, EXPERT_BYTES, 256, dev)
         cl = bench_read_ceiling(torch, LAYER_BYTES, 64, dev)
