@@ -277,6 +277,83 @@ class RoutedMoE:
         return y, r
 
 
+class LatentMoE:
+    """Drop-in for K3's routed layer, LatentMoE (air_llm/models/kimi_k3/moe.py:40-132).
+
+    ``LatentMoE(cfg, layer, w, expert_source, fused=True)`` keeps the reference constructor
+    and weight names: ``gate.weight`` [E, H] and ``gate.e_score_correction_bias`` [E]
+    (sigmoid + bias routing), ``routed_expert_down_proj.weight`` [L, H] and
+    ``routed_expert_up_proj.weight`` [H, L] (the latent projections, bf16),
+    ``routed_expert_norm.weight`` [L], ``shared_experts.{gate,up,down}_proj.weight`` (bf16;
+    K3's two shared experts are one MLP of twice the width).  ``expert_source(layer, e, which)``
+    returns latent-width MXFP4 experts (gate/up [I, L], down [L, I]).  cfg carries the
+    K3Config fields hidden_size, routed_expert_hidden_size, moe_intermediate_size,
+    num_experts, num_experts_per_token, moe_renormalize, routed_scaling_factor, situ_beta,
+    situ_linear_beta and rms_norm_eps.
+
+    ``__call__(x)`` (moe.py:110-132): route on x; h = x W_down^T in bf16 (the reference's
+    dtype); the routed experts on h, grouped by expert on the device (k3_moe_grouped_ffn,
+    no host synchronisation, SiTU); KimiRMSNorm of their weighted sum in fp32; the up
+    projection in fp32; plus the shared expert on the original x."""
+
+    def __init__(self, cfg, layer: int, w: dict, expert_source: Callable, fused: bool = True):
+        self.cfg, self.L = cfg, layer
+        self.fused = fused
+        H = int(cfg.hidden_size)
+        self.latent = int(getattr(cfg, "routed_expert_hidden_size"))
+        rcfg = MoEConfig(hidden_size=H, moe_intermediate_size=int(cfg.moe_intermediate_size),
+                         num_experts=int(cfg.num_experts), num_experts_per_token=int(cfg.num_experts_per_token),
+                         moe_renormalize=bool(cfg.moe_renormalize),
+                         routed_scaling_factor=float(cfg.routed_scaling_factor), router="sigmoid_bias",
+                         activation="situ", situ_beta=float(cfg.situ_beta),
+                         situ_linear_beta=getattr(cfg, "situ_linear_beta", None))
+        shared = {f"shared_experts.{n}_proj.weight": w[f"shared_experts.{n}_proj.weight"]
+                  for n in ("gate", "up", "down") if f"shared_experts.{n}_proj.weight" in w}
+        self._routed = RoutedMoE(rcfg, layer, {"gate.weight": w["gate.weight"],
+                                               "gate.e_score_correction_bias": w["gate.e_score_correction_bias"],
+                                               **shared}, expert_source, fused)
+        self.down = w["routed_expert_down_proj.weight"]
+        self.up = w["routed_expert_up_proj.weight"]
+        self.norm_w = w["routed_expert_norm.weight"]
+        if tuple(self.down.shape) != (self.latent, H) or tuple(self.up.shape) != (H, self.latent):
+            raise ValueError(f"latent projections must be [{self.latent}, {H}] and [{H}, {self.latent}]; got "
+                             f"{tuple(self.down.shape)}, {tuple(self.up.shape)}")
+        if self.down.dtype != torch.bfloat16 or self.up.dtype != torch.bfloat16:
+            raise TypeError("latent projections must be bfloat16")
+        T.require_device(self.down, self.up, self.norm_w)
+        self._up32 = self.up.float()      # the reference applies W_up to the fp32 normalised sum
+        self._norm32 = self.norm_w.float()
+
+    def route(self, x: torch.Tensor) -> RouterResult:
+        """Sigmoid + bias router on the hidden state (moe.py:65-76)."""
+        return self._routed.route(x)
+
+    def expert_forward(self, h: torch.Tensor, e: int) -> torch.Tensor:
+        """One routed expert on latent rows h [N, L] (moe.py:90-103)."""
+        return self._routed.expert_forward(h, e)
+
+    def shared_forward(self, x: torch.Tensor) -> torch.Tensor:
+        """Shared expert(s) on the original hidden state (moe.py:105-107)."""
+        return self._routed.shared_forward(x)
+
+    def __call__(self, x: torch.Tensor, return_router: bool = False):
+        c = self.cfg
+        orig = x.shape
+        flat = x.reshape(-1, orig[-1])
+        r = self.route(flat)
+        h = flat.to(torch.bfloat16) @ self.down.T                         # hidden -> latent
+        act, beta, lb = self._routed._act()
+        y = moe_grouped_ffn(h.contiguous(), r.expert_indices, r.expert_weights, self._routed.expert_table(),
+                            int(c.moe_intermediate_size), act, beta, lb, out_dtype=torch.float32, validate=False)
+        eps = float(c.rms_norm_eps)
+        y = self._norm32 * (y * torch.rsqrt((y * y).mean(dim=-1, keepdim=True) + eps))
+        y = y @ self._up32.T                                              # latent -> hidden
+        if self._routed.sh_gate is not None:
+            y = y + self.shared_forward(flat)
+        y = y.reshape(*orig[:-1], orig[-1])
+        return (y, r) if return_router else y
+
+
 def moe_grouped_ffn(x: torch.Tensor, expert_indices: torch.Tensor, expert_weights: torch.Tensor,
                     table: torch.Tensor, intermediate: int, act: str = "silu", beta: float = 1.0,
                     linear_beta: float | None = None, out_dtype: torch.dtype = torch.float32,

@@ -1,7 +1,6 @@
 """MoE routing / expert FFN / layer-combine oracle (test infrastructure only).
 
-Follows ``k3ref/layers.py:198-261`` (``LatentMoE``) and ``air_llm/models/kimi_k3/moe.py:65-132``
-without the K3 latent down/norm/up wrapper, which is not on the benchmarked path:
+Follows ``k3ref/layers.py:198-261`` (``LatentMoE``) and ``air_llm/models/kimi_k3/moe.py:65-132``:
 
 * ``route_softmax``     softmax over router logits, top-k, optional renormalisation by
                         ``sum + 1e-20`` and a scaling factor (the reference's weight
@@ -14,6 +13,12 @@ without the K3 latent down/norm/up wrapper, which is not on the benchmarked path
                         ``k3ref/layers.py:53-60``).
 * ``moe_layer``         weighted sum of the routed experts plus the shared expert on the
                         original hidden state (``k3ref/layers.py:241-261``).
+* ``latent_moe``        K3's layer (``moe.py:110-132``): route on the hidden state, project
+                        it to the latent width (``routed_expert_down_proj``), run the routed
+                        experts there, RMS-normalise their weighted sum
+                        (``routed_expert_norm``, ``ops.py:11-14``), project back to the hidden
+                        width (``routed_expert_up_proj``) and add the shared expert applied to
+                        the original hidden state.
 
 Everything is float64.  Ties in top-k go to the lower expert index.
 
@@ -22,7 +27,10 @@ Pinning (``tests/test_oracle_moe.py``): softmax/top-k against ``torch.softmax`` 
 (k distinct indices, weights sum to the scaling factor, selection by corrected scores,
 weights from raw scores); SwiGLU/SiTU against their closed forms at chosen points
 (silu(0)=0, silu(x)->x for large x, situ's tanh saturation at +-beta); the expert FFN
-against a brute-force per-row loop; the layer against a loop over experts.
+against a brute-force per-row loop; the layer against a loop over experts.  The latent
+layer: with identity down/up projections and unit norm weights it equals the normalised
+plain layer; the routed scaling factor cancels in the normalisation (eps = 0); it is
+linear in the up projection; a planted swap of normalisation and up projection fails.
 """
 from __future__ import annotations
 
@@ -127,3 +135,32 @@ def moe_layer(x, idx, weights, experts, shared=None, kind="silu", beta=1.0,
     if shared is not None:
         y += dense_ffn(x, *shared, kind=kind, beta=beta, linear_beta=linear_beta)[0]
     return y
+
+
+def rmsnorm(x, w, eps: float):
+    """KimiRMSNorm (``ops.py:11-14``): ``w * x / sqrt(mean(x^2) + eps)`` over the last axis."""
+    x = np.asarray(x, np.float64)
+    return np.asarray(w, np.float64) * (x / np.sqrt((x * x).mean(axis=-1, keepdims=True) + eps))
+
+
+def latent_moe(x, router_w, bias, down_w, up_w, norm_w, experts, shared, k: int,
+               renormalize: bool = True, scaling: float = 1.0, beta: float = 1.0,
+               linear_beta=None, eps: float = 1e-5, kind: str = "situ", h_bf16: bool = False):
+    """K3's routed layer (``moe.py:110-132``).
+
+    x [T, H]; router_w [E, H] and bias [E] (sigmoid + bias routing); down_w [L, H] and
+    up_w [H, L] the latent projections; norm_w [L]; ``experts[e]`` = (gate, up, down)
+    (packed, scales) pairs of latent-width experts; ``shared`` = (wg, wu, wd) dense or
+    None.  ``h_bf16`` rounds the latent state to bf16, as the reference's bf16 matmul
+    ``flat @ self.down.T`` does (``moe.py:117``).  Returns (y [T, H], idx, weights)."""
+    x = np.atleast_2d(np.asarray(x, np.float64))
+    idx, w, _, _ = route_sigmoid_bias(x, router_w, bias, k, renormalize, scaling)
+    h = x @ np.asarray(down_w, np.float64).T
+    if h_bf16:
+        from .mxfp4 import bf16_round
+        h = bf16_round(h.astype(np.float32)).astype(np.float64)
+    y = moe_layer(h, idx, w, experts, None, kind, beta, linear_beta)
+    y = rmsnorm(y, norm_w, eps) @ np.asarray(up_w, np.float64).T
+    if shared is not None:
+        y = y + dense_ffn(x, *shared, kind=kind, beta=beta, linear_beta=linear_beta)[0]
+    return y, idx, w

@@ -1,0 +1,109 @@
+"""GPU parity of K3's routed layer with the latent wrapper (LatentMoE, moe.py:110-132)
+against the fp64 oracle (``oracle.moe.latent_moe``).
+
+The latent state h = x W_down^T is bf16 in the reference (its bf16 matmul, moe.py:117) and
+here (torch's bf16 GEMM), and the oracle rounds it the same way; a 1-ulp difference in a
+few elements of h (fp32 vs fp64 accumulation before the rounding) and the grouped MFMA
+path's ~1e-4 error set the bar: normwise max-relative 5e-4 (the grouped path's own bar),
+under BASELINE's 1e-3.  The router result is compared exactly (ids) and to 1e-5 (weights).
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import moe as omoe
+from oracle import mxfp4 as om
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+TOL = 5e-4
+
+
+@dataclass
+class K3Cfg:
+    """The K3Config fields the layer reads (air_llm/models/kimi_k3/config.py:13-35)."""
+    hidden_size: int
+    routed_expert_hidden_size: int
+    moe_intermediate_size: int
+    num_experts: int
+    num_experts_per_token: int
+    moe_renormalize: bool = True
+    routed_scaling_factor: float = 2.5
+    situ_beta: float = 2.0
+    situ_linear_beta: float | None = 3.0
+    rms_norm_eps: float = 1e-5
+
+
+def make(seed, H, L, I, E, k, Is, distinct=None):
+    rng = np.random.default_rng(seed)
+    D = distinct or E
+    experts_np = [(om.random_mxfp4(rng, I, L), om.random_mxfp4(rng, I, L), om.random_mxfp4(rng, L, I))
+                  for _ in range(D)]
+    experts_dev = [tuple(tuple(torch.from_numpy(a).to(DEV) for a in pair) for pair in ex) for ex in experts_np]
+    bf = lambda a: om.bf16_round(np.asarray(a, np.float32))  # noqa: E731
+    router_w = bf(rng.standard_normal((E, H)) * 0.02)
+    bias = (rng.standard_normal(E) * 0.05).astype(np.float32)
+    down = bf(rng.standard_normal((L, H)) * 0.02)
+    up = bf(rng.standard_normal((H, L)) * 0.02)
+    norm_w = (1.0 + 0.1 * rng.standard_normal(L)).astype(np.float32)
+    shared = tuple(bf(rng.standard_normal(s) * 0.02) for s in ((Is, H), (Is, H), (H, Is)))
+    t = lambda a, dt=torch.bfloat16: torch.from_numpy(np.ascontiguousarray(a)).to(DEV).to(dt)  # noqa: E731
+    w = {"gate.weight": t(router_w), "gate.e_score_correction_bias": t(bias, torch.float32),
+         "routed_expert_down_proj.weight": t(down), "routed_expert_up_proj.weight": t(up),
+         "routed_expert_norm.weight": t(norm_w, torch.float32),
+         "shared_experts.gate_proj.weight": t(shared[0]), "shared_experts.up_proj.weight": t(shared[1]),
+         "shared_experts.down_proj.weight": t(shared[2])}
+    which_ix = {"w1": 0, "w3": 1, "w2": 2}
+
+    def source(layer, e, which):
+        return experts_dev[e % D][which_ix[which]]
+
+    oracle_args = (router_w, bias, down, up, norm_w, {e: experts_np[e % D] for e in range(E)}, shared)
+    return w, source, oracle_args
+
+
+def check(cfg, seed, T, distinct=None):
+    from k3hip.moe import LatentMoE
+    w, source, (router_w, bias, down, up, norm_w, experts, shared) = make(
+        seed, cfg.hidden_size, cfg.routed_expert_hidden_size, cfg.moe_intermediate_size, cfg.num_experts,
+        cfg.num_experts_per_token, 2 * cfg.moe_intermediate_size, distinct)
+    moe = LatentMoE(cfg, 0, w, source)
+    rng = np.random.default_rng(seed + 1)
+    x = om.bf16_round(rng.standard_normal((T, cfg.hidden_size)).astype(np.float32))
+    y, r = moe(torch.from_numpy(x).to(DEV).to(torch.bfloat16), return_router=True)
+    want, idx, wts = omoe.latent_moe(x, router_w, bias, down, up, norm_w, experts, shared,
+                                     cfg.num_experts_per_token, cfg.moe_renormalize, cfg.routed_scaling_factor,
+                                     cfg.situ_beta, cfg.situ_linear_beta, cfg.rms_norm_eps, h_bf16=True)
+    assert np.array_equal(r.expert_indices.cpu().numpy(), idx)
+    assert np.allclose(r.expert_weights.cpu().numpy(), wts, rtol=1e-5, atol=1e-7)
+    rel = om.normwise_rel(y.float().cpu().numpy(), want)
+    print(f"T={T} E={cfg.num_experts} k={cfg.num_experts_per_token} rel={rel:.2e}")
+    assert rel <= TOL, rel
+
+
+@pytest.mark.parametrize("T", [1, 5])
+def test_latent_moe_small(T):
+    check(K3Cfg(hidden_size=256, routed_expert_hidden_size=128, moe_intermediate_size=128, num_experts=16,
+                num_experts_per_token=4), seed=40 + T, T=T)
+
+
+def test_latent_moe_k3_shapes_decode():
+    """K3's routed layer shapes: hidden 7168, latent 3584, experts [3072 x 3584], top-16 of
+    896 (four distinct expert weight sets behind the 896 table rows), two shared experts
+    (one MLP of width 6144); one decode token."""
+    check(K3Cfg(hidden_size=7168, routed_expert_hidden_size=3584, moe_intermediate_size=3072, num_experts=896,
+                num_experts_per_token=16), seed=50, T=1, distinct=4)
+
+
+def test_latent_moe_rejects_wrong_projection_shapes():
+    from k3hip.moe import LatentMoE
+    cfg = K3Cfg(hidden_size=256, routed_expert_hidden_size=128, moe_intermediate_size=128, num_experts=8,
+                num_experts_per_token=2)
+    w, source, _ = make(3, 256, 128, 128, 8, 2, 256)
+    w["routed_expert_up_proj.weight"] = w["routed_expert_up_proj.weight"][:, :64]
+    with pytest.raises(ValueError):
+        LatentMoE(cfg, 0, w, source)

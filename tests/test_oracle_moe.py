@@ -177,3 +177,60 @@ def test_moe_layer_vs_token_slot_loop():
     w_raw = np.take_along_axis(omoe.route_softmax(x, wr, k, renormalize=False)[2], idx, axis=-1)
     bad = omoe.moe_layer(x, idx, w_raw, experts, shared=shared)
     assert om.normwise_rel(bad, want) > 1e-2
+
+
+# ------------------------------------------------------------------------- latent layer
+def _latent_case(seed=31, H=96, L=64, I=32, E=8, k=3, T=3, Is=40):
+    rng = np.random.default_rng(seed)
+    experts = [(om.random_mxfp4(rng, I, L, 122, 126), om.random_mxfp4(rng, I, L, 122, 126),
+                om.random_mxfp4(rng, L, I, 122, 126)) for _ in range(E)]
+    shared = tuple(rng.standard_normal(s) * 0.05 for s in ((Is, H), (Is, H), (H, Is)))
+    x = rng.standard_normal((T, H))
+    wr = rng.standard_normal((E, H)) * 0.1
+    bias = rng.standard_normal(E) * 0.05
+    down = rng.standard_normal((L, H)) * 0.1
+    up = rng.standard_normal((H, L)) * 0.1
+    norm_w = 1.0 + 0.1 * rng.standard_normal(L)
+    return x, wr, bias, down, up, norm_w, experts, shared, k
+
+
+def test_rmsnorm_closed_form_and_torch():
+    """rms_norm of torch (a library routine) and a constant vector (x / |x_i| * w)."""
+    rng = np.random.default_rng(3)
+    x = rng.standard_normal((4, 33))
+    w = rng.standard_normal(33)
+    want = torch.nn.functional.rms_norm(torch.from_numpy(x), (33,), torch.from_numpy(w), eps=1e-5).numpy()
+    assert np.allclose(omoe.rmsnorm(x, w, 1e-5), want, rtol=1e-12, atol=1e-12)
+    c = np.full((1, 8), -3.0)
+    assert np.allclose(omoe.rmsnorm(c, np.arange(8.0), 0.0), -np.arange(8.0)[None, :], rtol=1e-14)
+
+
+def test_latent_layer_reduces_to_normalised_plain_layer():
+    """Identity down/up projections and unit norm weights: the latent layer is
+    rmsnorm(plain routed layer) + shared, routed by the same sigmoid + bias router."""
+    x, wr, bias, _, _, _, experts, shared, k = _latent_case(H=64, L=64)
+    eye = np.eye(64)
+    got, idx, w = omoe.latent_moe(x, wr, bias, eye, eye, np.ones(64), experts, shared, k, eps=1e-6)
+    r_idx, r_w, _, _ = omoe.route_sigmoid_bias(x, wr, bias, k)
+    assert np.array_equal(idx, r_idx) and np.allclose(w, r_w, rtol=1e-14)
+    plain = omoe.moe_layer(x, idx, w, experts, None, "situ")
+    want = plain / np.sqrt((plain * plain).mean(axis=-1, keepdims=True) + 1e-6)
+    want = want + omoe.dense_ffn(x, *shared, kind="situ")[0]
+    assert om.normwise_rel(got, want) < 1e-12
+
+
+def test_latent_layer_invariants_and_planted_mistake():
+    """The routed scaling factor cancels in the normalisation (eps = 0); the layer is
+    linear in the up projection; normalising after the up projection (a plausible slip)
+    changes the result."""
+    x, wr, bias, down, up, norm_w, experts, shared, k = _latent_case()
+    a = omoe.latent_moe(x, wr, bias, down, up, norm_w, experts, shared, k, scaling=1.0, eps=0.0)[0]
+    b = omoe.latent_moe(x, wr, bias, down, up, norm_w, experts, shared, k, scaling=2.5, eps=0.0)[0]
+    assert om.normwise_rel(a, b) < 1e-12
+    sh = omoe.dense_ffn(x, *shared, kind="situ")[0]
+    c = omoe.latent_moe(x, wr, bias, down, 3.0 * up, norm_w, experts, shared, k, eps=0.0)[0]
+    assert om.normwise_rel(c - sh, 3.0 * (a - sh)) < 1e-12
+    idx, w, _, _ = omoe.route_sigmoid_bias(x, wr, bias, k)
+    y = omoe.moe_layer(x @ down.T, idx, w, experts, None, "situ") @ up.T
+    bad = omoe.rmsnorm(y, np.ones(up.shape[0]), 0.0) + sh
+    assert om.normwise_rel(bad, a) > 1e-2
