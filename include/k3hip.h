@@ -160,6 +160,31 @@ int k3_moe_grouped_ffn(const void *x, int x_dtype, const int32_t *expert_idx, co
                        int64_t I, int64_t n_experts, int64_t top_k, int act_kind, float beta,
                        float linear_beta, void *workspace, int64_t workspace_bytes, void *stream);
 
+/* Workspace bytes for k3_moe_latent_layer_decode: the k3_moe_layer_decode records plus the
+ * bf16 latent state and the fp32 routed sum.  Same counter rule as k3_moe_layer_workspace_size
+ * (first 256 bytes zero before the first call; every call returns them to zero). */
+int64_t k3_moe_latent_layer_workspace_size(int64_t H, int64_t latent, int64_t I, int64_t shared_I,
+                                           int64_t n_experts, int64_t top_k);
+
+/* K3's routed layer with its latent wrapper for one token (bf16 x [H]):
+ *   route (sigmoid + bias, as k3_moe_route) on x;
+ *   h = bf16(latent_down . x)                         latent_down bf16 [latent, H]
+ *   y = sum_j w_j * expert_{idx_j}(h)                 experts of width latent (expert_table)
+ *   out = latent_up . (latent_norm * y / sqrt(mean(y^2) + eps)) + shared(x)
+ * latent_up bf16 [H, latent], latent_norm fp32 [latent]; shared_* as in k3_moe_layer_decode
+ * (K3's two shared experts are one MLP of width shared_I).  Four stream-ordered launches,
+ * no device-to-host synchronisation.  latent, I, shared_I multiples of 128, H <= 8192,
+ * top_k <= 16, n_experts <= 1024.
+ * Replaces LatentMoE.__call__ (air_llm/models/kimi_k3/moe.py:110-132) at batch 1, including
+ * the latent down/norm/up wrapper (moe.py:116,129-130). */
+int k3_moe_latent_layer_decode(const void *x, const void *router_w, const void *router_bias, int renormalize,
+                               float scaling, const void *expert_table, const void *latent_down,
+                               const void *latent_up, const void *latent_norm, float eps,
+                               const void *shared_gate, const void *shared_up, const void *shared_down,
+                               void *out, int out_dtype, int64_t H, int64_t latent, int64_t I,
+                               int64_t shared_I, int64_t n_experts, int64_t top_k, int act_kind, float beta,
+                               float linear_beta, void *workspace, int64_t workspace_bytes, void *stream);
+
 /* ---- latent-MLA absorbed decode (one query token, batch 1) ------------------------------ */
 
 /* Workspace bytes k3_mla_decode_absorbed needs for H heads over T cached tokens (qa

@@ -41,6 +41,8 @@ struct LayerWs {
     float *yshared;      // [H]
     uint64_t *sel_ptrs;  // [k][6] weight pointers of the selected experts
     uint32_t *counter;   // router blocks done in this launch (returns to 0 after each)
+    uint16_t *h;         // [Hr] bf16 latent state (latent layer)
+    float *ylat;         // [Hr] routed sum in latent space (latent layer)
 };
 
 struct LayerArgs {
@@ -59,11 +61,21 @@ struct LayerArgs {
     int out_bf16;
     int l1_router_blocks;          // L1: blocks [0, l1_router_blocks) do router rows
     int l2_shared_blocks;          // L2: blocks [0, l2_shared_blocks) do shared down rows
+    // K3's latent wrapper (moe.py:116,129-130); lat_down == null: the plain layer
+    int Hr;                        // width the routed experts read and write (H, or the latent width)
+    const uint16_t *lat_down;      // [Hr, H] bf16: h = x W_down^T, rounded to bf16
+    const uint16_t *lat_up;        // [H, Hr] bf16
+    const float *lat_norm;         // [Hr] KimiRMSNorm weight
+    float eps;
+    int l1_latent_blocks;          // L1: the next blocks do latent down rows (4 per block)
 };
 
 constexpr int kMaxTopK = 16;
 constexpr int kMaxExperts = 1024;
-constexpr int kSharedDownRows = 2;  // shared down rows per wave (L2)
+constexpr int kSharedDownRows = 2;  // shared down rows per wave (L2; L4)
+// shared down rows per wave for CHI chunks per lane: one row past 8 chunks (wide shared
+// experts), so the fp32 activation and the rows stay in registers
+constexpr int shared_down_rows(int chi) { return chi > 8 ? 1 : kSharedDownRows; }
 constexpr int kRoutedPairs = 2;     // routed (gate, up) row pairs per wave (L2)
 
 // ------------------------------------------------------------------ bf16 row dots
@@ -347,11 +359,36 @@ __global__ __launch_bounds__(256) void layer_l1(LayerArgs a) {
         }
         __syncthreads();
         if (last_s) route_block(a);
+    } else if (static_cast<int>(blockIdx.x) < a.l1_router_blocks + a.l1_latent_blocks) {
+        // latent down rows: h[l] = bf16(W_down[l] . x), the reference's bf16 matmul
+        const int l = (blockIdx.x - a.l1_router_blocks) * 4 + wave;
+        const auto r = make_rsrc(a.lat_down, static_cast<uint32_t>(a.Hr) * row_bytes);
+        uint4 w[CHH];
+#pragma unroll
+        for (int u = 0; u < CHH; ++u) {
+            const int c = u * 64 + lane;
+            w[u] = buf_load16(r, (l < a.Hr && c < nch) ? static_cast<uint32_t>(l) * row_bytes + c * 16u : kOobOffset);
+        }
+        x_store<XT, XREG, false>(smem, xr);
+        __syncthreads();
+        float acc0 = 0.f, acc1 = 0.f;
+#pragma unroll
+        for (int u = 0; u < CHH; ++u) {
+            const int c = u * 64 + lane;
+            if (c < nch) {
+                if (u & 1)
+                    acc1 = dot_chunk<XT>(w[u], smem, c, acc1);
+                else
+                    acc0 = dot_chunk<XT>(w[u], smem, c, acc0);
+            }
+        }
+        const float tot = wave_sum_to_lane63(acc0 + acc1);
+        if (lane == 63 && l < a.Hr) a.ws.h[l] = f32_to_bf16(tot);
     } else {
         // ~0.2 us head start for the router rows' loads (issued by the first blocks): the
         // router blocks then finish early and the routing block runs under this stream
         __builtin_amdgcn_s_sleep(8);
-        const int i = (blockIdx.x - a.l1_router_blocks) * 4 + wave;
+        const int i = (blockIdx.x - a.l1_router_blocks - a.l1_latent_blocks) * 4 + wave;
         const bool v = i < a.Is;
         const auto rg = make_rsrc(a.sh_gate, static_cast<uint32_t>(a.Is) * row_bytes);
         const auto ru = make_rsrc(a.sh_up, static_cast<uint32_t>(a.Is) * row_bytes);
@@ -390,7 +427,8 @@ __global__ __launch_bounds__(256) void layer_l2(LayerArgs a) {
         // shared down: kSharedDownRows bf16 rows [H, Is] per wave against the fp32 shared act,
         // which each lane holds in registers for its own chunks (L2-resident after the first
         // waves)
-        const int n0 = (blockIdx.x * 4 + wave) * kSharedDownRows;
+        constexpr int SDR = shared_down_rows(CHI);
+        const int n0 = (blockIdx.x * 4 + wave) * SDR;
         const uint32_t row_bytes = static_cast<uint32_t>(a.Is) * 2u;
         const int nch = a.Is >> 3;
         const auto ra = make_rsrc(a.ws.shared_act, static_cast<uint32_t>(a.Is) * 4u);
@@ -403,9 +441,9 @@ __global__ __launch_bounds__(256) void layer_l2(LayerArgs a) {
             av[u][1] = __builtin_bit_cast(float4, buf_load16(ra, ok ? c * 32u + 16u : kOobOffset));
         }
         const auto rr = make_rsrc(a.sh_down, static_cast<uint32_t>(a.H) * row_bytes);
-        uint4 w[kSharedDownRows][CHI];
+        uint4 w[SDR][CHI];
 #pragma unroll
-        for (int r = 0; r < kSharedDownRows; ++r)
+        for (int r = 0; r < SDR; ++r)
 #pragma unroll
             for (int u = 0; u < CHI; ++u) {
                 const int c = u * 64 + lane, n = n0 + r;
@@ -413,7 +451,7 @@ __global__ __launch_bounds__(256) void layer_l2(LayerArgs a) {
                                                                 : kOobOffset);
             }
 #pragma unroll
-        for (int r = 0; r < kSharedDownRows; ++r) {
+        for (int r = 0; r < SDR; ++r) {
             float acc = 0.f;
 #pragma unroll
             for (int u = 0; u < CHI; ++u) acc = dot8(w[r][u], av[u][0], av[u][1], acc);
@@ -422,13 +460,14 @@ __global__ __launch_bounds__(256) void layer_l2(LayerArgs a) {
         }
         return;
     }
-    // routed gate/up: kRoutedPairs (slot j, row i) pairs per wave
+    // routed gate/up: kRoutedPairs (slot j, row i) pairs per wave, over the routed input
+    // (x, or the bf16 latent state h, which the host pairs with XT = bf16)
     constexpr int CPGX = XTile<XT>::kChunks;
     constexpr int XREG = x_regs<XT>();
-    const int GH = a.H >> 5;
-    const uint32_t rowA = static_cast<uint32_t>(a.H >> 1);
+    const int GH = a.Hr >> 5;
+    const uint32_t rowA = static_cast<uint32_t>(a.Hr >> 1);
     uint4 xr[XREG];
-    x_load<XREG>(xr, a.x, GH * CPGX);
+    x_load<XREG>(xr, a.lat_down ? static_cast<const void *>(a.ws.h) : a.x, GH * CPGX);
     uint4 wg[kRoutedPairs][GA], wu[kRoutedPairs][GA];
     uint32_t sg[kRoutedPairs][GA], su[kRoutedPairs][GA];
     int jj[kRoutedPairs], ii[kRoutedPairs];
@@ -488,58 +527,135 @@ __global__ __launch_bounds__(256) void layer_l2(LayerArgs a) {
 // values of its GB groups of expert j in registers (fp32, loaded from the workspace); the
 // block combines the experts' row totals in slot order.
 template <int KT, int RPW, int GB>
-__global__ __launch_bounds__(KT * 64) void layer_l3(LayerArgs a) {
+__global__ __launch_bounds__((KT > 8 ? 8 : KT) * 64) void layer_l3(LayerArgs a) {
+    // up to 8 waves; with 16 slots each wave takes slots w and w + 8 one after the other, so a
+    // block keeps RPW rows per expert without the register budget of 16 waves
+    constexpr int NW = KT > 8 ? 8 : KT, EPW = KT / NW;
     __shared__ float ys[RPW][KT];
-    const int j = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
-    const bool live = j < a.k;  // waves past top_k idle (KT rounds top_k up)
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
     const int GI = a.I >> 5;
     const uint32_t rowB = static_cast<uint32_t>(a.I >> 1);
     const int n0 = blockIdx.x * RPW;
-    // 1. the expert's down-projection pointers, then its act for this lane's groups (8 chunks
-    //    of 4 floats per group)
-    const uint64_t *t = a.ws.sel_ptrs + (live ? j : 0) * 6;
-    const auto rd = make_rsrc(uniform_ptr(t[4]), static_cast<uint32_t>(a.H) * rowB);
-    const auto rds = make_rsrc(uniform_ptr(t[5]), static_cast<uint32_t>(a.H * GI));
-    const auto ra = make_rsrc(a.ws.act + static_cast<int64_t>(live ? j : 0) * a.I, static_cast<uint32_t>(a.I) * 4u);
-    float4 av[GB][8];
-#pragma unroll
-    for (int u = 0; u < GB; ++u) {
-        const int g = u * 64 + lane;
-#pragma unroll
-        for (int q = 0; q < 8; ++q)
-            av[u][q] = __builtin_bit_cast(float4, buf_load16(ra, (live && g < GI) ? static_cast<uint32_t>(g) * 128u + q * 16u
-                                                                                   : kOobOffset));
-    }
-    // 2. the expert's down rows of this block, and their scale bytes
-    uint4 wd[RPW][GB];
-    uint32_t sd[RPW][GB];
-#pragma unroll
-    for (int r = 0; r < RPW; ++r)
+#pragma unroll 1
+    for (int e2 = 0; e2 < EPW; ++e2) {
+        const int j = wave + NW * e2;
+        const bool live = j < a.k;  // slots past top_k idle (KT rounds top_k up)
+        // 1. the expert's down-projection pointers, then its act for this lane's groups (8
+        //    chunks of 4 floats per group)
+        const uint64_t *t = a.ws.sel_ptrs + (live ? j : 0) * 6;
+        const auto rd = make_rsrc(uniform_ptr(t[4]), static_cast<uint32_t>(a.Hr) * rowB);
+        const auto rds = make_rsrc(uniform_ptr(t[5]), static_cast<uint32_t>(a.Hr * GI));
+        const auto ra = make_rsrc(a.ws.act + static_cast<int64_t>(live ? j : 0) * a.I, static_cast<uint32_t>(a.I) * 4u);
+        float4 av[GB][8];
 #pragma unroll
         for (int u = 0; u < GB; ++u) {
-            const int n = n0 + r, g = u * 64 + lane;
-            const bool ok = live && n < a.H && g < GI;
-            wd[r][u] = buf_load16(rd, ok ? static_cast<uint32_t>(n) * rowB + g * 16u : kOobOffset);
-            sd[r][u] = __builtin_amdgcn_raw_buffer_load_b8(rds, ok ? static_cast<uint32_t>(n * GI + g) : kOobOffset, 0, 0);
+            const int g = u * 64 + lane;
+#pragma unroll
+            for (int q = 0; q < 8; ++q)
+                av[u][q] = __builtin_bit_cast(
+                    float4, buf_load16(ra, (live && g < GI) ? static_cast<uint32_t>(g) * 128u + q * 16u : kOobOffset));
         }
-    // 3. row dots; wave totals to LDS
+        // 2. the expert's down rows of this block, and their scale bytes
+        uint4 wd[RPW][GB];
+        uint32_t sd[RPW][GB];
 #pragma unroll
-    for (int r = 0; r < RPW; ++r) {
-        float acc = 0.f;
+        for (int r = 0; r < RPW; ++r)
 #pragma unroll
-        for (int u = 0; u < GB; ++u)
-            if (u * 64 + lane < GI) acc = fmaf(group_dot(wd[r][u], av[u]), e8m0_to_f32(sd[r][u]), acc);
-        const float tot = wave_sum_to_lane63(acc);
-        if (lane == 63) ys[r][j] = tot;
+            for (int u = 0; u < GB; ++u) {
+                const int n = n0 + r, g = u * 64 + lane;
+                const bool ok = live && n < a.Hr && g < GI;
+                wd[r][u] = buf_load16(rd, ok ? static_cast<uint32_t>(n) * rowB + g * 16u : kOobOffset);
+                sd[r][u] = __builtin_amdgcn_raw_buffer_load_b8(rds, ok ? static_cast<uint32_t>(n * GI + g) : kOobOffset,
+                                                               0, 0);
+            }
+        // 3. row dots; wave totals to LDS
+#pragma unroll
+        for (int r = 0; r < RPW; ++r) {
+            float acc = 0.f;
+#pragma unroll
+            for (int u = 0; u < GB; ++u)
+                if (u * 64 + lane < GI) acc = fmaf(group_dot(wd[r][u], av[u]), e8m0_to_f32(sd[r][u]), acc);
+            const float tot = wave_sum_to_lane63(acc);
+            if (lane == 63) ys[r][j] = tot;
+        }
     }
     __syncthreads();
-    // 4. combine in slot order with the shared expert's row
+    // 4. combine in slot order with the shared expert's row (latent layer: the routed sum
+    // in latent space, for the norm and up projection of L4)
     if (static_cast<int>(threadIdx.x) < RPW) {
         const int r = threadIdx.x, n = n0 + r;
-        if (n < a.H) {
+        if (n < a.Hr) {
             float y = 0.f;
             for (int jj = 0; jj < a.k; ++jj) y = fmaf(a.ws.topk_w[jj], ys[r][jj], y);
+            if (a.lat_down) {
+                a.ws.ylat[n] = y;
+                return;
+            }
             if (a.sh_down) y += a.ws.yshared[n];
+            if (a.out_bf16)
+                static_cast<uint16_t *>(a.out)[n] = f32_to_bf16(y);
+            else
+                static_cast<float *>(a.out)[n] = y;
+        }
+    }
+}
+
+
+// ------------------------------------------------------------------ L4 (latent layer)
+// out[n] = W_up[n] . (norm * ylat / sqrt(mean(ylat^2) + eps)) + yshared[n]   (moe.py:129-131;
+// KimiRMSNorm, ops.py:11-14).  Block: 4 waves x kSharedDownRows rows of W_up [H, Hr].  Every
+// wave holds the whole latent vector (lane l: chunks l, l + 64, ... of 8 values), so its
+// sum of squares is one wave reduction and no block barrier is needed.
+template <int CHU>
+__global__ __launch_bounds__(256) void layer_l4(LayerArgs a) {
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int n0 = (blockIdx.x * 4 + wave) * kSharedDownRows;
+    const uint32_t row_bytes = static_cast<uint32_t>(a.Hr) * 2u;
+    const int nch = a.Hr >> 3;
+    // 1. the latent sum and the norm weight (L2-resident), then the up rows
+    const auto ry = make_rsrc(a.ws.ylat, static_cast<uint32_t>(a.Hr) * 4u);
+    const auto rn = make_rsrc(a.lat_norm, static_cast<uint32_t>(a.Hr) * 4u);
+    float4 yv[CHU][2], nv[CHU][2];
+#pragma unroll
+    for (int u = 0; u < CHU; ++u) {
+        const int c = u * 64 + lane;
+        const bool ok = c < nch;
+#pragma unroll
+        for (int q = 0; q < 2; ++q) {
+            yv[u][q] = __builtin_bit_cast(float4, buf_load16(ry, ok ? c * 32u + q * 16u : kOobOffset));
+            nv[u][q] = __builtin_bit_cast(float4, buf_load16(rn, ok ? c * 32u + q * 16u : kOobOffset));
+        }
+    }
+    const auto rr = make_rsrc(a.lat_up, static_cast<uint32_t>(a.H) * row_bytes);
+    uint4 w[kSharedDownRows][CHU];
+#pragma unroll
+    for (int r = 0; r < kSharedDownRows; ++r)
+#pragma unroll
+        for (int u = 0; u < CHU; ++u) {
+            const int c = u * 64 + lane, n = n0 + r;
+            w[r][u] = buf_load16(rr, (n < a.H && c < nch) ? static_cast<uint32_t>(n) * row_bytes + c * 16u : kOobOffset);
+        }
+    // 2. 1 / rms of the latent sum (every wave, the full vector); norm weight folded in
+    float ss = 0.f;
+#pragma unroll
+    for (int u = 0; u < CHU; ++u)
+#pragma unroll
+        for (int q = 0; q < 2; ++q) {
+            const float4 y = yv[u][q];
+            ss = fmaf(y.x, y.x, fmaf(y.y, y.y, fmaf(y.z, y.z, fmaf(y.w, y.w, ss))));
+            yv[u][q] = make_float4(y.x * nv[u][q].x, y.y * nv[u][q].y, y.z * nv[u][q].z, y.w * nv[u][q].w);
+        }
+    const float rs = 1.0f / sqrtf(wave_sum_all(ss) / static_cast<float>(a.Hr) + a.eps);
+    // 3. up rows . normalised latent, plus the shared experts' row
+#pragma unroll
+    for (int r = 0; r < kSharedDownRows; ++r) {
+        float acc = 0.f;
+#pragma unroll
+        for (int u = 0; u < CHU; ++u) acc = dot8(w[r][u], yv[u][0], yv[u][1], acc);
+        const float t = wave_sum_to_lane63(acc);
+        const int n = n0 + r;
+        if (lane == 63 && n < a.H) {
+            const float y = t * rs + (a.sh_down ? a.ws.yshared[n] : 0.f);
             if (a.out_bf16)
                 static_cast<uint16_t *>(a.out)[n] = f32_to_bf16(y);
             else
@@ -550,7 +666,7 @@ __global__ __launch_bounds__(KT * 64) void layer_l3(LayerArgs a) {
 
 // ------------------------------------------------------------------ host side
 struct LayerWsLayout {
-    size_t logits, scores, corrected, idx, w, shared_act, act, yshared, ptrs, counter, total;
+    size_t logits, scores, corrected, idx, w, shared_act, act, yshared, ptrs, counter, h, ylat, total;
 };
 
 static size_t up256(size_t v) { return (v + 255) & ~size_t(255); }
@@ -558,7 +674,7 @@ static size_t up256(size_t v) { return (v + 255) & ~size_t(255); }
 // The router-block counter sits in the first 256 bytes for every shape, so workspaces
 // shared by layers of different shapes keep it at one place (zero between calls); the
 // records after it are rewritten by every call.
-static LayerWsLayout layer_ws_layout(int64_t H, int64_t I, int64_t Is, int64_t E, int64_t k) {
+static LayerWsLayout layer_ws_layout(int64_t H, int64_t I, int64_t Is, int64_t E, int64_t k, int64_t Hr = 0) {
     LayerWsLayout L{};
     size_t o = 0;
     L.counter = o, o += 256;
@@ -571,6 +687,8 @@ static LayerWsLayout layer_ws_layout(int64_t H, int64_t I, int64_t Is, int64_t E
     L.act = o, o += up256(k * I * 4);
     L.yshared = o, o += up256(H * 4);
     L.ptrs = o, o += up256(k * 6 * 8);
+    L.h = o, o += up256(Hr * 2);
+    L.ylat = o, o += up256(Hr * 4);
     L.total = o;
     return L;
 }
@@ -579,7 +697,8 @@ template <typename XT>
 static int launch_l1(LayerArgs &a, bool with_shared, hipStream_t st) {
     const int chh = static_cast<int>(cdiv(a.H / 8, 64));
     a.l1_router_blocks = static_cast<int>(cdiv(a.E, 4));
-    const int blocks = a.l1_router_blocks + (with_shared ? static_cast<int>(cdiv(a.Is, 4)) : 0);
+    a.l1_latent_blocks = a.lat_down ? static_cast<int>(cdiv(a.Hr, 4)) : 0;
+    const int blocks = a.l1_router_blocks + a.l1_latent_blocks + (with_shared ? static_cast<int>(cdiv(a.Is, 4)) : 0);
     const size_t lds = static_cast<size_t>(256) * x_regs<XT>() * 16;
 #define K3_L1(C) \
     if (chh <= C) { \
@@ -591,18 +710,35 @@ static int launch_l1(LayerArgs &a, bool with_shared, hipStream_t st) {
     return set_error(K3_ERR_SHAPE, "moe layer: H=%d too wide", a.H);
 }
 
+// L4 of the latent layer (nothing to do for the plain layer)
+static int launch_l4(const LayerArgs &a, hipStream_t st) {
+    if (!a.lat_down) return K3_OK;
+    const dim3 g4(static_cast<unsigned>(cdiv(a.H, 4 * kSharedDownRows)));
+    const int chu = static_cast<int>(cdiv(a.Hr / 8, 64));
+    if (chu <= 4)
+        layer_l4<4><<<g4, 256, 0, st>>>(a);
+    else if (chu <= 8)
+        layer_l4<8><<<g4, 256, 0, st>>>(a);
+    else if (chu <= 16)
+        layer_l4<16><<<g4, 256, 0, st>>>(a);
+    else
+        return set_error(K3_ERR_SHAPE, "moe latent layer: latent width %d too wide", a.Hr);
+    return check_hip(hipGetLastError(), "moe latent layer L4");
+}
+
 template <typename XT>
 static int launch_layer(LayerArgs &a, hipStream_t st) {
-    const int GH = a.H / 32, GI = a.I / 32;
+    const int GH = a.Hr / 32, GI = a.I / 32;
     const int chi = static_cast<int>(cdiv(a.Is / 8, 64));
     const int ga = GH <= 64 ? 1 : (GH <= 128 ? 2 : (GH <= 256 ? 4 : 0));
     const int gb = GI <= 64 ? 1 : (GI <= 128 ? 2 : 0);
-    if (!ga || !gb || (a.sh_down && chi > 8))
+    if (!ga || !gb || (a.sh_down && chi > 16))
         return set_error(K3_ERR_SHAPE, "moe layer: H=%d I=%d Is=%d outside the kernels' range", a.H, a.I, a.Is);
     int rc = launch_l1<XT>(a, a.sh_gate != nullptr, st);
     if (rc) return rc;
     // L2
-    a.l2_shared_blocks = a.sh_down ? static_cast<int>(cdiv(a.H, 4 * kSharedDownRows)) : 0;
+    const int chi_l2 = chi <= 4 ? 4 : (chi <= 8 ? 8 : 16);
+    a.l2_shared_blocks = a.sh_down ? static_cast<int>(cdiv(a.H, 4 * shared_down_rows(chi_l2))) : 0;
     const int routed_blocks = static_cast<int>(cdiv(static_cast<int64_t>(a.k) * a.I, 4 * kRoutedPairs));
     const size_t lds2 = static_cast<size_t>(256) * x_regs<XT>() * 16;
     const dim3 g2(static_cast<unsigned>(a.l2_shared_blocks + routed_blocks));
@@ -610,20 +746,23 @@ static int launch_layer(LayerArgs &a, hipStream_t st) {
     if (ga == G_ && (chi <= C_ || !a.sh_down)) { \
         layer_l2<XT, G_, C_><<<g2, 256, lds2, st>>>(a); \
     } else
-    K3_L2(1, 4) K3_L2(1, 8) K3_L2(2, 4) K3_L2(2, 8) K3_L2(4, 4) K3_L2(4, 8) {
+    K3_L2(1, 4) K3_L2(1, 8) K3_L2(1, 16) K3_L2(2, 4) K3_L2(2, 8) K3_L2(2, 16) K3_L2(4, 4) K3_L2(4, 8)
+    K3_L2(4, 16) {
         return set_error(K3_ERR_SHAPE, "moe layer: no L2 kernel for H=%d Is=%d", a.H, a.Is);
     }
 #undef K3_L2
     rc = check_hip(hipGetLastError(), "moe layer L2");
     if (rc) return rc;
-    // L3: rows per block so each wave streams a few KiB of its expert's down rows
+    // L3: rows per block so each wave streams a few KiB of its expert's down rows (half as
+    // many for two slots per wave of two groups per lane, within 256 registers)
     constexpr int R = 16;
-    const dim3 g3(static_cast<unsigned>(cdiv(a.H, R)));
     const int kt = a.k <= 1 ? 1 : (a.k <= 2 ? 2 : (a.k <= 4 ? 4 : (a.k <= 8 ? 8 : 16)));
 #define K3_L3(KT_, GB_) \
     if (kt == KT_ && gb == GB_) { \
-        layer_l3<KT_, R, GB_><<<g3, KT_ * 64, 0, st>>>(a); \
-        return check_hip(hipGetLastError(), "moe layer L3"); \
+        constexpr int R_ = KT_ > 8 && GB_ > 1 ? R / 2 : R; \
+        layer_l3<KT_, R_, GB_><<<dim3(static_cast<unsigned>(cdiv(a.Hr, R_))), (KT_ > 8 ? 8 : KT_) * 64, 0, st>>>(a); \
+        rc = check_hip(hipGetLastError(), "moe layer L3"); \
+        return rc ? rc : launch_l4(a, st); \
     }
     K3_L3(1, 1) K3_L3(2, 1) K3_L3(4, 1) K3_L3(8, 1) K3_L3(16, 1)
     K3_L3(1, 2) K3_L3(2, 2) K3_L3(4, 2) K3_L3(8, 2) K3_L3(16, 2)
@@ -644,9 +783,23 @@ static int layer_impl(const void *x, int x_dtype, const void *router_w, const vo
                       int renormalize, float scaling, const void *expert_table, const void *shared_gate,
                       const void *shared_up, const void *shared_down, void *out, int out_dtype, int64_t H, int64_t I,
                       int64_t shared_I, int64_t n_experts, int64_t top_k, int act_kind, float beta, float linear_beta,
-                      void *workspace, int64_t workspace_bytes, void *stream, bool route_only_flag) {
+                      void *workspace, int64_t workspace_bytes, void *stream, bool route_only_flag,
+                      const void *lat_down = nullptr, const void *lat_up = nullptr, const void *lat_norm = nullptr,
+                      float eps = 0.f, int64_t latent = 0) {
     if (!x || !router_w || !workspace || (!route_only_flag && (!expert_table || !out)))
         return set_error(K3_ERR_NULL, "moe layer: null pointer");
+    const bool lat = lat_down != nullptr;
+    if (lat) {
+        if (!lat_up || !lat_norm) return set_error(K3_ERR_NULL, "moe latent layer: null pointer");
+        if (x_dtype != K3_BF16) return set_error(K3_ERR_DTYPE, "moe latent layer: x must be bf16");
+        if (latent <= 0 || latent % 128 || latent > 8192)
+            return set_error(K3_ERR_SHAPE, "moe latent layer: latent=%lld must be a positive multiple of 128, <= 8192",
+                             (long long)latent);
+        if (!aligned16(lat_down) || !aligned16(lat_up) || !aligned16(lat_norm))
+            return set_error(K3_ERR_ALIGN, "moe latent layer: projections must be 16-byte aligned");
+        if (latent * H * 2 >= (1ll << 31) || latent * I / 2 >= (1ll << 31))
+            return set_error(K3_ERR_SHAPE, "moe latent layer: a weight matrix exceeds 2 GiB");
+    }
     const bool has_shared = shared_gate || shared_up || shared_down;
     if (has_shared && !(shared_gate && shared_up && shared_down))
         return set_error(K3_ERR_NULL, "moe layer: shared expert needs gate, up and down");
@@ -661,7 +814,7 @@ static int layer_impl(const void *x, int x_dtype, const void *router_w, const vo
     if (n_experts <= 0 || n_experts > kMaxExperts || top_k <= 0 || top_k > kMaxTopK || top_k > n_experts)
         return set_error(K3_ERR_SHAPE, "moe layer: n_experts must be in 1..%d and top_k in 1..min(%d, n_experts)",
                          kMaxExperts, kMaxTopK);
-    const LayerWsLayout L = layer_ws_layout(H, I, has_shared ? shared_I : 0, n_experts, top_k);
+    const LayerWsLayout L = layer_ws_layout(H, I, has_shared ? shared_I : 0, n_experts, top_k, lat ? latent : 0);
     if (workspace_bytes < static_cast<int64_t>(L.total))
         return set_error(K3_ERR_WORKSPACE, "moe layer: workspace %lld < %zu bytes", (long long)workspace_bytes, L.total);
     if (!aligned16(x) || !aligned16(router_w) || !aligned16(workspace) ||
@@ -690,6 +843,15 @@ static int layer_impl(const void *x, int x_dtype, const void *router_w, const vo
     a.ws.sel_ptrs = reinterpret_cast<uint64_t *>(w + L.ptrs);
     a.ws.counter = reinterpret_cast<uint32_t *>(w + L.counter);
     a.H = static_cast<int>(H);
+    a.Hr = static_cast<int>(lat ? latent : H);
+    if (lat) {
+        a.lat_down = static_cast<const uint16_t *>(lat_down);
+        a.lat_up = static_cast<const uint16_t *>(lat_up);
+        a.lat_norm = static_cast<const float *>(lat_norm);
+        a.eps = eps;
+        a.ws.h = reinterpret_cast<uint16_t *>(w + L.h);
+        a.ws.ylat = reinterpret_cast<float *>(w + L.ylat);
+    }
     a.I = static_cast<int>(I);
     a.Is = has_shared ? static_cast<int>(shared_I) : 0;
     a.E = static_cast<int>(n_experts);
@@ -716,6 +878,26 @@ extern "C" int k3_moe_layer_decode(const void *x, int x_dtype, const void *route
     return layer_impl(x, x_dtype, router_w, router_bias, route_kind, renormalize, scaling, expert_table, shared_gate,
                       shared_up, shared_down, out, out_dtype, H, I, shared_I, n_experts, top_k, act_kind, beta,
                       linear_beta, workspace, workspace_bytes, stream, false);
+}
+
+extern "C" int64_t k3_moe_latent_layer_workspace_size(int64_t H, int64_t latent, int64_t I, int64_t shared_I,
+                                                      int64_t n_experts, int64_t top_k) {
+    return static_cast<int64_t>(layer_ws_layout(H, I, shared_I, n_experts, top_k, latent).total);
+}
+
+extern "C" int k3_moe_latent_layer_decode(const void *x, const void *router_w, const void *router_bias,
+                                          int renormalize, float scaling, const void *expert_table,
+                                          const void *latent_down, const void *latent_up, const void *latent_norm,
+                                          float eps, const void *shared_gate, const void *shared_up,
+                                          const void *shared_down, void *out, int out_dtype, int64_t H,
+                                          int64_t latent, int64_t I, int64_t shared_I, int64_t n_experts,
+                                          int64_t top_k, int act_kind, float beta, float linear_beta,
+                                          void *workspace, int64_t workspace_bytes, void *stream) {
+    if (!latent_down) return set_error(K3_ERR_NULL, "moe latent layer: null pointer");
+    return layer_impl(x, K3_BF16, router_w, router_bias, K3_ROUTE_SIGMOID_BIAS, renormalize, scaling, expert_table,
+                      shared_gate, shared_up, shared_down, out, out_dtype, H, I, shared_I, n_experts, top_k, act_kind,
+                      beta, linear_beta, workspace, workspace_bytes, stream, false, latent_down, latent_up,
+                      latent_norm, eps, latent);
 }
 
 extern "C" int k3_moe_route(const void *x, int x_dtype, const void *router_w, const void *router_bias, int route_kind,

@@ -42,6 +42,9 @@ SIGNATURES: dict[str, list] = {
     "k3_moe_route": [_P, _I32, _P, _P, _I32, _I32, _F32, _I64, _I64, _I64, _P, _I64, _P],
     "k3_moe_layer_decode": [_P, _I32, _P, _P, _I32, _I32, _F32, _P, _P, _P, _P, _P, _I32, _I64, _I64,
                             _I64, _I64, _I64, _I32, _F32, _F32, _P, _I64, _P],
+    "k3_moe_latent_layer_workspace_size": [_I64, _I64, _I64, _I64, _I64, _I64],
+    "k3_moe_latent_layer_decode": [_P, _P, _P, _I32, _F32, _P, _P, _P, _P, _F32, _P, _P, _P, _P, _I32, _I64, _I64,
+                                   _I64, _I64, _I64, _I64, _I32, _F32, _F32, _P, _I64, _P],
     "k3_mla_workspace_size": [_I64, _I64],
     "k3_mla_decode_absorbed": [_P, _P, _I64, _I64, _I32, _P, _P, _P, _I64, _P, _I64, _I64, _I64, _I64, _I64,
                                _I64, _I64, _F32, _P, _I32, _I64, _P, _I64, _P],
@@ -54,6 +57,7 @@ SIGNATURES: dict[str, list] = {
 _RESTYPE = {"k3_last_error": ctypes.c_char_p, "k3_version": ctypes.c_char_p,
             "k3_expert_ffn_workspace_size": ctypes.c_int64,
             "k3_moe_layer_workspace_size": ctypes.c_int64,
+            "k3_moe_latent_layer_workspace_size": ctypes.c_int64,
             "k3_mla_workspace_size": ctypes.c_int64,
             "k3_moe_grouped_workspace_size": ctypes.c_int64}
 

@@ -336,10 +336,49 @@ class LatentMoE:
         """Shared expert(s) on the original hidden state (moe.py:105-107)."""
         return self._routed.shared_forward(x)
 
-    def __call__(self, x: torch.Tensor, return_router: bool = False):
-        c = self.cfg
+    DECODE_TOKENS = 8  # up to this many tokens: one fused decode per token; more: grouped
+
+    def __call__(self, x: torch.Tensor, return_router: bool = False, out_dtype=torch.float32):
         orig = x.shape
         flat = x.reshape(-1, orig[-1])
+        if flat.shape[0] <= self.DECODE_TOKENS:
+            return self._decode(flat, orig, return_router, out_dtype)
+        return self.grouped_forward(flat, return_router, out_dtype, orig)
+
+    def _decode(self, flat, orig, return_router, out_dtype):
+        """Per token: k3_moe_latent_layer_decode (route, latent down, routed experts,
+        norm, up projection, shared experts; four launches, no host synchronisation)."""
+        c, R = self.cfg, self._routed
+        act, beta, lb = R._act()
+        table = R.expert_table()
+        H, Lw, I, Is, E, k = R._H, self.latent, R._I, R._Is, R._E, R._k
+        nbytes = int(_lib.lib().k3_moe_latent_layer_workspace_size(H, Lw, I, Is, E, k))
+        outs, recs = [], []
+        for t in range(flat.shape[0]):
+            xt = T.contiguous_aligned(flat[t].reshape(1, -1).to(torch.bfloat16))
+            ws = _workspace.get(R.device, nbytes, "moe_latent")
+            out = torch.empty((1, H), dtype=out_dtype, device=R.device)
+            _lib.call("k3_moe_latent_layer_decode", T.ptr(xt), T.ptr(R.gate_w), T.ptr(R.gate_b),
+                      int(bool(c.moe_renormalize)), float(c.routed_scaling_factor), T.ptr(table), T.ptr(self.down),
+                      T.ptr(self.up), T.ptr(self._norm32), float(c.rms_norm_eps), T.ptr(R.sh_gate), T.ptr(R.sh_up),
+                      T.ptr(R.sh_down), T.ptr(out), T.dtype_code(out_dtype), H, Lw, I, Is, E, k, ACTS[act],
+                      float(beta), float(lb or 0.0), T.ptr(ws), ws.numel(), T.stream(xt))
+            outs.append(out)
+            if return_router:
+                recs.append(R._records(ws))
+        y = torch.cat(outs).reshape(*orig[:-1], H)
+        if not return_router:
+            return y
+        return y, RouterResult(*(torch.cat([getattr(rr, f) for rr in recs]) for f in
+                                 ("expert_indices", "expert_weights", "raw_scores", "corrected_scores")))
+
+    def grouped_forward(self, flat, return_router=False, out_dtype=torch.float32, orig=None):
+        """Many tokens: route every token, h in bf16 through the BLAS library, the routed
+        experts grouped by expert on the device (k3_moe_grouped_ffn), the norm and the up
+        projection in fp32, the shared experts in fp32."""
+        c = self.cfg
+        orig = orig if orig is not None else flat.shape
+        flat = flat.reshape(-1, flat.shape[-1])
         r = self.route(flat)
         h = flat.to(torch.bfloat16) @ self.down.T                         # hidden -> latent
         act, beta, lb = self._routed._act()
@@ -350,7 +389,7 @@ class LatentMoE:
         y = y @ self._up32.T                                              # latent -> hidden
         if self._routed.sh_gate is not None:
             y = y + self.shared_forward(flat)
-        y = y.reshape(*orig[:-1], orig[-1])
+        y = y.to(out_dtype).reshape(*orig[:-1], orig[-1])
         return (y, r) if return_router else y
 
 

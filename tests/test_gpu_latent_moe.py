@@ -2,10 +2,12 @@
 against the fp64 oracle (``oracle.moe.latent_moe``).
 
 The latent state h = x W_down^T is bf16 in the reference (its bf16 matmul, moe.py:117) and
-here (torch's bf16 GEMM), and the oracle rounds it the same way; a 1-ulp difference in a
+here (the decode kernel rounds its fp32 row dots; the grouped path uses torch's bf16 GEMM),
+and the oracle rounds it the same way; a 1-ulp difference in a
 few elements of h (fp32 vs fp64 accumulation before the rounding) and the grouped MFMA
-path's ~1e-4 error set the bar: normwise max-relative 5e-4 (the grouped path's own bar),
-under BASELINE's 1e-3.  The router result is compared exactly (ids) and to 1e-5 (weights).
+path's ~1e-4 error set the bar of the grouped path (T > 8): normwise max-relative 5e-4 (its
+own bar), under BASELINE's 1e-3.  The decode path (T <= 8) rounds h exactly as the oracle
+does and accumulates in fp32: 1e-5.  The router result is compared exactly (ids) and to 1e-5 (weights).
 """
 from __future__ import annotations
 
@@ -20,7 +22,8 @@ from oracle import mxfp4 as om
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda"
-TOL = 5e-4
+TOL_GROUPED = 5e-4
+TOL_DECODE = 1e-5
 
 
 @dataclass
@@ -82,11 +85,13 @@ def check(cfg, seed, T, distinct=None):
     assert np.allclose(r.expert_weights.cpu().numpy(), wts, rtol=1e-5, atol=1e-7)
     rel = om.normwise_rel(y.float().cpu().numpy(), want)
     print(f"T={T} E={cfg.num_experts} k={cfg.num_experts_per_token} rel={rel:.2e}")
-    assert rel <= TOL, rel
+    assert rel <= (TOL_DECODE if T <= moe.DECODE_TOKENS else TOL_GROUPED), rel
 
 
-@pytest.mark.parametrize("T", [1, 5])
+@pytest.mark.parametrize("T", [1, 5, 12])
 def test_latent_moe_small(T):
+    """T <= 8: the fused decode (k3_moe_latent_layer_decode) per token; T = 12: the
+    grouped path."""
     check(K3Cfg(hidden_size=256, routed_expert_hidden_size=128, moe_intermediate_size=128, num_experts=16,
                 num_experts_per_token=4), seed=40 + T, T=T)
 
