@@ -9,7 +9,7 @@ resident expert (64 experts rotate, 1.5 GB, so the 256 MB MALL cannot serve the 
 `value` is algorithmic weight bytes per second over the K timed steps.  The same line
 carries the MoE-layer figure (384 resident experts, top-8 softmax routing, one bf16 shared
 expert, a fresh token per step), the grouped-prefill, single-projection GEMV and MLA decode
-figures, the roofline of the expert step (its two launches) and a CPU baseline
+figures, K3's latent routed layer at batch 1 (896 experts, top-16), the roofline of the expert step (its two launches) and a CPU baseline
 (torch-CPU restatement of the k3ref path timed on a bounded sample on this host).
 
 Synthetic, seeded data; weights are random-init with the benchmark shapes.  Steps are
@@ -209,6 +209,51 @@ def bench_layer(torch, steps, warmup, dev):
     return sec, len(touched), stats
 
 
+K3_H, K3_L, K3_I, K3_E, K3_K, K3_IS = 7168, 3584, 3072, 896, 16, 6144
+K3_LAYER_BYTES = (K3_E * K3_H * 2 + 2 * K3_L * K3_H * 2 + K3_K * 3 * proj_bytes(K3_I, K3_L)
+                  + 3 * K3_IS * K3_H * 2)                                 # 660,602,880
+
+
+def bench_k3_layer(torch, steps, warmup, dev):
+    """K3's routed layer at batch 1 with its latent wrapper (LatentMoE): sigmoid + bias
+    routing of x over 896 experts (top-16, renormalised, scaling 2.5), latent down projection
+    [3584, 7168] bf16, 16 routed SiTU experts [3072 x 3584] MXFP4 on the latent state, RMS
+    norm, up projection [7168, 3584] bf16, two shared experts (one bf16 MLP of width 6144)
+    on x.  All 896 experts are distinct and resident (15.7 GB); a fresh token per step."""
+    from types import SimpleNamespace
+    from k3hip.moe import LatentMoE
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(1006)
+    bf = torch.bfloat16
+    experts = [(rand_mxfp4(torch, gen, K3_I, K3_L, dev), rand_mxfp4(torch, gen, K3_I, K3_L, dev),
+                rand_mxfp4(torch, gen, K3_L, K3_I, dev)) for _ in range(K3_E)]
+    rn = lambda *s: torch.randn(*s, device=dev, generator=gen)  # noqa: E731
+    w = {"gate.weight": (rn(K3_E, K3_H) * 0.02).to(bf), "gate.e_score_correction_bias": rn(K3_E) * 0.05,
+         "routed_expert_down_proj.weight": (rn(K3_L, K3_H) * 0.02).to(bf),
+         "routed_expert_up_proj.weight": (rn(K3_H, K3_L) * 0.02).to(bf),
+         "routed_expert_norm.weight": 1.0 + 0.1 * rn(K3_L),
+         "shared_experts.gate_proj.weight": (rn(K3_IS, K3_H) * 0.02).to(bf),
+         "shared_experts.up_proj.weight": (rn(K3_IS, K3_H) * 0.02).to(bf),
+         "shared_experts.down_proj.weight": (rn(K3_H, K3_IS) * 0.02).to(bf)}
+    cfg = SimpleNamespace(hidden_size=K3_H, routed_expert_hidden_size=K3_L, moe_intermediate_size=K3_I,
+                          num_experts=K3_E, num_experts_per_token=K3_K, moe_renormalize=True,
+                          routed_scaling_factor=2.5, situ_beta=2.0, situ_linear_beta=3.0, rms_norm_eps=1e-5)
+    which = {"w1": 0, "w3": 1, "w2": 2}
+    moe = LatentMoE(cfg, 0, w, lambda L, e, wh: experts[e][which[wh]])
+    xs = rn(steps + warmup + 3, K3_H).to(bf)
+
+    def step(i):
+        moe(xs[i:i + 1])
+
+    sec, _ = graph_time(torch, step, steps, warmup)
+    stats = None if EAGER else step_stats(torch, step, min(64, steps))
+    touched = set()
+    for i in range(min(steps, 32)):
+        touched.update(moe.route(xs[i:i + 1]).expert_indices.view(-1).tolist())
+    del moe, experts, w
+    return sec, len(touched), stats
+
+
 PF_T, PF_K = 2048, 8
 PF_FLOPS = 2 * PF_T * PF_K * 3 * H * I                                   # 1.443e12 useful
 
@@ -351,7 +396,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=64)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
-    ap.add_argument("--workloads", default="expert,layer,prefill,gemv,mla,ceiling")
+    ap.add_argument("--workloads", default="expert,layer,k3layer,prefill,gemv,mla,ceiling")
     ap.add_argument("--eager", action="store_true",
                     help="launch steps one by one instead of replaying a HIP graph (profiler counter runs)")
     args = ap.parse_args()
@@ -408,6 +453,18 @@ def main():
                              "bytes_per_layer": LAYER_BYTES, "experts": E_LAYER, "top_k": TOPK,
                              "shared_expert": "bf16", "distinct_experts_routed_first32": touched,
                              "launches_per_layer": 3, "step_us": lstats}
+    if "k3layer" in work:
+        ks = min(K, 256)
+        ksec, ktouched, kstats = bench_k3_layer(torch, ks, min(W, 32), dev)
+        kus = ksec / ks * 1e6
+        kgbs = K3_LAYER_BYTES / (kus * 1e-6) / 1e9
+        line["k3_latent_layer"] = {"us_per_token": round(kus, 2), "GB/s": round(kgbs, 1),
+                                   "pct_hbm_peak": round(100 * kgbs / HBM_PEAK_GBS, 1),
+                                   "bytes_per_token": K3_LAYER_BYTES, "hidden": K3_H, "latent": K3_L,
+                                   "expert_intermediate": K3_I, "experts": K3_E, "top_k": K3_K,
+                                   "shared_intermediate": K3_IS, "router": "sigmoid + bias",
+                                   "act": "situ", "distinct_experts_routed_first32": ktouched,
+                                   "launches_per_token": 4, "step_us": kstats}
     if "prefill" in work:
         pst, pbytes, counts = bench_prefill(torch, 8, 2, dev)
         line["moe_prefill"] = {

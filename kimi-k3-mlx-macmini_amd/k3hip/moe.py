@@ -292,9 +292,11 @@ class LatentMoE:
     situ_linear_beta and rms_norm_eps.
 
     ``__call__(x)`` (moe.py:110-132): route on x; h = x W_down^T in bf16 (the reference's
-    dtype); the routed experts on h, grouped by expert on the device (k3_moe_grouped_ffn,
-    no host synchronisation, SiTU); KimiRMSNorm of their weighted sum in fp32; the up
-    projection in fp32; plus the shared expert on the original x."""
+    dtype); the routed experts (SiTU) on h; KimiRMSNorm of their weighted sum in fp32; the up
+    projection in fp32; plus the shared expert on the original x.  Up to DECODE_TOKENS
+    tokens run one by one through k3_moe_latent_layer_decode (four launches per token);
+    more tokens run the routed experts grouped by expert (k3_moe_grouped_ffn).  Neither
+    path synchronises with the host."""
 
     def __init__(self, cfg, layer: int, w: dict, expert_source: Callable, fused: bool = True):
         self.cfg, self.L = cfg, layer
@@ -366,7 +368,7 @@ class LatentMoE:
             outs.append(out)
             if return_router:
                 recs.append(R._records(ws))
-        y = torch.cat(outs).reshape(*orig[:-1], H)
+        y = (outs[0] if len(outs) == 1 else torch.cat(outs)).reshape(*orig[:-1], H)
         if not return_router:
             return y
         return y, RouterResult(*(torch.cat([getattr(rr, f) for rr in recs]) for f in
