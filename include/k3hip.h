@@ -95,9 +95,9 @@ int k3_expert_ffn(const void *x, int x_dtype, const void *gate_packed, const voi
 /* ---- routed MoE layer at batch 1 ------------------------------------------------------ */
 
 /* Workspace bytes for k3_moe_layer_decode / k3_moe_route (pass shared_I = 0 without a
- * shared expert).  Its first 256 bytes hold a counter of finished router blocks (at that
- * place for every shape): zero-fill them before the first call; every call returns them to
- * zero.  The rest is rewritten by every call.  Calls that share a workspace must not
+ * shared expert).  Its first 4096 bytes hold arrival counters (finished router blocks,
+ * finished blocks of each range of output rows; at that place for every shape): zero-fill
+ * them before the first call; every call returns them to zero.  The rest is rewritten by every call.  Calls that share a workspace must not
  * overlap (calls on one stream never do). */
 int64_t k3_moe_layer_workspace_size(int64_t H, int64_t I, int64_t shared_I, int64_t n_experts,
                                     int64_t top_k);
@@ -162,7 +162,7 @@ int k3_moe_grouped_ffn(const void *x, int x_dtype, const int32_t *expert_idx, co
 
 /* Workspace bytes for k3_moe_latent_layer_decode: the k3_moe_layer_decode records plus the
  * bf16 latent state and the fp32 routed sum.  Same counter rule as k3_moe_layer_workspace_size
- * (first 256 bytes zero before the first call; every call returns them to zero). */
+ * (first 4096 bytes zero before the first call; every call returns them to zero). */
 int64_t k3_moe_latent_layer_workspace_size(int64_t H, int64_t latent, int64_t I, int64_t shared_I,
                                            int64_t n_experts, int64_t top_k);
 

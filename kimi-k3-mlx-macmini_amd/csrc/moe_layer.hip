@@ -15,9 +15,11 @@
 //       need no routing, then the routed gate/up row pairs of the k selected experts (MXFP4,
 //       through the device pointer table, so every expert stays resident and each selected
 //       expert's bytes are read once) with their activation.
-//   L3  per block, RPW output rows and one wave per selected expert: the wave holds its
-//       expert's act in registers and reduces its down rows; the block combines
-//       y = shared + sum_j w_j * down_j in a fixed order.
+//   L3  per block, one selected expert and 4*RW down rows (RW per wave): each lane holds the
+//       act values of its pieces of the row in registers and the wave reduces its rows; the
+//       row totals go to the workspace, and the last of the k blocks of a row range to
+//       finish (an arrival counter per range) combines y = shared + sum_j w_j * down_j in
+//       slot order.
 //
 // Every kernel issues its activation loads, then its whole weight stream, before it stages
 // anything into LDS or registers it consumes, and stages with unconditional stores, so the
@@ -40,7 +42,9 @@ struct LayerWs {
     float *act;          // [k][I]
     float *yshared;      // [H]
     uint64_t *sel_ptrs;  // [k][6] weight pointers of the selected experts
-    uint32_t *counter;   // router blocks done in this launch (returns to 0 after each)
+    uint32_t *counter;   // [0] router blocks done (L1), [1 + r] blocks of L3 row range r
+                         // done; every launch returns them to 0
+    float *yrow;         // [k][Hr] per-slot down-row totals (L3)
     uint16_t *h;         // [Hr] bf16 latent state (latent layer)
     float *ylat;         // [Hr] routed sum in latent space (latent layer)
 };
@@ -72,6 +76,9 @@ struct LayerArgs {
 
 constexpr int kMaxTopK = 16;
 constexpr int kMaxExperts = 1024;
+// Arrival counters at the head of the workspace: [0] for L1's router blocks, [1 + r] for the
+// blocks of L3's row range r
+constexpr size_t kCounterBytes = 4096;
 constexpr int kSharedDownRows = 2;  // shared down rows per wave (L2; L4)
 // shared down rows per wave for CHI chunks per lane: one row past 8 chunks (wide shared
 // experts), so the fp32 activation and the rows stay in registers
@@ -523,81 +530,113 @@ __global__ __launch_bounds__(256) void layer_l2(LayerArgs a) {
 }
 
 // ------------------------------------------------------------------ L3
-// Block: KT waves (wave j = selected expert j) x RPW output rows.  Each lane holds the act
-// values of its GB groups of expert j in registers (fp32, loaded from the workspace); the
-// block combines the experts' row totals in slot order.
-template <int KT, int RPW, int GB>
-__global__ __launch_bounds__((KT > 8 ? 8 : KT) * 64) void layer_l3(LayerArgs a) {
-    // up to 8 waves; with 16 slots each wave takes slots w and w + 8 one after the other, so a
-    // block keeps RPW rows per expert without the register budget of 16 waves
-    constexpr int NW = KT > 8 ? 8 : KT, EPW = KT / NW;
-    __shared__ float ys[RPW][KT];
+// Block: 4 waves on selected expert j = blockIdx.x % k and row range rr = blockIdx.x / k of
+// 4 * RW down rows (RW consecutive rows per wave).  A down row is cut into pieces of S
+// elements (S = 32: one group, 16 bytes; S = 16: half a group, 8 bytes); lane l takes pieces
+// l, l + 64, ... (NP of them), so each of the wave's loads is one contiguous run of the row,
+// and it holds the act values of those pieces in registers for all RW rows.  The row totals
+// go to yrow[j]; the last of the range's k blocks to finish combines them in slot order, so
+// the result does not depend on the order in which the blocks finish.
+template <int S, int NP, int RW>
+__global__ __launch_bounds__(256, 4) void layer_l3(LayerArgs a) {
+    static_assert(S == 16 || S == 32, "a piece is half a group or one group");
+    constexpr int ND = S / 8;   // packed dwords per piece
+    constexpr int NC = S / 4;   // float4 act chunks per piece
+    constexpr int RB = 4 * RW;  // rows per block
+    __shared__ uint32_t last_s;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
-    const int GI = a.I >> 5;
+    // slot-major order: consecutive blocks read different rows of one expert, so every XCD
+    // streams from every selected expert
+    const int nR = (a.Hr + RB - 1) / RB;
+    const int j = blockIdx.x / nR, rr = blockIdx.x % nR;
+    const int GI = a.I >> 5, P = a.I / S;
     const uint32_t rowB = static_cast<uint32_t>(a.I >> 1);
-    const int n0 = blockIdx.x * RPW;
-#pragma unroll 1
-    for (int e2 = 0; e2 < EPW; ++e2) {
-        const int j = wave + NW * e2;
-        const bool live = j < a.k;  // slots past top_k idle (KT rounds top_k up)
-        // 1. the expert's down-projection pointers, then its act for this lane's groups (8
-        //    chunks of 4 floats per group)
-        const uint64_t *t = a.ws.sel_ptrs + (live ? j : 0) * 6;
-        const auto rd = make_rsrc(uniform_ptr(t[4]), static_cast<uint32_t>(a.Hr) * rowB);
-        const auto rds = make_rsrc(uniform_ptr(t[5]), static_cast<uint32_t>(a.Hr * GI));
-        const auto ra = make_rsrc(a.ws.act + static_cast<int64_t>(live ? j : 0) * a.I, static_cast<uint32_t>(a.I) * 4u);
-        float4 av[GB][8];
+    const int n0 = rr * RB + wave * RW;
+    const uint64_t *t = a.ws.sel_ptrs + j * 6;
+    const auto rd = make_rsrc(uniform_ptr(t[4]), static_cast<uint32_t>(a.Hr) * rowB);
+    const auto rds = make_rsrc(uniform_ptr(t[5]), static_cast<uint32_t>(a.Hr * GI));
+    const auto ra = make_rsrc(a.ws.act + static_cast<int64_t>(j) * a.I, static_cast<uint32_t>(a.I) * 4u);
+    // 1. the act values of this lane's pieces (the block's four waves read the same bytes),
+    //    then the wave's down rows and their scale bytes
+    float4 av[NP][NC];
 #pragma unroll
-        for (int u = 0; u < GB; ++u) {
-            const int g = u * 64 + lane;
+    for (int p = 0; p < NP; ++p) {
+        const int pc = p * 64 + lane;
 #pragma unroll
-            for (int q = 0; q < 8; ++q)
-                av[u][q] = __builtin_bit_cast(
-                    float4, buf_load16(ra, (live && g < GI) ? static_cast<uint32_t>(g) * 128u + q * 16u : kOobOffset));
-        }
-        // 2. the expert's down rows of this block, and their scale bytes
-        uint4 wd[RPW][GB];
-        uint32_t sd[RPW][GB];
+        for (int q = 0; q < NC; ++q)
+            av[p][q] = __builtin_bit_cast(
+                float4, buf_load16(ra, pc < P ? static_cast<uint32_t>(pc) * (S * 4u) + q * 16u : kOobOffset));
+    }
+    uint32_t wd[RW][NP][ND];
+    uint32_t sd[RW][NP];
 #pragma unroll
-        for (int r = 0; r < RPW; ++r)
+    for (int r = 0; r < RW; ++r)
 #pragma unroll
-            for (int u = 0; u < GB; ++u) {
-                const int n = n0 + r, g = u * 64 + lane;
-                const bool ok = live && n < a.Hr && g < GI;
-                wd[r][u] = buf_load16(rd, ok ? static_cast<uint32_t>(n) * rowB + g * 16u : kOobOffset);
-                sd[r][u] = __builtin_amdgcn_raw_buffer_load_b8(rds, ok ? static_cast<uint32_t>(n * GI + g) : kOobOffset,
-                                                               0, 0);
+        for (int p = 0; p < NP; ++p) {
+            const int n = n0 + r, pc = p * 64 + lane;
+            const bool ok = n < a.Hr && pc < P;
+            const uint32_t off = ok ? static_cast<uint32_t>(n) * rowB + pc * (S / 2u) : kOobOffset;
+            if constexpr (S == 32) {
+                const uint4 v = buf_load16(rd, off);
+                wd[r][p][0] = v.x, wd[r][p][1] = v.y, wd[r][p][2] = v.z, wd[r][p][3] = v.w;
+            } else {
+                const auto v = __builtin_amdgcn_raw_buffer_load_b64(rd, off, 0, 0);
+                wd[r][p][0] = v[0], wd[r][p][1] = v[1];
             }
-        // 3. row dots; wave totals to LDS
-#pragma unroll
-        for (int r = 0; r < RPW; ++r) {
-            float acc = 0.f;
-#pragma unroll
-            for (int u = 0; u < GB; ++u)
-                if (u * 64 + lane < GI) acc = fmaf(group_dot(wd[r][u], av[u]), e8m0_to_f32(sd[r][u]), acc);
-            const float tot = wave_sum_to_lane63(acc);
-            if (lane == 63) ys[r][j] = tot;
+            sd[r][p] = __builtin_amdgcn_raw_buffer_load_b8(
+                rds, ok ? static_cast<uint32_t>(n * GI + pc * S / 32) : kOobOffset, 0, 0);
         }
+    // 2. row dots (out-of-range pieces hold zeros); wave totals to the workspace
+#pragma unroll
+    for (int r = 0; r < RW; ++r) {
+        float acc = 0.f;
+#pragma unroll
+        for (int p = 0; p < NP; ++p) acc = fmaf(piece_dot<ND>(wd[r][p], av[p]), e8m0_to_f32(sd[r][p]), acc);
+        const float tot = wave_sum_to_lane63(acc);
+        const int n = n0 + r;
+        if (lane == 63 && n < a.Hr)
+            __hip_atomic_store(a.ws.yrow + static_cast<int64_t>(j) * a.Hr + n, tot, __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
+    }
+    // 3. the block counts itself done once its row stores are complete; the last of the
+    //    range's k blocks resets the counter and combines
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        uint32_t *c = a.ws.counter + 1 + rr;
+        const uint32_t old = __hip_atomic_fetch_add(c, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        last_s = old + 1 == static_cast<uint32_t>(a.k);
+        if (last_s) __hip_atomic_store(c, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
     __syncthreads();
-    // 4. combine in slot order with the shared expert's row (latent layer: the routed sum
-    // in latent space, for the norm and up projection of L4)
-    if (static_cast<int>(threadIdx.x) < RPW) {
-        const int r = threadIdx.x, n = n0 + r;
-        if (n < a.Hr) {
-            float y = 0.f;
-            for (int jj = 0; jj < a.k; ++jj) y = fmaf(a.ws.topk_w[jj], ys[r][jj], y);
-            if (a.lat_down) {
-                a.ws.ylat[n] = y;
-                return;
-            }
-            if (a.sh_down) y += a.ws.yshared[n];
-            if (a.out_bf16)
-                static_cast<uint16_t *>(a.out)[n] = f32_to_bf16(y);
-            else
-                static_cast<float *>(a.out)[n] = y;
-        }
+    if (!last_s) return;
+    const int n = rr * RB + static_cast<int>(threadIdx.x);
+    if (static_cast<int>(threadIdx.x) >= RB || n >= a.Hr) return;
+    // 4. y = sum_j w_j * down_j in slot order (latent layer: the routed sum in latent space,
+    //    for the norm and up projection of L4), plus the shared expert's row.  The row totals
+    //    are read with device-coherent loads, all issued before the sum (slot indices past k
+    //    are clamped and their terms dropped).
+    const auto rw = make_rsrc(a.ws.topk_w, static_cast<uint32_t>(a.k) * 4u);
+    float v[kMaxTopK], tw[kMaxTopK];
+#pragma unroll
+    for (int jj = 0; jj < kMaxTopK; ++jj) {
+        const int js = jj < a.k ? jj : a.k - 1;
+        v[jj] = __hip_atomic_load(a.ws.yrow + static_cast<int64_t>(js) * a.Hr + n, __ATOMIC_RELAXED,
+                                  __HIP_MEMORY_SCOPE_AGENT);
+        tw[jj] = __builtin_bit_cast(float, buf_load4(rw, jj * 4u));
     }
+    float y = 0.f;
+#pragma unroll
+    for (int jj = 0; jj < kMaxTopK; ++jj) y = jj < a.k ? fmaf(tw[jj], v[jj], y) : y;
+    if (a.lat_down) {
+        a.ws.ylat[n] = y;
+        return;
+    }
+    if (a.sh_down) y += a.ws.yshared[n];
+    if (a.out_bf16)
+        static_cast<uint16_t *>(a.out)[n] = f32_to_bf16(y);
+    else
+        static_cast<float *>(a.out)[n] = y;
 }
 
 
@@ -666,18 +705,18 @@ __global__ __launch_bounds__(256) void layer_l4(LayerArgs a) {
 
 // ------------------------------------------------------------------ host side
 struct LayerWsLayout {
-    size_t logits, scores, corrected, idx, w, shared_act, act, yshared, ptrs, counter, h, ylat, total;
+    size_t logits, scores, corrected, idx, w, shared_act, act, yshared, ptrs, counter, h, ylat, yrow, total;
 };
 
 static size_t up256(size_t v) { return (v + 255) & ~size_t(255); }
 
-// The router-block counter sits in the first 256 bytes for every shape, so workspaces
-// shared by layers of different shapes keep it at one place (zero between calls); the
-// records after it are rewritten by every call.
+// The arrival counters sit in the first kCounterBytes for every shape, so workspaces shared
+// by layers of different shapes keep them at one place (zero between calls); the records
+// after them are rewritten by every call.
 static LayerWsLayout layer_ws_layout(int64_t H, int64_t I, int64_t Is, int64_t E, int64_t k, int64_t Hr = 0) {
     LayerWsLayout L{};
     size_t o = 0;
-    L.counter = o, o += 256;
+    L.counter = o, o += kCounterBytes;
     L.logits = o, o += up256(E * 4);
     L.scores = o, o += up256(E * 4);
     L.corrected = o, o += up256(E * 4);
@@ -689,6 +728,7 @@ static LayerWsLayout layer_ws_layout(int64_t H, int64_t I, int64_t Is, int64_t E
     L.ptrs = o, o += up256(k * 6 * 8);
     L.h = o, o += up256(Hr * 2);
     L.ylat = o, o += up256(Hr * 4);
+    L.yrow = o, o += up256(k * std::max(H, Hr) * 4);
     L.total = o;
     return L;
 }
@@ -753,21 +793,21 @@ static int launch_layer(LayerArgs &a, hipStream_t st) {
 #undef K3_L2
     rc = check_hip(hipGetLastError(), "moe layer L2");
     if (rc) return rc;
-    // L3: rows per block so each wave streams a few KiB of its expert's down rows (half as
-    // many for two slots per wave of two groups per lane, within 256 registers)
-    constexpr int R = 16;
-    const int kt = a.k <= 1 ? 1 : (a.k <= 2 ? 2 : (a.k <= 4 ? 4 : (a.k <= 8 ? 8 : 16)));
-#define K3_L3(KT_, GB_) \
-    if (kt == KT_ && gb == GB_) { \
-        constexpr int R_ = KT_ > 8 && GB_ > 1 ? R / 2 : R; \
-        layer_l3<KT_, R_, GB_><<<dim3(static_cast<unsigned>(cdiv(a.Hr, R_))), (KT_ > 8 ? 8 : KT_) * 64, 0, st>>>(a); \
-        rc = check_hip(hipGetLastError(), "moe layer L3"); \
-        return rc ? rc : launch_l4(a, st); \
-    }
-    K3_L3(1, 1) K3_L3(2, 1) K3_L3(4, 1) K3_L3(8, 1) K3_L3(16, 1)
-    K3_L3(1, 2) K3_L3(2, 2) K3_L3(4, 2) K3_L3(8, 2) K3_L3(16, 2)
-#undef K3_L3
-    return set_error(K3_ERR_SHAPE, "moe layer: no combine kernel for top_k=%d", a.k);
+    // L3: pieces of a down row per lane and rows per wave, so a lane's act values and its
+    // rows' weights fit in about 128 registers (four blocks per CU)
+    const int rb = GI <= 64 ? 4 * 14 : (GI <= 96 ? 4 * 7 : 4 * 4);
+    if (1 + cdiv(a.Hr, rb) > static_cast<int64_t>(kCounterBytes / 4))
+        return set_error(K3_ERR_SHAPE, "moe layer: %d rows need more row-range counters than the workspace holds",
+                         a.Hr);
+    const dim3 g3(static_cast<unsigned>(a.k * cdiv(a.Hr, rb)));
+    if (GI <= 64)
+        layer_l3<32, 1, 14><<<g3, 256, 0, st>>>(a);
+    else if (GI <= 96)
+        layer_l3<16, 3, 7><<<g3, 256, 0, st>>>(a);
+    else
+        layer_l3<32, 2, 4><<<g3, 256, 0, st>>>(a);
+    rc = check_hip(hipGetLastError(), "moe layer L3");
+    return rc ? rc : launch_l4(a, st);
 }
 
 }  // namespace k3
@@ -842,6 +882,7 @@ static int layer_impl(const void *x, int x_dtype, const void *router_w, const vo
     a.ws.yshared = reinterpret_cast<float *>(w + L.yshared);
     a.ws.sel_ptrs = reinterpret_cast<uint64_t *>(w + L.ptrs);
     a.ws.counter = reinterpret_cast<uint32_t *>(w + L.counter);
+    a.ws.yrow = reinterpret_cast<float *>(w + L.yrow);
     a.H = static_cast<int>(H);
     a.Hr = static_cast<int>(lat ? latent : H);
     if (lat) {

@@ -41,12 +41,12 @@ __device__ __forceinline__ float group_dot(const uint4 w, const uint4 *xc) {
     return p0 + p1;
 }
 
-// 32-element dot of one packed group with fp32 activations (8 chunks of 4 floats).
-__device__ __forceinline__ float group_dot(const uint4 w, const float4 *xc) {
-    const uint32_t wd[4] = {w.x, w.y, w.z, w.w};
+// Dot of ND packed dwords (8 * ND elements) with fp32 activations (2 * ND chunks of 4 floats).
+template <int ND>
+__device__ __forceinline__ float piece_dot(const uint32_t (&wd)[ND], const float4 *xc) {
     float p0 = 0.f, p1 = 0.f;
 #pragma unroll
-    for (int d = 0; d < 4; ++d) {
+    for (int d = 0; d < ND; ++d) {
         const float4 a = xc[2 * d], b = xc[2 * d + 1];
         f32x2 w0 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(wd[d], 1.0f, 0);
         f32x2 w1 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(wd[d], 1.0f, 1);
@@ -62,6 +62,12 @@ __device__ __forceinline__ float group_dot(const uint4 w, const float4 *xc) {
         p1 = fmaf(b.w, w3.y, p1);
     }
     return p0 + p1;
+}
+
+// 32-element dot of one packed group with fp32 activations (8 chunks of 4 floats).
+__device__ __forceinline__ float group_dot(const uint4 w, const float4 *xc) {
+    const uint32_t wd[4] = {w.x, w.y, w.z, w.w};
+    return piece_dot<4>(wd, xc);
 }
 
 template <typename XT>

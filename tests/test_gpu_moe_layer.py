@@ -72,6 +72,7 @@ CASES = [
     (2048, 384, 64, 8, 512, 8, "sigmoid_bias", "situ", torch.bfloat16),
     (7168, 2048, 384, 8, 2048, 12, "softmax", "silu", torch.bfloat16),
     (3584, 3072, 96, 8, 0, 6, "sigmoid_bias", "situ", torch.bfloat16),
+    (2048, 4096, 32, 16, 0, 8, "sigmoid_bias", "situ", torch.bfloat16),
 ]
 
 
