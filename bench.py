@@ -254,6 +254,46 @@ def bench_k3_layer(torch, steps, warmup, dev):
     return sec, len(touched), stats
 
 
+def bench_ingest(torch, dev, n_experts=32):
+    """Checkpoint ingestion: n K3-shaped experts ([3072 x 3584] MXFP4, three projections,
+    reference tensor names) written as one safetensors shard to a temporary directory, then
+    made resident through TensorSource.load_experts (one read per adjacent (packed, scale)
+    pair into page-locked staging, asynchronous host-to-device copies, device scale check).
+    The file is in the page cache, so this is the host-memory -> HBM ingest rate, not SSD."""
+    import shutil
+    import tempfile
+    import numpy as np
+    from k3hip.checkpoint import TensorSource, expert_name, write_safetensors
+    rng = np.random.default_rng(1007)
+    tmp = Path(tempfile.mkdtemp(prefix="k3ingest"))
+    try:
+        t = {}
+        for e in range(n_experts):
+            for w, (n, k) in (("w1", (K3_I, K3_L)), ("w3", (K3_I, K3_L)), ("w2", (K3_L, K3_I))):
+                t[expert_name(0, e, w) + ".weight_packed"] = (rng.integers(0, 256, (n, k // 2), dtype=np.uint8), "U8")
+                t[expert_name(0, e, w) + ".weight_scale"] = (rng.integers(118, 131, (n, k // 32), dtype=np.uint8), "U8")
+        write_safetensors(tmp / "model-00001-of-00001.safetensors", t)
+        nbytes = sum(a.nbytes for a, _ in t.values())
+        del t
+        best = None
+        for _ in range(3):
+            src = TensorSource(ckpt=tmp, device=dev)
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            res = src.load_experts(0, n_experts)
+            torch.cuda.synchronize()
+            dt = time.perf_counter() - t0
+            best = dt if best is None else min(best, dt)
+            reads = src.reads
+            src.close()
+            del res
+        return {"GB/s": round(nbytes / best / 1e9, 2), "bytes": nbytes, "s": round(best, 4),
+                "experts": n_experts, "file_reads": reads, "projections": 3 * n_experts,
+                "source": "page cache (a file written just before)"}
+    finally:
+        shutil.rmtree(tmp, ignore_errors=True)
+
+
 PF_T, PF_K = 2048, 8
 PF_FLOPS = 2 * PF_T * PF_K * 3 * H * I                                   # 1.443e12 useful
 
@@ -396,7 +436,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=64)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
-    ap.add_argument("--workloads", default="expert,layer,k3layer,prefill,gemv,mla,ceiling")
+    ap.add_argument("--workloads", default="expert,layer,k3layer,ingest,prefill,gemv,mla,ceiling")
     ap.add_argument("--eager", action="store_true",
                     help="launch steps one by one instead of replaying a HIP graph (profiler counter runs)")
     args = ap.parse_args()
@@ -465,6 +505,8 @@ def main():
                                    "shared_intermediate": K3_IS, "router": "sigmoid + bias",
                                    "act": "situ", "distinct_experts_routed_first32": ktouched,
                                    "launches_per_token": 4, "step_us": kstats}
+    if "ingest" in work:
+        line["checkpoint_ingest"] = bench_ingest(torch, dev)
     if "prefill" in work:
         pst, pbytes, counts = bench_prefill(torch, 8, 2, dev)
         line["moe_prefill"] = {
