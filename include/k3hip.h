@@ -210,6 +210,33 @@ int k3_mla_decode_absorbed(const void *q_nope, const void *q_rot, int64_t ld_q, 
                            float scale, void *out, int out_dtype, int64_t ld_out, void *workspace,
                            int64_t workspace_bytes, void *stream);
 
+/* ---- one decode token through a whole MLA layer (batch 1) ------------------------------ */
+
+/* Workspace bytes k3_mla_step_decode needs (its projections' outputs and the attention
+ * core's workspace for T = pos + 1 cache rows).  No initialisation. */
+int64_t k3_mla_step_workspace_size(int64_t hidden, int64_t q_lora_rank, int64_t heads, int64_t nope_dim,
+                                   int64_t rope_dim, int64_t v_dim, int64_t kv_lora_rank, int64_t T);
+
+/* MLAAttention.__call__ for one token (air_llm/models/kimi_k3/attention_mla.py:168-216):
+ *   q = rmsnorm(x q_a^T, q_a_norm) q_b^T; ckv = x kv_a^T; the cache row pos gets
+ *   bf16(rmsnorm(ckv[:r], kv_a_norm)) and bf16(ckv[r:]) (MLACache.append,
+ *   attention_mla.py:89-108); o = the absorbed core over rows 0..pos
+ *   (k3_mla_decode_absorbed); o *= sigmoid(x g_proj^T) when g_proj is not null;
+ *   out = o o_proj^T.
+ * x [hidden] bf16 or fp32; q_a [q_lora_rank, hidden], q_b [heads*(nope+rope), q_lora_rank],
+ * kv_a [r + rope, hidden], g_proj [heads*v, hidden] (or null), o_proj [hidden, heads*v]: bf16
+ * row-major; q_a_norm [q_lora_rank], kv_a_norm [r]: fp32; w_uk / w_uv as for
+ * k3_mla_decode_absorbed; lat / rot the bf16 cache with cache_rows rows (pos < cache_rows).
+ * hidden, q_lora_rank and heads*v: multiples of 8, <= 12288.  fp32 accumulation and
+ * norms.  Six stream-ordered launches. */
+int k3_mla_step_decode(const void *x, int x_dtype, const void *q_a, const float *q_a_norm, const void *q_b,
+                       const void *kv_a, const float *kv_a_norm, const void *w_uk, const void *w_uv,
+                       const void *g_proj, const void *o_proj, void *lat, int64_t ld_lat, void *rot,
+                       int64_t ld_rot, int64_t cache_rows, int64_t pos, float eps, float scale, void *out,
+                       int out_dtype, int64_t hidden, int64_t q_lora_rank, int64_t heads, int64_t nope_dim,
+                       int64_t rope_dim, int64_t v_dim, int64_t kv_lora_rank, void *workspace,
+                       int64_t workspace_bytes, void *stream);
+
 /* ---- HBM calibration ------------------------------------------------------------------- */
 
 /* Streaming read of `bytes` (multiple of 16) from src; sink is a >= 4096-byte device scratch

@@ -12,11 +12,12 @@ capacity, valid prefix ``length``, ``append`` with chunked doubling growth, ``vi
 ``bytes_per_token``, ``nbytes_used``, ``attention_mla.py:62-117``), with bf16 device storage
 by default: the kernel reads the valid prefix directly, so ``view`` does not upcast.
 
-``MLAAttention(cfg, w)`` keeps the reference constructor and ``__call__(x, cache)``.  The
-decode step (one token, batch 1) runs the attention core on the HIP kernels; the
-projections around it (q_a/q_b, kv_a, RMSNorms, output gate, o_proj) are torch GPU
-matmuls, as they are plain MLX matmuls in the reference.  Prefill (T > 1) keeps the
-reference's dense masked form in torch on the GPU.
+``MLAAttention(cfg, w)`` keeps the reference constructor and ``__call__(x, cache)``.  With
+bf16 projection weights (the checkpoint dtype) the decode step (one token, batch 1) is
+``k3_mla_step_decode``: the projections, RMSNorms, cache append, attention core, output
+gate and o_proj in six HIP launches.  With other weight dtypes the projections are torch
+fp32 matmuls around the HIP core.  Prefill (T > 1) keeps the reference's dense masked form
+in torch on the GPU.
 """
 from __future__ import annotations
 
@@ -52,14 +53,21 @@ class MLACache:
         """The valid prefix, in the storage dtype (the kernels read bf16 directly)."""
         return self.latent[:, :self.length], self.rot[:, :self.length]
 
-    def append(self, c_new: torch.Tensor, r_new: torch.Tensor) -> "MLACache":
-        """Write T new positions, growing by doubling (floor CACHE_STEP) when full."""
-        n = c_new.shape[1]
+    def reserve(self, n: int) -> "MLACache":
+        """Capacity for n more positions, growing by doubling (floor CACHE_STEP) when full
+        (attention_mla.py:93-101)."""
         need = self.length + n
         if need > self.capacity:
             cap = _round_up(max(need, 2 * self.capacity, CACHE_STEP), CACHE_STEP)
             self.latent = _grown(self.latent, cap, self.length)
             self.rot = _grown(self.rot, cap, self.length)
+        return self
+
+    def append(self, c_new: torch.Tensor, r_new: torch.Tensor) -> "MLACache":
+        """Write T new positions, growing by doubling (floor CACHE_STEP) when full."""
+        n = c_new.shape[1]
+        need = self.length + n
+        self.reserve(n)
         self.latent[:, self.length:need] = c_new.to(self.latent.dtype)
         self.rot[:, self.length:need] = r_new.to(self.rot.dtype)
         self.length = need
@@ -188,6 +196,16 @@ class MLAAttention:
         self.wk = kb[:, :nope, :].contiguous()        # [H, nope, r]
         self.wv = kb[:, nope:, :].contiguous()        # [H, v, r]
         self.cache_dtype = getattr(cfg, "mla_cache_dtype", torch.bfloat16)
+        mats = [self.q_a, self.q_b, self.kv_a, self.o_w] + ([self.g_w] if self.g_w is not None else [])
+        self.fused_step = (all(m.dtype == torch.bfloat16 and m.is_cuda for m in mats)
+                           and self.cache_dtype == torch.bfloat16
+                           and cfg.kv_lora_rank == KV_LORA_RANK and cfg.qk_rope_head_dim == ROPE_DIM)
+        if self.fused_step:
+            self._mats = {k: T.contiguous_aligned(m) for k, m in
+                          (("q_a", self.q_a), ("q_b", self.q_b), ("kv_a", self.kv_a), ("o", self.o_w))}
+            self._mats["g"] = T.contiguous_aligned(self.g_w) if self.g_w is not None else None
+            self._q_an32 = T.contiguous_aligned(self.q_an.to(torch.float32))
+            self._kv_an32 = T.contiguous_aligned(self.kv_an.to(torch.float32))
 
     @staticmethod
     def _mm(a: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
@@ -196,6 +214,8 @@ class MLAAttention:
     def __call__(self, x: torch.Tensor, cache: MLACache | None = None):
         c = self.cfg
         B, Tn, _ = x.shape
+        if self.fused_step and B == 1 and Tn == 1 and (cache is None or cache.latent.dtype == torch.bfloat16):
+            return self.decode_step(x, cache)
         nh, qhd, vhd = c.num_attention_heads, c.q_head_dim, c.v_head_dim
         nope, rope, klr = c.qk_nope_head_dim, c.qk_rope_head_dim, c.kv_lora_rank
         eps = c.rms_norm_eps
@@ -217,6 +237,34 @@ class MLAAttention:
         if getattr(c, "mla_use_output_gate", False):
             o = o * torch.sigmoid(self._mm(x, self.g_w))
         return self._mm(o, self.o_w), cache
+
+    def decode_step(self, x: torch.Tensor, cache: MLACache | None = None):
+        """One token at batch 1 through k3_mla_step_decode (attention_mla.py:168-216): the
+        new latent row is written into the cache at position ``cache.length``."""
+        c = self.cfg
+        nh, nope, rope, vhd, klr = (c.num_attention_heads, c.qk_nope_head_dim, c.qk_rope_head_dim,
+                                    c.v_head_dim, c.kv_lora_rank)
+        hidden, ql = x.shape[-1], self.q_a.shape[0]
+        if cache is None:
+            cache = new_cache(1, klr, rope, 1, self.cache_dtype, x.device)
+        cache.reserve(1)
+        pos = cache.length
+        xin = T.contiguous_aligned(x.reshape(hidden))
+        if xin.dtype not in (torch.float32, torch.bfloat16):
+            xin = xin.to(torch.float32)
+        lat, rot = cache.latent[0], cache.rot[0]
+        nbytes = int(_lib.lib().k3_mla_step_workspace_size(hidden, ql, nh, nope, rope, vhd, klr, pos + 1))
+        ws = _workspace.get(x.device, nbytes, "mla_step")
+        out = torch.empty(hidden, dtype=torch.float32, device=x.device)
+        m = self._mats
+        _lib.call("k3_mla_step_decode", T.ptr(xin), T.dtype_code(xin.dtype), T.ptr(m["q_a"]), T.ptr(self._q_an32),
+                  T.ptr(m["q_b"]), T.ptr(m["kv_a"]), T.ptr(self._kv_an32), T.ptr(self.wk), T.ptr(self.wv),
+                  T.ptr(m["g"] if getattr(c, "mla_use_output_gate", False) else None), T.ptr(m["o"]), T.ptr(lat),
+                  lat.stride(0), T.ptr(rot), rot.stride(0), cache.capacity, pos, float(c.rms_norm_eps),
+                  float(c.q_head_dim ** -0.5), T.ptr(out), _lib.K3_F32, hidden, ql, nh, nope, rope, vhd, klr,
+                  T.ptr(ws), ws.numel(), T.stream(xin))
+        cache.length = pos + 1
+        return out.reshape(1, 1, hidden), cache
 
     def _dense(self, q, lat, rot, scale):
         """Multi-token form (prefill): absorbed scores with the causal mask, fp32."""

@@ -208,3 +208,75 @@ def test_mla_layer_incremental_decode_matches_one_shot_oracle():
     assert om.normwise_rel(inc[prefill:], full[prefill:]) <= 2e-2
     assert cache.bytes_per_token() == (512 + 64) * 2
     assert cache.nbytes_used() == T * (512 + 64) * 2
+
+
+def test_mla_fused_decode_step_matches_torch_step_and_oracle():
+    """bf16 projection weights select k3_mla_step_decode for the decode steps (projections,
+    norms, cache append, core, gate, o_proj in HIP).  Each step is checked against the same
+    module with the torch projections around the HIP core, on a copy of the same cache, and
+    against the fp64 restatement on the latents the fused step stored."""
+    from k3hip.mla import MLACache, MLAAttention
+    cfg = Cfg()
+    rng = np.random.default_rng(17)
+    w32 = {k: bf(v) for k, v in omla.random_mla_weights(rng, cfg).items()}
+    wdev = {k: torch.from_numpy(v).to(DEV).to(torch.bfloat16) for k, v in w32.items()}
+    wdev["q_a_layernorm.weight"] = torch.from_numpy(w32["q_a_layernorm.weight"]).to(DEV)
+    wdev["kv_a_layernorm.weight"] = torch.from_numpy(w32["kv_a_layernorm.weight"]).to(DEV)
+    fused, ref = MLAAttention(cfg, wdev), MLAAttention(cfg, wdev)
+    assert fused.fused_step
+    ref.fused_step = False
+    T, prefill = 262, 250                      # the decode steps cross the 256-row capacity step
+    x = (rng.standard_normal((1, T, cfg.hidden_size)) * 0.5).astype(np.float32)
+    xd = torch.from_numpy(x).to(DEV).to(torch.bfloat16)
+    _, cache = fused(xd[:, :prefill])
+    cref = MLACache(cache.latent.clone(), cache.rot.clone(), cache.length)
+    w = {k: v.astype(np.float64) for k, v in w32.items()}
+    nh, nope, klr, vhd = cfg.num_attention_heads, 128, 512, 128
+    kb = w["kv_b_proj.weight"].reshape(nh, nope + vhd, klr)
+    rms = lambda a, g: g * a / np.sqrt((a * a).mean(-1, keepdims=True) + cfg.rms_norm_eps)  # noqa: E731
+    xb = om.bf16_round(x[0]).astype(np.float64)
+    worst_ref = worst_oracle = 0.0
+    for t in range(prefill, T):
+        o, cache = fused(xd[:, t:t + 1], cache=cache)
+        o_ref, cref = ref(xd[:, t:t + 1], cache=cref)
+        assert cache.length == cref.length == t + 1
+        got = o.float().cpu().numpy().reshape(-1)
+        worst_ref = max(worst_ref, om.normwise_rel(got, o_ref.float().cpu().numpy().reshape(-1)))
+        d = (cache.latent[0, t].float() - cref.latent[0, t].float()).abs().max().item()
+        assert d <= 2 ** -7 * cref.latent[0, t].float().abs().max().item()       # one bf16 ulp at most
+        assert torch.equal(cache.rot[0, t], cref.rot[0, t]) or \
+            (cache.rot[0, t].float() - cref.rot[0, t].float()).abs().max().item() <= \
+            2 ** -7 * cref.rot[0, t].float().abs().max().item()
+        lat = cache.latent[0, :t + 1].float().cpu().numpy().astype(np.float64)
+        rot = cache.rot[0, :t + 1].float().cpu().numpy().astype(np.float64)
+        q = (rms(xb[t] @ w["q_a_proj.weight"].T, w["q_a_layernorm.weight"]) @ w["q_b_proj.weight"].T
+             ).reshape(nh, cfg.q_head_dim)
+        oo = omla.mla_decode_absorbed(q[:, :nope], q[:, nope:], kb[:, :nope], kb[:, nope:], lat, rot,
+                                      cfg.q_head_dim ** -0.5)[0].reshape(-1)
+        oo = oo / (1.0 + np.exp(-(xb[t] @ w["g_proj.weight"].T)))
+        worst_oracle = max(worst_oracle, om.normwise_rel(got, oo @ w["o_proj.weight"].T))
+    print(f"fused step vs torch step {worst_ref:.2e}, vs oracle {worst_oracle:.2e}")
+    assert worst_ref <= 1e-4 and worst_oracle <= 1e-4
+    assert cache.capacity == 512
+
+
+def test_mla_fused_decode_step_errors():
+    from k3hip import _lib
+    from k3hip.mla import MLAAttention
+    cfg = Cfg()
+    rng = np.random.default_rng(3)
+    wdev = {k: torch.from_numpy(v).to(DEV).to(torch.bfloat16) for k, v in omla.random_mla_weights(rng, cfg).items()}
+    attn = MLAAttention(cfg, wdev)
+    x = torch.randn(1, 1, cfg.hidden_size, device=DEV).to(torch.bfloat16)
+    o, cache = attn(x)                                  # no cache: a new one, position 0
+    assert cache.length == 1 and torch.isfinite(o).all()
+    lat, rot = cache.latent[0], cache.rot[0]
+    out = torch.empty(cfg.hidden_size, device=DEV)
+    ws = torch.empty(1 << 20, dtype=torch.uint8, device=DEV)
+    with pytest.raises(ValueError, match="outside the cache"):
+        _lib.call("k3_mla_step_decode", x.data_ptr(), _lib.K3_BF16, wdev["q_a_proj.weight"].data_ptr(),
+                  attn._q_an32.data_ptr(), wdev["q_b_proj.weight"].data_ptr(),
+                  wdev["kv_a_proj_with_mqa.weight"].data_ptr(), attn._kv_an32.data_ptr(), attn.wk.data_ptr(),
+                  attn.wv.data_ptr(), None, wdev["o_proj.weight"].data_ptr(), lat.data_ptr(), 512, rot.data_ptr(),
+                  64, cache.capacity, cache.capacity, 1e-5, 0.1, out.data_ptr(), _lib.K3_F32, cfg.hidden_size,
+                  cfg.q_lora_rank, cfg.num_attention_heads, 128, 64, 128, 512, ws.data_ptr(), ws.numel(), None)
