@@ -369,6 +369,51 @@ def bench_mla(torch, steps, warmup, dev):
     return sec, stats
 
 
+MS_HID, MS_QL = 7168, 1536
+MS_BYTES = (2 * (MS_QL * MS_HID + (512 + 64) * MS_HID + MLA_H * 128 * MS_HID + MLA_H * 192 * MS_QL
+                 + MS_HID * MLA_H * 128) + MLA_BYTES)                     # 357,490,688
+
+
+def bench_mla_step(torch, steps, warmup, dev):
+    """One decode token through a whole MLA layer at K3 shapes (k3_mla_step_decode): hidden
+    7168, q_lora_rank 1536, 64 heads (nope 128, rope 64, v 128), kv_lora_rank 512, output
+    gate, bf16 weights, the new cache row written at position 32767 of a bf16 cache.  Two
+    weight sets and four caches rotate (1.6 GB), so the MALL cannot hold them."""
+    from types import SimpleNamespace
+    from k3hip.mla import MLACache, MLAAttention
+    cfg = SimpleNamespace(hidden_size=MS_HID, num_attention_heads=MLA_H, q_lora_rank=MS_QL, kv_lora_rank=512,
+                          qk_nope_head_dim=128, qk_rope_head_dim=64, v_head_dim=128, q_head_dim=192,
+                          rms_norm_eps=1e-5, mla_use_output_gate=True)
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(1008)
+    bf = torch.bfloat16
+
+    def lin(o, i):
+        return (torch.randn(o, i, device=dev, generator=gen) / i ** 0.5).to(bf)
+
+    mods = []
+    for _ in range(2):
+        w = {"q_a_proj.weight": lin(MS_QL, MS_HID), "q_a_layernorm.weight": torch.ones(MS_QL, device=dev),
+             "q_b_proj.weight": lin(MLA_H * 192, MS_QL), "kv_a_proj_with_mqa.weight": lin(576, MS_HID),
+             "kv_a_layernorm.weight": torch.ones(512, device=dev), "kv_b_proj.weight": lin(MLA_H * 256, 512),
+             "g_proj.weight": lin(MLA_H * 128, MS_HID), "o_proj.weight": lin(MS_HID, MLA_H * 128)}
+        mods.append(MLAAttention(cfg, w))
+    pos = MLA_T - 1
+    caches = [MLACache(torch.randn(1, MLA_T, 512, device=dev, generator=gen).to(bf),
+                       torch.randn(1, MLA_T, 64, device=dev, generator=gen).to(bf), pos) for _ in range(4)]
+    xs = torch.randn(8, 1, 1, MS_HID, device=dev, generator=gen).to(bf)
+
+    def step(i):
+        c = caches[i % 4]
+        c.length = pos
+        mods[i % 2].decode_step(xs[i % 8], c)
+
+    sec, _ = graph_time(torch, step, steps, warmup)
+    stats = None if EAGER else step_stats(torch, step, 32)
+    del mods, caches
+    return sec, stats
+
+
 def bench_read_ceiling(torch, nbytes, steps, dev):
     """One streaming-read launch of nbytes (the library's calibration kernel), rotating
     over >= 1.5 GB of buffers: the bandwidth a single launch of this size can reach."""
@@ -436,7 +481,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=64)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
-    ap.add_argument("--workloads", default="expert,layer,k3layer,ingest,prefill,gemv,mla,ceiling")
+    ap.add_argument("--workloads", default="expert,layer,k3layer,ingest,prefill,gemv,mla,mlastep,ceiling")
     ap.add_argument("--eager", action="store_true",
                     help="launch steps one by one instead of replaying a HIP graph (profiler counter runs)")
     args = ap.parse_args()
@@ -527,6 +572,15 @@ def main():
                               "pct_hbm_peak": round(100 * mgbs / HBM_PEAK_GBS, 1), "bytes": MLA_BYTES,
                               "heads": MLA_H, "tokens": MLA_T, "kv_lora_rank": 512, "rope": 64,
                               "cache": "bf16", "launches": 3, "step_us": mstats}
+    if "mlastep" in work:
+        ms_ = min(K, 128)
+        ssec, sstats = bench_mla_step(torch, ms_, min(W, 16), dev)
+        sus = ssec / ms_ * 1e6
+        sgbs = MS_BYTES / (sus * 1e-6) / 1e9
+        line["mla_step"] = {"us": round(sus, 2), "GB/s": round(sgbs, 1), "pct_hbm_peak": round(100 * sgbs / HBM_PEAK_GBS, 1),
+                            "bytes": MS_BYTES, "hidden": MS_HID, "q_lora_rank": MS_QL, "heads": MLA_H,
+                            "tokens": MLA_T, "weights": "bf16", "output_gate": True, "launches": 6,
+                            "step_us": sstats}
     if "ceiling" in work:
         ce = bench_read_ceiling(torch, EXPERT_BYTES, 256, dev)
         cl = bench_read_ceiling(torch, LAYER_BYTES, 64, dev)

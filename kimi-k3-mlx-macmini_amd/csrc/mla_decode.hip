@@ -479,6 +479,7 @@ struct MergeArgs {
     int64_t ld_out;
     int H, NS, V;
     int out_bf16;
+    const float *gate;     // [H, V] logits or null: o *= sigmoid(gate) (the MLA output gate)
 };
 
 __device__ __forceinline__ float block_sum256(float v, float *red) {
@@ -528,6 +529,9 @@ __global__ __launch_bounds__(256) void mla_merge_uv_kernel(MergeArgs a) {
         w[u] = v < a.V ? *reinterpret_cast<const uint4 *>(a.w_uv + (static_cast<int64_t>(h) * a.V + v) * kR + lane * 8)
                        : make_uint4(0u, 0u, 0u, 0u);
     }
+    // output-gate logit of row r0 + lane (lanes below kMergeRows / 4), read with the rows
+    float gv = 0.f;
+    if (a.gate && lane < kMergeRows / 4 && r0 + lane < a.V) gv = a.gate[static_cast<int64_t>(h) * a.V + r0 + lane];
     // split maxima and sums
     float2 mlv[kMaxSplits / 256];
 #pragma unroll
@@ -602,6 +606,7 @@ __global__ __launch_bounds__(256) void mla_merge_uv_kernel(MergeArgs a) {
             o = fmaf(__uint_as_float(wd[q] & 0xffff0000u), c8[2 * q + 1], o);
         }
         o = wave_sum_to_lane63(o);
+        if (a.gate) o /= 1.0f + expf(-readlane_f(gv, u));
         if (lane == 63 && v < a.V) {
             const int64_t oi = static_cast<int64_t>(h) * a.ld_out + v;
             if (a.out_bf16)
@@ -661,6 +666,16 @@ extern "C" int k3_mla_decode_absorbed(const void *q_nope, const void *q_rot, int
                                       int64_t rope_dim, int64_t nope_dim, int64_t v_dim, float scale, void *out,
                                       int out_dtype, int64_t ld_out, void *workspace, int64_t workspace_bytes,
                                       void *stream) {
+    return k3::mla_decode_core(q_nope, q_rot, ld_q, ld_q_rot, q_dtype, w_uk, w_uv, lat, ld_lat, rot, ld_rot, T, H,
+                               kv_lora_rank, rope_dim, nope_dim, v_dim, scale, out, out_dtype, ld_out, nullptr,
+                               workspace, workspace_bytes, stream);
+}
+
+int k3::mla_decode_core(const void *q_nope, const void *q_rot, int64_t ld_q, int64_t ld_q_rot, int q_dtype,
+                        const void *w_uk, const void *w_uv, const void *lat, int64_t ld_lat, const void *rot,
+                        int64_t ld_rot, int64_t T, int64_t H, int64_t kv_lora_rank, int64_t rope_dim,
+                        int64_t nope_dim, int64_t v_dim, float scale, void *out, int out_dtype, int64_t ld_out,
+                        const float *gate, void *workspace, int64_t workspace_bytes, void *stream) {
     if (!q_nope || !q_rot || !w_uk || !w_uv || !lat || !rot || !out || !workspace)
         return set_error(K3_ERR_NULL, "mla decode: null pointer");
     if (q_dtype != K3_F32 && q_dtype != K3_BF16) return set_error(K3_ERR_DTYPE, "mla decode: q_dtype %d", q_dtype);
@@ -735,7 +750,7 @@ extern "C" int k3_mla_decode_absorbed(const void *q_nope, const void *q_rot, int
     if (rc) return rc;
 
     MergeArgs ma{part, ml, static_cast<const uint16_t *>(w_uv), out, ld_out, static_cast<int>(H), NS,
-                 static_cast<int>(v_dim), out_dtype == K3_BF16};
+                 static_cast<int>(v_dim), out_dtype == K3_BF16, gate};
     mla_merge_uv_kernel<<<dim3(static_cast<unsigned>(H * cdiv(v_dim, kMergeRows))), 256, 0, st>>>(ma);
     return check_hip(hipGetLastError(), "mla decode: merge and W_UV launch");
 }

@@ -13,8 +13,9 @@
 //   S2  rows of q_b against the normalised q_a output (every block normalises the 1536-wide
 //       vector itself, so no launch is spent on it), and one block that normalises the kv
 //       latent and writes the new cache row (bf16) at position pos;
-//   core  k3_mla_decode_absorbed (three launches) over the pos + 1 cache rows;
-//   S3  rows of o_proj against o * sigmoid(gate).
+//   core  the absorbed core of k3_mla_decode_absorbed (three launches) over the pos + 1
+//       cache rows, its last launch multiplying o by sigmoid(gate) as it writes it;
+//   S3  rows of o_proj against the gated o.
 // Every row kernel issues its weight rows first, then stages its fp32 input vector in LDS
 // (K floats), then reduces: a lane takes 16-byte chunks (8 bf16) l, l + 64, ... of a row.
 #include <algorithm>
@@ -296,13 +297,13 @@ extern "C" int k3_mla_step_decode(const void *x, int x_dtype, const void *q_a, c
     rc = launch_rows<kModeNorm>(b, st);
     if (rc) return rc;
     // core over the pos + 1 cache rows
-    rc = k3_mla_decode_absorbed(q, q + nope_dim, qhd, qhd, K3_F32, w_uk, w_uv, lat, ld_lat, rot, ld_rot, T, heads,
-                                kv_lora_rank, rope_dim, nope_dim, v_dim, scale, o, K3_F32, v_dim, ws + L.core,
-                                workspace_bytes - static_cast<int64_t>(L.core), stream);
+    rc = mla_decode_core(q, q + nope_dim, qhd, qhd, K3_F32, w_uk, w_uv, lat, ld_lat, rot, ld_rot, T, heads,
+                         kv_lora_rank, rope_dim, nope_dim, v_dim, scale, o, K3_F32, v_dim, g_proj ? gl : nullptr,
+                         ws + L.core, workspace_bytes - static_cast<int64_t>(L.core), stream);
     if (rc) return rc;
-    // S3: o_proj rows against o * sigmoid(gate)
+    // S3: o_proj rows against the gated o
     RowsArgs c{};
-    c.o = o, c.gl = g_proj ? gl : nullptr, c.K = static_cast<int>(hv);
+    c.o = o, c.gl = nullptr, c.K = static_cast<int>(hv);
     c.w[0] = static_cast<const uint16_t *>(o_proj), c.N[0] = static_cast<int>(hidden);
     c.out = out, c.out_bf16 = out_dtype == K3_BF16;
     return launch_rows<kModeGate>(c, st);
