@@ -269,7 +269,7 @@ class RoutedMoE:
             outs.append(out)
             if return_router:
                 recs.append(self._records(ws))
-        y = torch.cat(outs).reshape(*orig[:-1], self._H)
+        y = (outs[0] if len(outs) == 1 else torch.cat(outs)).reshape(*orig[:-1], self._H)
         if not return_router:
             return y
         r = RouterResult(*(torch.cat([getattr(rr, f) for rr in recs]) for f in
