@@ -414,6 +414,37 @@ def bench_mla_step(torch, steps, warmup, dev):
     return sec, stats
 
 
+KDA_H, KDA_D = 96, 128
+KDA_BYTES = 2 * KDA_H * KDA_D * KDA_D * 4 + KDA_H * KDA_D * 4 * 5 + KDA_H * 4   # 12,829,056
+
+
+def bench_kda(torch, steps, warmup, dev):
+    """One KDA recurrent decode step (k3_kda_recurrent_decode) at K3 shapes: 96 heads,
+    128 x 128 fp32 state per head (6 MiB, read and written in place), fp32 q/k/v/g/beta.
+    32 states rotate (403 MB), so the MALL cannot hold them."""
+    import ctypes
+    from k3hip import _lib
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(1009)
+    states = [torch.randn(KDA_H, KDA_D, KDA_D, device=dev, generator=gen) * 0.1 for _ in range(32)]
+    q, k, v = (torch.nn.functional.normalize(torch.randn(KDA_H, KDA_D, device=dev, generator=gen), dim=-1)
+               for _ in range(3))
+    g = -5.0 * torch.sigmoid(torch.randn(KDA_H, KDA_D, device=dev, generator=gen))
+    beta = torch.sigmoid(torch.randn(KDA_H, device=dev, generator=gen))
+    out = torch.empty(KDA_H, KDA_D, device=dev)
+
+    def step(i):
+        st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+        _lib.call("k3_kda_recurrent_decode", q.data_ptr(), k.data_ptr(), v.data_ptr(), g.data_ptr(), beta.data_ptr(),
+                  _lib.K3_F32, states[i % 32].data_ptr(), out.data_ptr(), _lib.K3_F32, KDA_H, KDA_H, KDA_D, KDA_D,
+                  KDA_D ** -0.5, st)
+
+    sec, _ = graph_time(torch, step, steps, warmup)
+    stats = None if EAGER else step_stats(torch, step, 32)
+    del states
+    return sec, stats
+
+
 def bench_read_ceiling(torch, nbytes, steps, dev):
     """One streaming-read launch of nbytes (the library's calibration kernel), rotating
     over >= 1.5 GB of buffers: the bandwidth a single launch of this size can reach."""
@@ -481,7 +512,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=64)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
-    ap.add_argument("--workloads", default="expert,layer,k3layer,ingest,prefill,gemv,mla,mlastep,ceiling")
+    ap.add_argument("--workloads", default="expert,layer,k3layer,ingest,prefill,gemv,mla,mlastep,kda,ceiling")
     ap.add_argument("--eager", action="store_true",
                     help="launch steps one by one instead of replaying a HIP graph (profiler counter runs)")
     args = ap.parse_args()
@@ -581,6 +612,14 @@ def main():
                             "bytes": MS_BYTES, "hidden": MS_HID, "q_lora_rank": MS_QL, "heads": MLA_H,
                             "tokens": MLA_T, "weights": "bf16", "output_gate": True, "launches": 6,
                             "step_us": sstats}
+    if "kda" in work:
+        ks_ = min(K, 256)
+        kdsec, kdstats = bench_kda(torch, ks_, min(W, 32), dev)
+        kus = kdsec / ks_ * 1e6
+        kgb = KDA_BYTES / (kus * 1e-6) / 1e9
+        line["kda_decode"] = {"us": round(kus, 3), "GB/s": round(kgb, 1), "pct_hbm_peak": round(100 * kgb / HBM_PEAK_GBS, 1),
+                              "bytes": KDA_BYTES, "heads": KDA_H, "key_dim": KDA_D, "value_dim": KDA_D,
+                              "state": "fp32, in place", "launches": 1, "step_us": kdstats}
     if "ceiling" in work:
         ce = bench_read_ceiling(torch, EXPERT_BYTES, 256, dev)
         cl = bench_read_ceiling(torch, LAYER_BYTES, 64, dev)

@@ -237,6 +237,22 @@ int k3_mla_step_decode(const void *x, int x_dtype, const void *q_a, const float 
                        int64_t rope_dim, int64_t v_dim, int64_t kv_lora_rank, void *workspace,
                        int64_t workspace_bytes, void *stream);
 
+/* ---- Kimi Delta Attention recurrent step (one token) -------------------------------------- */
+
+/* For every value head h (q/k head h / (v_heads / qk_heads)), on the fp32 state
+ * S [v_heads, key_dim, value_dim] in place:
+ *   S[h] = S[h] * exp(g[h])[:, None];  S[h] += (beta[h] k) (x) (v[h] - k . S[h]);
+ *   out[h] = (scale q) . S[h]
+ * q, k [qk_heads, key_dim], v [v_heads, value_dim], g [v_heads, key_dim], beta [v_heads]:
+ * in_dtype (K3_F32 / K3_BF16) for all five; out [v_heads, value_dim] out_dtype.  key_dim
+ * must be 128 (K3's KDA heads), value_dim a multiple of 32.  fp32 arithmetic, fixed
+ * reduction order.  Replaces one step of KDAAttention._recurrent
+ * (air_llm/models/kimi_k3/attention_kda.py:65-90; naive_recurrent_kda,
+ * k3ref/_vendor/kda_naive.py:46-60). */
+int k3_kda_recurrent_decode(const void *q, const void *k, const void *v, const void *g, const void *beta,
+                            int in_dtype, float *state, void *out, int out_dtype, int64_t qk_heads,
+                            int64_t v_heads, int64_t key_dim, int64_t value_dim, float scale, void *stream);
+
 /* ---- HBM calibration ------------------------------------------------------------------- */
 
 /* Streaming read of `bytes` (multiple of 16) from src; sink is a >= 4096-byte device scratch

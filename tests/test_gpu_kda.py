@@ -1,0 +1,74 @@
+"""GPU parity of the KDA recurrent step (k3_kda_recurrent_decode) against the fp64 oracle
+(oracle/kda.py, restating attention_kda.py:65-90).  fp32 state and arithmetic; the bar is
+normwise max-relative 1e-5 per step for output and state, over multi-step sequences (the
+state carries every step's rounding forward)."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import kda as okda
+from oracle import mxfp4 as om
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+TOL = 1e-5
+
+
+def _inputs(rng, B, Tn, H, HV, K=128, V=128):
+    q = okda.l2norm(rng.standard_normal((B, Tn, H, K))).astype(np.float32)
+    k = okda.l2norm(rng.standard_normal((B, Tn, H, K))).astype(np.float32)
+    v = rng.standard_normal((B, Tn, HV, V)).astype(np.float32)
+    g = (-5.0 / (1.0 + np.exp(-rng.standard_normal((B, Tn, HV, K))))).astype(np.float32)
+    beta = (1.0 / (1.0 + np.exp(-rng.standard_normal((B, Tn, HV))))).astype(np.float32)
+    S0 = (rng.standard_normal((B, HV, K, V)) * 0.5).astype(np.float32)
+    return q, k, v, g, beta, S0
+
+
+def _dev(*a, dtype=torch.float32):
+    return [torch.from_numpy(np.ascontiguousarray(x)).to(DEV).to(dtype) for x in a]
+
+
+@pytest.mark.parametrize("B,Tn,H,HV,V", [(1, 1, 96, 96, 128), (1, 5, 4, 4, 128), (2, 3, 3, 6, 64), (1, 2, 2, 2, 256)])
+def test_kda_matches_oracle(B, Tn, H, HV, V):
+    from k3hip.kda import kda_recurrent
+    rng = np.random.default_rng(B * 100 + Tn * 10 + HV)
+    q, k, v, g, beta, S0 = _inputs(rng, B, Tn, H, HV, V=V)
+    o, S = kda_recurrent(*_dev(q, k, v, g, beta), state=_dev(S0)[0])
+    want_o, want_S = okda.kda_recurrent(q, k, v, g, beta, None, S0)
+    ro = om.normwise_rel(o.cpu().numpy(), want_o)
+    rs = om.normwise_rel(S.cpu().numpy(), want_S)
+    print(f"B={B} T={Tn} H={H} HV={HV} V={V}: out {ro:.2e} state {rs:.2e}")
+    assert ro <= TOL and rs <= TOL
+
+
+def test_kda_bf16_inputs_zero_state_and_in_place():
+    """bf16 q/k/v/g/beta (read as their bf16 values); no initial state; the fp32 state
+    passed back in is updated in place; the delta rule at beta = 1 writes v at the key."""
+    from k3hip.kda import kda_recurrent
+    rng = np.random.default_rng(7)
+    q, k, v, g, beta, _ = _inputs(rng, 1, 1, 8, 8)
+    qb, kb, vb, gb, bb = (om.bf16_round(a) for a in (q, k, v, g, beta))
+    o, S = kda_recurrent(*_dev(qb, kb, vb, gb, bb, dtype=torch.bfloat16))
+    want_o, want_S = okda.kda_recurrent(qb, kb, vb, gb, bb, None, None)
+    assert om.normwise_rel(o.cpu().numpy(), want_o) <= TOL and om.normwise_rel(S.cpu().numpy(), want_S) <= TOL
+    ptr = S.data_ptr()
+    k1 = kb / np.linalg.norm(kb.astype(np.float64), axis=-1, keepdims=True).astype(np.float32)
+    o2, S2 = kda_recurrent(*_dev(q, k1, v, g, np.ones_like(beta)), state=S)
+    assert S2.data_ptr() == ptr
+    ks = np.einsum("hk,hkv->hv", k1[0, 0].astype(np.float64), S2[0].double().cpu().numpy())
+    assert np.abs(ks - v[0, 0]).max() <= 1e-4 * np.abs(v).max()
+
+
+def test_kda_is_deterministic_and_validates():
+    from k3hip.kda import kda_recurrent
+    rng = np.random.default_rng(9)
+    q, k, v, g, beta, S0 = _inputs(rng, 1, 3, 4, 4)
+    a = kda_recurrent(*_dev(q, k, v, g, beta), state=_dev(S0)[0])
+    b = kda_recurrent(*_dev(q, k, v, g, beta), state=_dev(S0)[0])
+    assert torch.equal(a[0], b[0]) and torch.equal(a[1], b[1])
+    with pytest.raises(ValueError):
+        kda_recurrent(*_dev(q[..., :64], k[..., :64], v, g[..., :64], beta))     # key_dim != 128
+    with pytest.raises(ValueError):
+        kda_recurrent(*_dev(q, k, v[..., :48], g, beta))                        # V not a multiple of 32
