@@ -253,6 +253,28 @@ int k3_kda_recurrent_decode(const void *q, const void *k, const void *v, const v
                             int in_dtype, float *state, void *out, int out_dtype, int64_t qk_heads,
                             int64_t v_heads, int64_t key_dim, int64_t value_dim, float scale, void *stream);
 
+/* Workspace bytes k3_kda_step_decode needs for `heads` heads of 128 (projection outputs and
+ * the recurrence output).  No initialisation. */
+int64_t k3_kda_step_workspace_size(int64_t heads);
+
+/* KDAAttention.__call__ for one token at batch 1 (air_llm/models/kimi_k3/attention_kda.py:94-115):
+ *   q, k, v = silu(short_conv(x W^T)) with the convolution state (ops.py:46-60); q, k L2-normalised
+ *   per head (eps 1e-6); g = gate_lower_bound * sigmoid(exp(A_log[h]) * (f_b(f_a x) + dt_bias));
+ *   beta = sigmoid(b x); the recurrence of k3_kda_recurrent_decode on `state` (in place) with
+ *   scale 128^-0.5; o = gated_rmsnorm(o, o_norm, g_proj x) per head (ops.py:36-39); out = o o_proj^T.
+ * q/k/v/g_proj [heads*128, hidden], o_proj [hidden, heads*128], f_a [128, hidden],
+ * f_b [heads*128, 128], b_proj [heads, hidden]: bf16.  q/k/v_conv [heads*128, conv_size],
+ * o_norm [128], A_log [>= heads], dt_bias [heads*128]: fp32.  conv_in / conv_out
+ * [3, conv_size - 1, heads*128] fp32 (q, k, v; oldest input first): distinct buffers, conv_out
+ * receives the shifted window.  head_dim must be 128; heads*128 and hidden <= 12288.
+ * Four stream-ordered launches. */
+int k3_kda_step_decode(const void *x, int x_dtype, const void *q_proj, const void *k_proj, const void *v_proj,
+                       const void *g_proj, const void *o_proj, const void *f_a, const void *f_b, const void *b_proj,
+                       const float *q_conv, const float *k_conv, const float *v_conv, const float *conv_in,
+                       float *conv_out, const float *o_norm, const float *A_log, const float *dt_bias, float *state,
+                       void *out, int out_dtype, int64_t hidden, int64_t heads, int64_t head_dim, int64_t conv_size,
+                       float gate_lower_bound, float eps, void *workspace, int64_t workspace_bytes, void *stream);
+
 /* ---- HBM calibration ------------------------------------------------------------------- */
 
 /* Streaming read of `bytes` (multiple of 16) from src; sink is a >= 4096-byte device scratch

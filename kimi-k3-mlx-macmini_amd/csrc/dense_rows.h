@@ -1,0 +1,214 @@
+// Dense bf16 row kernels for batch-1 decode steps: a launch takes up to six row sets
+// [N, K] (bf16, row-major) that share one fp32 input vector of K values, staged in LDS,
+// and writes one fp32 dot product per row.  The vector is built in the prologue:
+//   kModeX         x itself (bf16 or fp32)
+//   kModeNorm      rmsnorm(src) * nw over all K values (every block normalises it)
+//   kModeGate      a fp32 vector as is (gl null) or times sigmoid(gl)
+//   kModeHeadNorm  per head of hd values: rmsnorm over the head * nw[i] * sigmoid(gl)
+// Every block issues its weight rows first, then stages the vector, then reduces: a lane
+// takes 16-byte chunks (8 bf16) l, l + 64, ... of a row; R rows per wave, 4 waves.
+#pragma once
+
+#include "k3_common.h"
+
+namespace k3 {
+namespace {
+
+enum { kModeX = 0, kModeNorm = 1, kModeGate = 2, kModeHeadNorm = 3 };
+constexpr int kRowSets = 6;
+constexpr int kMaxWidth = 12288;  // input vector width (fp32 in LDS: 48 KB)
+
+struct RowsArgs {
+    const void *x;            // kModeX: [K] bf16 or fp32
+    int x_bf16;
+    const float *src, *nw;    // kModeNorm: v = src * rsqrt(mean(src^2) + eps) * nw
+    float eps;
+    const float *o, *gl;      // kModeGate / kModeHeadNorm: the vector and its gate logits
+    int K;
+    const uint16_t *w[kRowSets];   // bf16 row sets [N, K] sharing v (null: unused)
+    int N[kRowSets];
+    int blocks[kRowSets];
+    float *y[kRowSets];            // fp32 outputs [N] (when out is null)
+    void *out;                     // not null: set 0's outputs go here, fp32 or bf16
+    int out_bf16;
+    int hd;                        // kModeHeadNorm: values per head
+    // kModeNorm, last block: the cache append
+    const float *ckv, *kvw;   // ckv [r + rope] fp32, kv_a_layernorm [r]
+    uint16_t *lat_row, *rot_row;
+    int r, rope, append;
+};
+
+__device__ __forceinline__ float block_sum(float v, float *red) {
+    v = wave_sum_all(v);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+    __syncthreads();
+    const float t = red[0] + red[1] + red[2] + red[3];
+    __syncthreads();
+    return t;
+}
+
+// v (fp32, K values) into LDS; ends with a block barrier
+template <int MODE>
+__device__ __forceinline__ void stage_vector(const RowsArgs &a, float *vs, float *red) {
+    const int K = a.K;
+    if (MODE == kModeX) {
+        if (a.x_bf16) {
+            const uint4 *x8 = static_cast<const uint4 *>(a.x);
+            for (int c = threadIdx.x; c < K / 8; c += 256) {
+                const uint4 q = x8[c];
+                const uint32_t d[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    vs[8 * c + 2 * i] = __uint_as_float(d[i] << 16);
+                    vs[8 * c + 2 * i + 1] = __uint_as_float(d[i] & 0xffff0000u);
+                }
+            }
+        } else {
+            const float4 *x4 = static_cast<const float4 *>(a.x);
+            for (int c = threadIdx.x; c < K / 4; c += 256) reinterpret_cast<float4 *>(vs)[c] = x4[c];
+        }
+    } else if (MODE == kModeNorm) {
+        float ss = 0.f;
+        for (int c = threadIdx.x; c < K / 4; c += 256) {
+            const float4 s = reinterpret_cast<const float4 *>(a.src)[c];
+            ss = fmaf(s.x, s.x, fmaf(s.y, s.y, fmaf(s.z, s.z, fmaf(s.w, s.w, ss))));
+            reinterpret_cast<float4 *>(vs)[c] = s;
+        }
+        const float rs = 1.0f / sqrtf(block_sum(ss, red) / static_cast<float>(K) + a.eps);
+        for (int c = threadIdx.x; c < K / 4; c += 256) {
+            const float4 g = reinterpret_cast<const float4 *>(a.nw)[c];
+            float4 v = reinterpret_cast<float4 *>(vs)[c];
+            v.x = v.x * rs * g.x, v.y = v.y * rs * g.y, v.z = v.z * rs * g.z, v.w = v.w * rs * g.w;
+            reinterpret_cast<float4 *>(vs)[c] = v;
+        }
+    } else if (MODE == kModeHeadNorm) {
+        const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+        for (int hh = wave; hh < K / a.hd; hh += 4) {
+            float ss = 0.f;
+            for (int i = lane; i < a.hd; i += 64) ss = fmaf(a.o[hh * a.hd + i], a.o[hh * a.hd + i], ss);
+            const float rs = 1.0f / sqrtf(wave_sum_all(ss) / static_cast<float>(a.hd) + a.eps);
+            for (int i = lane; i < a.hd; i += 64) {
+                const int c = hh * a.hd + i;
+                vs[c] = a.o[c] * rs * a.nw[i] / (1.0f + expf(-a.gl[c]));
+            }
+        }
+    } else {
+        for (int c = threadIdx.x; c < K / 4; c += 256) {
+            float4 v = reinterpret_cast<const float4 *>(a.o)[c];
+            if (a.gl) {
+                const float4 g = reinterpret_cast<const float4 *>(a.gl)[c];
+                v.x /= 1.0f + expf(-g.x), v.y /= 1.0f + expf(-g.y), v.z /= 1.0f + expf(-g.z),
+                    v.w /= 1.0f + expf(-g.w);
+            }
+            reinterpret_cast<float4 *>(vs)[c] = v;
+        }
+    }
+    __syncthreads();
+}
+
+// c_new = rmsnorm(ckv[:r]) * kv_a_layernorm -> lat_row (bf16); rot_row = bf16(ckv[r:])
+__device__ void append_row(const RowsArgs &a, float *red) {
+    float ss = 0.f;
+    for (int j = threadIdx.x; j < a.r; j += 256) ss = fmaf(a.ckv[j], a.ckv[j], ss);
+    const float rs = 1.0f / sqrtf(block_sum(ss, red) / static_cast<float>(a.r) + a.eps);
+    for (int j = threadIdx.x; j < a.r; j += 256) a.lat_row[j] = f32_to_bf16(a.ckv[j] * rs * a.kvw[j]);
+    for (int j = threadIdx.x; j < a.rope; j += 256) a.rot_row[j] = f32_to_bf16(a.ckv[a.r + j]);
+}
+
+// 8 bf16 weights . 8 fp32 values
+__device__ __forceinline__ float dot8_bf16_f32(uint4 w, float4 v0, float4 v1, float acc) {
+    acc = fmaf(__uint_as_float(w.x << 16), v0.x, acc);
+    acc = fmaf(__uint_as_float(w.x & 0xffff0000u), v0.y, acc);
+    acc = fmaf(__uint_as_float(w.y << 16), v0.z, acc);
+    acc = fmaf(__uint_as_float(w.y & 0xffff0000u), v0.w, acc);
+    acc = fmaf(__uint_as_float(w.z << 16), v1.x, acc);
+    acc = fmaf(__uint_as_float(w.z & 0xffff0000u), v1.y, acc);
+    acc = fmaf(__uint_as_float(w.w << 16), v1.z, acc);
+    acc = fmaf(__uint_as_float(w.w & 0xffff0000u), v1.w, acc);
+    return acc;
+}
+
+// Block: 4 waves x R rows of one row set; CH 16-byte chunks per lane per row.
+template <int MODE, int CH, int R>
+__global__ __launch_bounds__(256) void step_rows_kernel(RowsArgs a) {
+    extern __shared__ float vs[];
+    __shared__ float red[4];
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+    if (MODE == kModeNorm && a.append && static_cast<int>(blockIdx.x) == static_cast<int>(gridDim.x) - 1) {
+        append_row(a, red);
+        return;
+    }
+    int b = blockIdx.x, s = 0;
+    while (s < kRowSets - 1 && b >= a.blocks[s]) b -= a.blocks[s++];
+    const int N = a.N[s], K = a.K, nch = K >> 3;
+    const uint32_t rowb = static_cast<uint32_t>(K) * 2u;
+    const int n0 = (b * 4 + wave) * R;
+    const auto rw = make_rsrc(a.w[s], static_cast<uint32_t>(N) * rowb);
+    // 1. the wave's rows
+    uint4 wr[R][CH];
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+        for (int u = 0; u < CH; ++u) {
+            const int c = u * 64 + lane, n = n0 + r;
+            wr[r][u] = buf_load16(rw, (n < N && c < nch) ? static_cast<uint32_t>(n) * rowb + c * 16u : kOobOffset);
+        }
+    // 2. the input vector
+    stage_vector<MODE>(a, vs, red);
+    // 3. row dots
+    const float4 *v4 = reinterpret_cast<const float4 *>(vs);
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        float acc0 = 0.f, acc1 = 0.f;
+#pragma unroll
+        for (int u = 0; u < CH; ++u) {
+            const int c = u * 64 + lane;
+            if (c < nch) {
+                if (u & 1)
+                    acc1 = dot8_bf16_f32(wr[r][u], v4[2 * c], v4[2 * c + 1], acc1);
+                else
+                    acc0 = dot8_bf16_f32(wr[r][u], v4[2 * c], v4[2 * c + 1], acc0);
+            }
+        }
+        const float t = wave_sum_to_lane63(acc0 + acc1);
+        const int n = n0 + r;
+        if (lane == 63 && n < N) {
+            if (a.out) {
+                if (a.out_bf16)
+                    static_cast<uint16_t *>(a.out)[n] = f32_to_bf16(t);
+                else
+                    static_cast<float *>(a.out)[n] = t;
+            } else {
+                a.y[s][n] = t;
+            }
+        }
+    }
+}
+
+template <int MODE, int CH>
+int launch_rows_ch(RowsArgs &a, hipStream_t st) {
+    constexpr int R = CH >= 16 ? 1 : (CH >= 8 ? 2 : (CH >= 4 ? 4 : 8));
+    int total = 0;
+    for (int s = 0; s < kRowSets; ++s) {
+        a.blocks[s] = a.w[s] ? static_cast<int>(cdiv(a.N[s], 4 * R)) : 0;
+        total += a.blocks[s];
+    }
+    if (MODE == kModeNorm && a.append) ++total;
+    step_rows_kernel<MODE, CH, R><<<dim3(static_cast<unsigned>(total)), 256, static_cast<size_t>(a.K) * 4, st>>>(a);
+    return check_hip(hipGetLastError(), "dense rows launch");
+}
+
+template <int MODE>
+int launch_rows(RowsArgs &a, hipStream_t st) {
+    const int ch = static_cast<int>(cdiv(a.K / 8, 64));
+    if (ch <= 1) return launch_rows_ch<MODE, 1>(a, st);
+    if (ch <= 2) return launch_rows_ch<MODE, 2>(a, st);
+    if (ch <= 4) return launch_rows_ch<MODE, 4>(a, st);
+    if (ch <= 8) return launch_rows_ch<MODE, 8>(a, st);
+    if (ch <= 16) return launch_rows_ch<MODE, 16>(a, st);
+    if (ch <= 24) return launch_rows_ch<MODE, 24>(a, st);
+    return set_error(K3_ERR_SHAPE, "dense rows: input width %d above %d", a.K, kMaxWidth);
+}
+
+}  // namespace
+}  // namespace k3

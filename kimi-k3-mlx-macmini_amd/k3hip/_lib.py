@@ -52,6 +52,9 @@ SIGNATURES: dict[str, list] = {
     "k3_mla_step_decode": [_P, _I32, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _P, _I64, _I64, _I64, _F32,
                            _F32, _P, _I32, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _P, _I64, _P],
     "k3_kda_recurrent_decode": [_P, _P, _P, _P, _P, _I32, _P, _P, _I32, _I64, _I64, _I64, _I64, _F32, _P],
+    "k3_kda_step_workspace_size": [_I64],
+    "k3_kda_step_decode": [_P, _I32, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I32,
+                           _I64, _I64, _I64, _I64, _F32, _F32, _P, _I64, _P],
     "k3_moe_grouped_workspace_size": [_I64, _I64, _I64, _I64, _I64],
     "k3_moe_grouped_ffn": [_P, _I32, _P, _P, _P, _P, _I32, _I64, _I64, _I64, _I64, _I64, _I32, _F32, _F32,
                            _P, _I64, _P],
@@ -64,6 +67,7 @@ _RESTYPE = {"k3_last_error": ctypes.c_char_p, "k3_version": ctypes.c_char_p,
             "k3_moe_latent_layer_workspace_size": ctypes.c_int64,
             "k3_mla_workspace_size": ctypes.c_int64,
             "k3_mla_step_workspace_size": ctypes.c_int64,
+            "k3_kda_step_workspace_size": ctypes.c_int64,
             "k3_moe_grouped_workspace_size": ctypes.c_int64}
 
 

@@ -1,5 +1,11 @@
-"""Kimi Delta Attention recurrence on MI355X -- the counterpart of
-``KDAAttention._recurrent`` (air_llm/models/kimi_k3/attention_kda.py:65-90).
+"""Kimi Delta Attention on MI355X -- the counterpart of ``KDAAttention``
+(air_llm/models/kimi_k3/attention_kda.py:32-115).
+
+``KDAAttention(cfg, w)`` keeps the reference constructor, weight names and
+``__call__(x, state=None, conv=None) -> (out, state, (cq, ck, cv))``; every token of every
+sequence is one ``k3_kda_step_decode`` (projections, short convolutions, norms, gate,
+recurrence, gated RMSNorm, o_proj in four launches).  The recurrent state is fp32
+[B, H, 128, 128], updated in place; the convolution states come back as fp32 [B, k-1, C].
 
 ``kda_recurrent(q, k, v, g, beta, scale, state)`` takes the reference's tensors
 (q, k [B, T, H, K]; v [B, T, HV, V]; g [B, T, HV, K] log decay; beta [B, T, HV]; state
@@ -12,7 +18,7 @@ from __future__ import annotations
 
 import torch
 
-from . import _lib
+from . import _lib, _workspace
 from . import _torch as T
 
 
@@ -50,3 +56,68 @@ def kda_recurrent(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, g: torch.Te
         _lib.call("k3_kda_recurrent_decode", T.ptr(q[i]), T.ptr(k[i]), T.ptr(v[i]), T.ptr(g[i]), T.ptr(beta[i]),
                   code, T.ptr(S), T.ptr(o[i]), _lib.K3_F32, B * H, B * HV, K, V, float(scale), st)
     return o.transpose(0, 1), S
+
+
+class KDAAttention:
+    """Drop-in for KDAAttention (attention_kda.py:32-115) on bf16 projection weights."""
+
+    KEYS = ("q_proj.weight", "k_proj.weight", "v_proj.weight", "g_proj.weight",
+            "o_proj.weight", "q_conv1d.weight", "k_conv1d.weight", "v_conv1d.weight",
+            "f_a_proj.weight", "f_b_proj.weight", "b_proj.weight", "o_norm.weight",
+            "A_log", "dt_bias")
+
+    def __init__(self, cfg, w: dict):
+        self.cfg = cfg
+        H, D, K = cfg.kda_num_heads, cfg.kda_head_dim, cfg.kda_conv_size
+        self.H, self.D, self.K = H, D, K
+        bf = lambda n: T.contiguous_aligned(w[n].to(torch.bfloat16))  # noqa: E731
+        f32 = lambda n: T.contiguous_aligned(w[n].to(torch.float32))  # noqa: E731
+        self.q_w, self.k_w, self.v_w = bf("q_proj.weight"), bf("k_proj.weight"), bf("v_proj.weight")
+        self.g_w, self.o_w = bf("g_proj.weight"), bf("o_proj.weight")
+        self.fa, self.fb, self.b_w = bf("f_a_proj.weight"), bf("f_b_proj.weight"), bf("b_proj.weight")
+        self.qc, self.kc, self.vc = (f32(n).reshape(H * D, K) for n in ("q_conv1d.weight", "k_conv1d.weight",
+                                                                         "v_conv1d.weight"))
+        self.o_norm_w, self.dt_bias = f32("o_norm.weight"), f32("dt_bias").reshape(-1)
+        A = f32("A_log").reshape(-1)
+        if A.shape[0] != D or (A.shape[0] > H and float(A[H:].abs().max()) != 0.0):
+            raise ValueError("A_log must be [head_dim] with zeros past num_heads (attention_kda.py:50-54)")
+        self.A_log = A
+
+    def decode_step(self, x1, state, conv_in, conv_out, out) -> None:
+        """One token of one sequence: x1 [hidden], state [H, D, D] fp32 (in place),
+        conv_in / conv_out [3, k-1, H*D] fp32, out [hidden] fp32."""
+        c = self.cfg
+        nbytes = int(_lib.lib().k3_kda_step_workspace_size(self.H))
+        ws = _workspace.get(x1.device, nbytes, "kda_step")
+        _lib.call("k3_kda_step_decode", T.ptr(x1), T.dtype_code(x1.dtype), T.ptr(self.q_w), T.ptr(self.k_w),
+                  T.ptr(self.v_w), T.ptr(self.g_w), T.ptr(self.o_w), T.ptr(self.fa), T.ptr(self.fb), T.ptr(self.b_w),
+                  T.ptr(self.qc), T.ptr(self.kc), T.ptr(self.vc), T.ptr(conv_in), T.ptr(conv_out),
+                  T.ptr(self.o_norm_w), T.ptr(self.A_log), T.ptr(self.dt_bias), T.ptr(state), T.ptr(out),
+                  _lib.K3_F32, x1.shape[-1], self.H, self.D, self.K, float(c.kda_gate_lower_bound),
+                  float(c.rms_norm_eps), T.ptr(ws), ws.numel(), T.stream(x1))
+
+    def __call__(self, x: torch.Tensor, state: torch.Tensor | None = None, conv: tuple | None = None):
+        T.require_device(x, state)
+        B, Tn, hid = x.shape
+        H, D, K = self.H, self.D, self.K
+        P = H * D
+        if state is None:
+            state = torch.zeros((B, H, D, D), dtype=torch.float32, device=x.device)
+        elif tuple(state.shape) != (B, H, D, D):
+            raise ValueError(f"state must be [{B}, {H}, {D}, {D}]; got {tuple(state.shape)}")
+        elif not (state.dtype == torch.float32 and state.is_contiguous() and state.data_ptr() % 16 == 0):
+            state = state.to(torch.float32).contiguous().clone()
+        bufs = [torch.zeros((B, 3, K - 1, P), dtype=torch.float32, device=x.device) for _ in range(2)]
+        if conv is not None:
+            for m in range(3):
+                bufs[0][:, m] = conv[m].to(torch.float32).reshape(B, K - 1, P)
+        xin = x if x.dtype in (torch.float32, torch.bfloat16) else x.to(torch.float32)
+        xin = xin.contiguous()
+        out = torch.empty((B, Tn, hid), dtype=torch.float32, device=x.device)
+        for t in range(Tn):
+            cin, cout = bufs[t % 2], bufs[(t + 1) % 2]
+            for b in range(B):
+                x1 = T.contiguous_aligned(xin[b, t])
+                self.decode_step(x1, state[b], cin[b], cout[b], out[b, t])
+        fin = bufs[Tn % 2]
+        return out, state, (fin[:, 0], fin[:, 1], fin[:, 2])

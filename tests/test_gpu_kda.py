@@ -72,3 +72,54 @@ def test_kda_is_deterministic_and_validates():
         kda_recurrent(*_dev(q[..., :64], k[..., :64], v, g[..., :64], beta))     # key_dim != 128
     with pytest.raises(ValueError):
         kda_recurrent(*_dev(q, k, v[..., :48], g, beta))                        # V not a multiple of 32
+
+
+class KdaCfg:
+    def __init__(self, hidden, heads):
+        self.hidden_size, self.kda_num_heads, self.kda_head_dim, self.kda_conv_size = hidden, heads, 128, 4
+        self.kda_gate_lower_bound, self.rms_norm_eps = -5.0, 1e-5
+
+
+def _layer(seed, hidden, heads, scale=0.02):
+    from k3hip.kda import KDAAttention
+    cfg = KdaCfg(hidden, heads)
+    rng = np.random.default_rng(seed)
+    w = okda.random_kda_weights(rng, cfg, scale)
+    for n in ("q_proj", "k_proj", "v_proj", "g_proj", "o_proj", "f_a_proj", "f_b_proj", "b_proj"):
+        w[n + ".weight"] = om.bf16_round(w[n + ".weight"])                 # bf16 checkpoint weights
+    wd = {n: torch.from_numpy(a).to(DEV) for n, a in w.items()}
+    return cfg, w, KDAAttention(cfg, wd), rng
+
+
+def test_kda_layer_steps_match_oracle_and_carry_state():
+    """Five tokens from a zero state through k3_kda_step_decode against the fp64 layer; then
+    the same tokens as 3 + 2 with the recurrent and convolution states carried (the
+    reference's prefill == incremental gate, tests/test_k3ref_layers.py:150-168)."""
+    cfg, w, attn, rng = _layer(21, 512, 4, scale=0.05)
+    x = om.bf16_round(rng.standard_normal((1, 5, 512)).astype(np.float32))
+    xd = torch.from_numpy(x).to(DEV).to(torch.bfloat16)
+    out, S, conv = attn(xd)
+    want, S_want, conv_want = okda.kda_layer(cfg, w, x)
+    r_out = om.normwise_rel(out.cpu().numpy(), want)
+    r_S = om.normwise_rel(S.cpu().numpy(), S_want)
+    r_c = max(om.normwise_rel(a.cpu().numpy(), b) for a, b in zip(conv, conv_want))
+    print(f"kda layer 5 tokens: out {r_out:.2e} state {r_S:.2e} conv {r_c:.2e}")
+    assert r_out <= 2e-5 and r_S <= 2e-5 and r_c <= 1e-6
+    o1, S1, c1 = attn(xd[:, :3])
+    o2, S2, c2 = attn(xd[:, 3:], state=S1, conv=c1)
+    assert om.normwise_rel(torch.cat([o1, o2], 1).cpu().numpy(), out.cpu().numpy()) <= 1e-6
+    assert om.normwise_rel(S2.cpu().numpy(), S.cpu().numpy()) <= 1e-6
+
+
+def test_kda_layer_k3_shapes_one_token():
+    """K3's KDA layer shapes (hidden 7168, 96 heads of 128) for one token on a random state."""
+    cfg, w, attn, rng = _layer(22, 7168, 96)
+    x = om.bf16_round(rng.standard_normal((1, 1, 7168)).astype(np.float32))
+    S0 = (rng.standard_normal((1, 96, 128, 128)) * 0.1).astype(np.float32)
+    cv0 = tuple((rng.standard_normal((1, 3, 96 * 128)) * 0.5).astype(np.float32) for _ in range(3))
+    out, S, conv = attn(torch.from_numpy(x).to(DEV).to(torch.bfloat16), state=torch.from_numpy(S0).to(DEV),
+                        conv=tuple(torch.from_numpy(c).to(DEV) for c in cv0))
+    want, S_want, _ = okda.kda_layer(cfg, w, x, S0, cv0)
+    r_out, r_S = om.normwise_rel(out.cpu().numpy(), want), om.normwise_rel(S.cpu().numpy(), S_want)
+    print(f"kda layer K3 shapes: out {r_out:.2e} state {r_S:.2e}")
+    assert r_out <= 2e-5 and r_S <= 2e-5

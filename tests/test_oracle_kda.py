@@ -89,3 +89,53 @@ def test_steps_compose():
                                     None, St)
         assert np.allclose(oi[:, 0], o[:, i], rtol=1e-13, atol=1e-14)
     assert np.allclose(St, S, rtol=1e-13, atol=1e-14)
+
+
+class _Cfg:
+    hidden_size, kda_num_heads, kda_head_dim, kda_conv_size = 48, 2, 8, 4
+    kda_gate_lower_bound, rms_norm_eps = -5.0, 1e-5
+
+
+def test_short_conv_matches_numpy_correlate():
+    rng = np.random.default_rng(4)
+    x = rng.standard_normal((1, 7, 5))
+    w = rng.standard_normal((5, 1, 4))
+    st = rng.standard_normal((1, 3, 5))
+    y, new = okda.short_conv(x, w, 4, st)
+    xp = np.concatenate([st, x], axis=1)
+    for c in range(5):
+        pre = np.correlate(xp[0, :, c], w[c, 0], mode="valid")        # library routine
+        assert np.allclose(y[0, :, c], pre / (1 + np.exp(-pre)), rtol=1e-14)
+    assert np.array_equal(new[0], xp[0, -3:])
+
+
+def test_gated_rmsnorm_and_l2norm_closed_forms():
+    rng = np.random.default_rng(5)
+    x = rng.standard_normal((3, 16))
+    w = rng.standard_normal(16)
+    y = okda.gated_rmsnorm(x, w, np.zeros_like(x), 0.0)           # sigmoid(0) = 1/2
+    assert np.allclose(y, 0.5 * w * x / np.sqrt((x * x).mean(-1, keepdims=True)), rtol=1e-14)
+    n = okda.l2norm(x, eps=0.0)
+    assert np.allclose((n * n).sum(-1), 1.0, rtol=1e-14)
+
+
+def test_layer_prefill_equals_incremental_and_gate_range():
+    """The reference's KDA state gate (tests/test_k3ref_layers.py:150-168): one call over
+    T tokens equals T single-token calls carrying the recurrent and convolution states."""
+    cfg = _Cfg()
+    rng = np.random.default_rng(6)
+    w = okda.random_kda_weights(rng, cfg, scale=0.2)
+    x = rng.standard_normal((1, 6, cfg.hidden_size))
+    full, S_full, conv_full = okda.kda_layer(cfg, w, x)
+    st, cv, outs = None, None, []
+    for t in range(6):
+        o, st, cv = okda.kda_layer(cfg, w, x[:, t:t + 1], st, cv)
+        outs.append(o)
+    assert np.allclose(np.concatenate(outs, axis=1), full, rtol=1e-12, atol=1e-13)
+    assert np.allclose(st, S_full, rtol=1e-12, atol=1e-13)
+    assert all(np.allclose(a, b) for a, b in zip(cv, conv_full))
+    # the decay gate stays in (lower_bound, 0)
+    f = {n: np.asarray(a, np.float64) for n, a in w.items()}
+    g_raw = (x @ f["f_a_proj.weight"].T) @ f["f_b_proj.weight"].T
+    g = -5.0 / (1 + np.exp(-(np.repeat(np.exp(f["A_log"][:2]), 8) * (g_raw + f["dt_bias"]))))
+    assert np.all((g > -5.0) & (g < 0.0))
