@@ -445,6 +445,49 @@ def bench_kda(torch, steps, warmup, dev):
     return sec, stats
 
 
+KS_HID, KS_P = 7168, KDA_H * KDA_D
+KS_BYTES = (2 * (5 * KS_P * KS_HID + KDA_D * KS_HID + KS_P * KDA_D + KDA_H * KS_HID)
+            + 2 * KDA_H * KDA_D * KDA_D * 4 + 2 * 3 * 3 * KS_P * 4)      # 900,628,480
+
+
+def bench_kda_step(torch, steps, warmup, dev):
+    """One token through a whole KDA layer at K3 shapes (k3_kda_step_decode): hidden 7168,
+    96 heads of 128, short convolutions of 4, bf16 projections (887 MB, beyond the MALL),
+    fp32 state updated in place, a fresh x per step."""
+    from types import SimpleNamespace
+    from k3hip.kda import KDAAttention
+    cfg = SimpleNamespace(hidden_size=KS_HID, kda_num_heads=KDA_H, kda_head_dim=KDA_D, kda_conv_size=4,
+                          kda_gate_lower_bound=-5.0, rms_norm_eps=1e-5)
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(1010)
+
+    def W(*shape, s=0.02):
+        return torch.randn(*shape, device=dev, generator=gen) * s
+
+    a = torch.zeros(KDA_D, device=dev)
+    a[:KDA_H] = torch.log(1 + 15 * torch.rand(KDA_H, device=dev, generator=gen))
+    w = {"q_proj.weight": W(KS_P, KS_HID), "k_proj.weight": W(KS_P, KS_HID), "v_proj.weight": W(KS_P, KS_HID),
+         "g_proj.weight": W(KS_P, KS_HID), "o_proj.weight": W(KS_HID, KS_P),
+         "q_conv1d.weight": W(KS_P, 1, 4, s=0.3), "k_conv1d.weight": W(KS_P, 1, 4, s=0.3),
+         "v_conv1d.weight": W(KS_P, 1, 4, s=0.3), "f_a_proj.weight": W(KDA_D, KS_HID),
+         "f_b_proj.weight": W(KS_P, KDA_D), "b_proj.weight": W(KDA_H, KS_HID), "o_norm.weight": 1 + W(KDA_D, s=0.1),
+         "A_log": a, "dt_bias": W(KS_P, s=1.0)}
+    attn = KDAAttention(cfg, w)
+    del w
+    state = torch.randn(KDA_H, KDA_D, KDA_D, device=dev, generator=gen) * 0.1
+    conv = [torch.zeros(3, 3, KS_P, device=dev) for _ in range(2)]
+    xs = torch.randn(16, KS_HID, device=dev, generator=gen).to(torch.bfloat16)
+    out = torch.empty(KS_HID, device=dev)
+
+    def step(i):
+        attn.decode_step(xs[i % 16], state, conv[i % 2], conv[(i + 1) % 2], out)
+
+    sec, _ = graph_time(torch, step, steps, warmup)
+    stats = None if EAGER else step_stats(torch, step, 32)
+    del attn
+    return sec, stats
+
+
 def bench_read_ceiling(torch, nbytes, steps, dev):
     """One streaming-read launch of nbytes (the library's calibration kernel), rotating
     over >= 1.5 GB of buffers: the bandwidth a single launch of this size can reach."""
@@ -512,7 +555,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=64)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
-    ap.add_argument("--workloads", default="expert,layer,k3layer,ingest,prefill,gemv,mla,mlastep,kda,ceiling")
+    ap.add_argument("--workloads", default="expert,layer,k3layer,ingest,prefill,gemv,mla,mlastep,kda,kdastep,ceiling")
     ap.add_argument("--eager", action="store_true",
                     help="launch steps one by one instead of replaying a HIP graph (profiler counter runs)")
     args = ap.parse_args()
@@ -620,6 +663,14 @@ def main():
         line["kda_decode"] = {"us": round(kus, 3), "GB/s": round(kgb, 1), "pct_hbm_peak": round(100 * kgb / HBM_PEAK_GBS, 1),
                               "bytes": KDA_BYTES, "heads": KDA_H, "key_dim": KDA_D, "value_dim": KDA_D,
                               "state": "fp32, in place", "launches": 1, "step_us": kdstats}
+    if "kdastep" in work:
+        kss = min(K, 128)
+        ksec, kstats2 = bench_kda_step(torch, kss, min(W, 16), dev)
+        kus2 = ksec / kss * 1e6
+        kgb2 = KS_BYTES / (kus2 * 1e-6) / 1e9
+        line["kda_step"] = {"us": round(kus2, 2), "GB/s": round(kgb2, 1), "pct_hbm_peak": round(100 * kgb2 / HBM_PEAK_GBS, 1),
+                            "bytes": KS_BYTES, "hidden": KS_HID, "heads": KDA_H, "head_dim": KDA_D, "conv": 4,
+                            "weights": "bf16", "launches": 4, "step_us": kstats2}
     if "ceiling" in work:
         ce = bench_read_ceiling(torch, EXPERT_BYTES, 256, dev)
         cl = bench_read_ceiling(torch, LAYER_BYTES, 64, dev)

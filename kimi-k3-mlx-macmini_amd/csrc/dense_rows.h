@@ -4,7 +4,8 @@
 //   kModeX         x itself (bf16 or fp32)
 //   kModeNorm      rmsnorm(src) * nw over all K values (every block normalises it)
 //   kModeGate      a fp32 vector as is (gl null) or times sigmoid(gl)
-//   kModeHeadNorm  per head of hd values: rmsnorm over the head * nw[i] * sigmoid(gl)
+//   kModeHeadNorm  per head of 128 values: o * nw[i] / rms(head), the head's sum of squares
+//                  given as four partial sums in gl (o already carries its gate)
 // Every block issues its weight rows first, then stages the vector, then reduces: a lane
 // takes 16-byte chunks (8 bf16) l, l + 64, ... of a row; R rows per wave, 4 waves.
 #pragma once
@@ -31,7 +32,6 @@ struct RowsArgs {
     float *y[kRowSets];            // fp32 outputs [N] (when out is null)
     void *out;                     // not null: set 0's outputs go here, fp32 or bf16
     int out_bf16;
-    int hd;                        // kModeHeadNorm: values per head
     // kModeNorm, last block: the cache append
     const float *ckv, *kvw;   // ckv [r + rope] fp32, kv_a_layernorm [r]
     uint16_t *lat_row, *rot_row;
@@ -82,15 +82,14 @@ __device__ __forceinline__ void stage_vector(const RowsArgs &a, float *vs, float
             reinterpret_cast<float4 *>(vs)[c] = v;
         }
     } else if (MODE == kModeHeadNorm) {
-        const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-        for (int hh = wave; hh < K / a.hd; hh += 4) {
-            float ss = 0.f;
-            for (int i = lane; i < a.hd; i += 64) ss = fmaf(a.o[hh * a.hd + i], a.o[hh * a.hd + i], ss);
-            const float rs = 1.0f / sqrtf(wave_sum_all(ss) / static_cast<float>(a.hd) + a.eps);
-            for (int i = lane; i < a.hd; i += 64) {
-                const int c = hh * a.hd + i;
-                vs[c] = a.o[c] * rs * a.nw[i] / (1.0f + expf(-a.gl[c]));
-            }
+        // heads of 128 values = 32 float4; gl holds four partial sums of squares per head
+        for (int c = threadIdx.x; c < K / 4; c += 256) {
+            const float4 p = reinterpret_cast<const float4 *>(a.gl)[c >> 5];
+            const float rs = 1.0f / sqrtf((((p.x + p.y) + p.z) + p.w) / 128.0f + a.eps);
+            const float4 w = reinterpret_cast<const float4 *>(a.nw)[c & 31];
+            float4 v = reinterpret_cast<const float4 *>(a.o)[c];
+            v.x = v.x * rs * w.x, v.y = v.y * rs * w.y, v.z = v.z * rs * w.z, v.w = v.w * rs * w.w;
+            reinterpret_cast<float4 *>(vs)[c] = v;
         }
     } else {
         for (int c = threadIdx.x; c < K / 4; c += 256) {

@@ -49,9 +49,10 @@ __device__ __forceinline__ float sum_row_groups(float x) {
 // The update of one block's 32 columns of head h's state, given this thread's four rows'
 // key values kk, scaled query values qq and decay factors dk, its four columns' values vv
 // and the head's beta.  x holds the thread's state values (loaded by the caller).
-__device__ __forceinline__ void kda_apply(float4 (&x)[4], float *const (&Sp)[4], const float (&kk)[4],
-                                          const float (&qq)[4], const float (&dk)[4], const float (&vv)[4], float b,
-                                          float (*red)[4][kKdaVS], void *out, int out_bf16, int64_t out_base) {
+// Returns the read-out of column t (valid in threads t < 32).
+__device__ __forceinline__ float kda_apply(float4 (&x)[4], float *const (&Sp)[4], const float (&kk)[4],
+                                           const float (&qq)[4], const float (&dk)[4], const float (&vv)[4], float b,
+                                           float (*red)[4][kKdaVS]) {
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6, cg = t & 7;
     // decay, then k . S' over the 128 channels
 #pragma unroll
@@ -103,13 +104,7 @@ __device__ __forceinline__ void kda_apply(float4 (&x)[4], float *const (&Sp)[4],
         for (int c = 0; c < 4; ++c) red[1][wave][4 * lane + c] = p[c];
     }
     __syncthreads();
-    if (t < kKdaVS) {
-        const float o = ((red[1][0][t] + red[1][1][t]) + red[1][2][t]) + red[1][3][t];
-        if (out_bf16)
-            static_cast<uint16_t *>(out)[out_base + t] = f32_to_bf16(o);
-        else
-            static_cast<float *>(out)[out_base + t] = o;
-    }
+    return t < kKdaVS ? ((red[1][0][t] + red[1][1][t]) + red[1][2][t]) + red[1][3][t] : 0.f;
 }
 
 // the four state rows t/8 + 32j of columns c0 .. c0+3 of head h
@@ -142,8 +137,14 @@ __global__ __launch_bounds__(256) void kda_decode_kernel(KdaArgs a) {
     }
 #pragma unroll
     for (int c = 0; c < 4; ++c) vv[c] = ldx(a.v, static_cast<int64_t>(h) * a.V + c0 + c, bf);
-    kda_apply(x, Sp, kk, qq, dk, vv, ldx(a.beta, h, bf), red, a.out, a.out_bf16,
-              static_cast<int64_t>(h) * a.V + vb * kKdaVS);
+    const float o = kda_apply(x, Sp, kk, qq, dk, vv, ldx(a.beta, h, bf), red);
+    if (t < kKdaVS) {
+        const int64_t oi = static_cast<int64_t>(h) * a.V + vb * kKdaVS + t;
+        if (a.out_bf16)
+            static_cast<uint16_t *>(a.out)[oi] = f32_to_bf16(o);
+        else
+            static_cast<float *>(a.out)[oi] = o;
+    }
 }
 
 // ------------------------------------------------------------------ whole KDA layer step
@@ -163,7 +164,9 @@ struct KdaStepArgs {
     const float *A_log, *dt_bias;            // [>= H], [P]
     float lower, scale;
     float *S;                                // [H, 128, 128] fp32, in place
-    float *o;                                // [P] fp32
+    const float *og;                         // [P] g_proj x (the output gate logits)
+    float *o;                                // [P] fp32: o * sigmoid(og)
+    float *hss;                              // [H, 4] sum of o^2 over each block's 32 columns
     int H, kc;
 };
 
@@ -233,7 +236,19 @@ __global__ __launch_bounds__(256) void kda_step_kernel(KdaStepArgs a) {
     }
 #pragma unroll
     for (int c = 0; c < 4; ++c) vv[c] = vsh[4 * cg + c];
-    kda_apply(x, Sp, kk, qq, dk, vv, b, red, a.o, 0, static_cast<int64_t>(h) * V + vb * kKdaVS);
+    const float o = kda_apply(x, Sp, kk, qq, dk, vv, b, red);
+    // the block's share of the head's sum of squares (for the gated RMSNorm), and o gated
+    if (t < kKdaVS) {
+        float ss = o * o;
+        ss += __shfl_xor(ss, 1);
+        ss += __shfl_xor(ss, 2);
+        ss += __shfl_xor(ss, 4);
+        ss += __shfl_xor(ss, 8);
+        ss += __shfl_xor(ss, 16);
+        if (t == 0) a.hss[h * nvb + vb] = ss;
+        const int64_t c = static_cast<int64_t>(h) * V + vb * kKdaVS + t;
+        a.o[c] = o / (1.0f + expf(-a.og[c]));
+    }
 }
 
 }  // namespace
@@ -275,7 +290,7 @@ extern "C" int k3_kda_recurrent_decode(const void *q, const void *k, const void 
 
 namespace {
 struct KdaStepWs {
-    size_t q, k, v, og, fa, b, fb, o, total;
+    size_t q, k, v, og, fa, b, fb, o, hss, total;
 };
 KdaStepWs kda_step_ws(int64_t H) {
     const size_t P = static_cast<size_t>(H) * kKdaK;
@@ -284,6 +299,7 @@ KdaStepWs kda_step_ws(int64_t H) {
     auto take = [&](size_t n) { const size_t at = off; off += (n * 4 + 255) & ~size_t(255); return at; };
     L.q = take(P), L.k = take(P), L.v = take(P), L.og = take(P), L.fa = take(kKdaK), L.b = take(H), L.fb = take(P);
     L.o = take(P);
+    L.hss = take(static_cast<size_t>(H) * (kKdaK / kKdaVS));
     L.total = off;
     return L;
 }
@@ -325,6 +341,7 @@ extern "C" int k3_kda_step_decode(const void *x, int x_dtype, const void *q_proj
     float *wv = reinterpret_cast<float *>(ws + L.v), *wog = reinterpret_cast<float *>(ws + L.og);
     float *wfa = reinterpret_cast<float *>(ws + L.fa), *wb = reinterpret_cast<float *>(ws + L.b);
     float *wfb = reinterpret_cast<float *>(ws + L.fb), *wo = reinterpret_cast<float *>(ws + L.o);
+    float *whss = reinterpret_cast<float *>(ws + L.hss);
     auto st = static_cast<hipStream_t>(stream);
     // K1: rows of q, k, v, g, f_a and b against x
     RowsArgs a1{};
@@ -347,13 +364,13 @@ extern "C" int k3_kda_step_decode(const void *x, int x_dtype, const void *q_proj
     k.q_raw = wq, k.k_raw = wk, k.v_raw = wv, k.fb = wfb, k.b_raw = wb;
     k.q_conv = q_conv, k.k_conv = k_conv, k.v_conv = v_conv, k.conv_in = conv_in, k.conv_out = conv_out;
     k.A_log = A_log, k.dt_bias = dt_bias, k.lower = gate_lower_bound, k.scale = 1.0f / sqrtf(static_cast<float>(kKdaK));
-    k.S = state, k.o = wo, k.H = static_cast<int>(heads), k.kc = static_cast<int>(conv_size);
+    k.S = state, k.og = wog, k.o = wo, k.hss = whss, k.H = static_cast<int>(heads), k.kc = static_cast<int>(conv_size);
     kda_step_kernel<<<dim3(static_cast<unsigned>(heads * (kKdaK / kKdaVS))), 256, 0, st>>>(k);
     rc = check_hip(hipGetLastError(), "kda step: recurrence launch");
     if (rc) return rc;
-    // K4: rows of o_proj against the gated RMS-normalised heads
+    // K4: rows of o_proj against the gated heads scaled by their RMS norms
     RowsArgs a4{};
-    a4.o = wo, a4.gl = wog, a4.nw = o_norm, a4.hd = kKdaK, a4.eps = eps, a4.K = static_cast<int>(P);
+    a4.o = wo, a4.gl = whss, a4.nw = o_norm, a4.eps = eps, a4.K = static_cast<int>(P);
     a4.w[0] = static_cast<const uint16_t *>(o_proj), a4.N[0] = static_cast<int>(hidden);
     a4.out = out, a4.out_bf16 = out_dtype == K3_BF16;
     return launch_rows<kModeHeadNorm>(a4, st);
