@@ -1,4 +1,4 @@
-"""CPU oracle for the MXFP4 expert / latent-MLA hot path.
+"""CPU oracle for the MXFP4 expert / latent-MLA / KDA decode path.
 
 TEST INFRASTRUCTURE ONLY.  Nothing in the product path (the ``k3hip`` package and
 ``libk3hip.so``) imports, links or calls this package.  Its only legitimate users are
@@ -16,6 +16,9 @@ Modules
                  (``k3ref/layers.py:241-261`` without the K3 latent wrapper).
 ``mla``          absorbed latent-MLA decode core (``attention_mla.py:193-212``) and the
                  expanded form it must equal (``k3ref/layers.py:152-185``), both fp64.
+``kda``          Kimi Delta Attention: the recurrence (``attention_kda.py:65-90``), the short
+                 convolution, L2 and gated RMS norms (``ops.py:31-60``) and the whole layer
+                 (``attention_kda.py:94-115``), fp64.
 ``cpu_baseline`` torch-CPU fp32 restatement of the k3ref path, timed by ``bench.py``.
 ``native``       ctypes loader for ``mxfp4_ref.c``: an independent C restatement of the
                  decode and of the reference Metal kernel's sequential fp32 FMA order
