@@ -7,7 +7,8 @@
 //   kModeHeadNorm  per head of 128 values: o * nw[i] / rms(head), the head's sum of squares
 //                  given as four partial sums in gl (o already carries its gate)
 // Every block issues its weight rows first, then stages the vector, then reduces: a lane
-// takes 16-byte chunks (8 bf16) l, l + 64, ... of a row; R rows per wave, 4 waves.
+// takes 16-byte chunks (8 bf16) l, l + 64, ... of a row; R rows per wave, 4 waves (8 for
+// rows of 4097..8192 values, so one staged vector serves more rows).
 #pragma once
 
 #include "k3_common.h"
@@ -38,23 +39,27 @@ struct RowsArgs {
     int r, rope, append;
 };
 
+template <int NW>
 __device__ __forceinline__ float block_sum(float v, float *red) {
     v = wave_sum_all(v);
     if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
     __syncthreads();
-    const float t = red[0] + red[1] + red[2] + red[3];
+    float t = 0.f;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) t += red[w];
     __syncthreads();
     return t;
 }
 
 // v (fp32, K values) into LDS; ends with a block barrier
-template <int MODE>
+template <int MODE, int NW>
 __device__ __forceinline__ void stage_vector(const RowsArgs &a, float *vs, float *red) {
+    constexpr int NT = 64 * NW;
     const int K = a.K;
     if (MODE == kModeX) {
         if (a.x_bf16) {
             const uint4 *x8 = static_cast<const uint4 *>(a.x);
-            for (int c = threadIdx.x; c < K / 8; c += 256) {
+            for (int c = threadIdx.x; c < K / 8; c += NT) {
                 const uint4 q = x8[c];
                 const uint32_t d[4] = {q.x, q.y, q.z, q.w};
 #pragma unroll
@@ -65,17 +70,17 @@ __device__ __forceinline__ void stage_vector(const RowsArgs &a, float *vs, float
             }
         } else {
             const float4 *x4 = static_cast<const float4 *>(a.x);
-            for (int c = threadIdx.x; c < K / 4; c += 256) reinterpret_cast<float4 *>(vs)[c] = x4[c];
+            for (int c = threadIdx.x; c < K / 4; c += NT) reinterpret_cast<float4 *>(vs)[c] = x4[c];
         }
     } else if (MODE == kModeNorm) {
         float ss = 0.f;
-        for (int c = threadIdx.x; c < K / 4; c += 256) {
+        for (int c = threadIdx.x; c < K / 4; c += NT) {
             const float4 s = reinterpret_cast<const float4 *>(a.src)[c];
             ss = fmaf(s.x, s.x, fmaf(s.y, s.y, fmaf(s.z, s.z, fmaf(s.w, s.w, ss))));
             reinterpret_cast<float4 *>(vs)[c] = s;
         }
-        const float rs = 1.0f / sqrtf(block_sum(ss, red) / static_cast<float>(K) + a.eps);
-        for (int c = threadIdx.x; c < K / 4; c += 256) {
+        const float rs = 1.0f / sqrtf(block_sum<NW>(ss, red) / static_cast<float>(K) + a.eps);
+        for (int c = threadIdx.x; c < K / 4; c += NT) {
             const float4 g = reinterpret_cast<const float4 *>(a.nw)[c];
             float4 v = reinterpret_cast<float4 *>(vs)[c];
             v.x = v.x * rs * g.x, v.y = v.y * rs * g.y, v.z = v.z * rs * g.z, v.w = v.w * rs * g.w;
@@ -83,7 +88,7 @@ __device__ __forceinline__ void stage_vector(const RowsArgs &a, float *vs, float
         }
     } else if (MODE == kModeHeadNorm) {
         // heads of 128 values = 32 float4; gl holds four partial sums of squares per head
-        for (int c = threadIdx.x; c < K / 4; c += 256) {
+        for (int c = threadIdx.x; c < K / 4; c += NT) {
             const float4 p = reinterpret_cast<const float4 *>(a.gl)[c >> 5];
             const float rs = 1.0f / sqrtf((((p.x + p.y) + p.z) + p.w) / 128.0f + a.eps);
             const float4 w = reinterpret_cast<const float4 *>(a.nw)[c & 31];
@@ -92,7 +97,7 @@ __device__ __forceinline__ void stage_vector(const RowsArgs &a, float *vs, float
             reinterpret_cast<float4 *>(vs)[c] = v;
         }
     } else {
-        for (int c = threadIdx.x; c < K / 4; c += 256) {
+        for (int c = threadIdx.x; c < K / 4; c += NT) {
             float4 v = reinterpret_cast<const float4 *>(a.o)[c];
             if (a.gl) {
                 const float4 g = reinterpret_cast<const float4 *>(a.gl)[c];
@@ -106,12 +111,14 @@ __device__ __forceinline__ void stage_vector(const RowsArgs &a, float *vs, float
 }
 
 // c_new = rmsnorm(ckv[:r]) * kv_a_layernorm -> lat_row (bf16); rot_row = bf16(ckv[r:])
+template <int NW>
 __device__ void append_row(const RowsArgs &a, float *red) {
+    constexpr int NT = 64 * NW;
     float ss = 0.f;
-    for (int j = threadIdx.x; j < a.r; j += 256) ss = fmaf(a.ckv[j], a.ckv[j], ss);
-    const float rs = 1.0f / sqrtf(block_sum(ss, red) / static_cast<float>(a.r) + a.eps);
-    for (int j = threadIdx.x; j < a.r; j += 256) a.lat_row[j] = f32_to_bf16(a.ckv[j] * rs * a.kvw[j]);
-    for (int j = threadIdx.x; j < a.rope; j += 256) a.rot_row[j] = f32_to_bf16(a.ckv[a.r + j]);
+    for (int j = threadIdx.x; j < a.r; j += NT) ss = fmaf(a.ckv[j], a.ckv[j], ss);
+    const float rs = 1.0f / sqrtf(block_sum<NW>(ss, red) / static_cast<float>(a.r) + a.eps);
+    for (int j = threadIdx.x; j < a.r; j += NT) a.lat_row[j] = f32_to_bf16(a.ckv[j] * rs * a.kvw[j]);
+    for (int j = threadIdx.x; j < a.rope; j += NT) a.rot_row[j] = f32_to_bf16(a.ckv[a.r + j]);
 }
 
 // 8 bf16 weights . 8 fp32 values
@@ -127,21 +134,21 @@ __device__ __forceinline__ float dot8_bf16_f32(uint4 w, float4 v0, float4 v1, fl
     return acc;
 }
 
-// Block: 4 waves x R rows of one row set; CH 16-byte chunks per lane per row.
-template <int MODE, int CH, int R>
-__global__ __launch_bounds__(256) void step_rows_kernel(RowsArgs a) {
+// Block: NW waves x R rows of one row set; CH 16-byte chunks per lane per row.
+template <int MODE, int CH, int R, int NW>
+__global__ __launch_bounds__(64 * NW) void step_rows_kernel(RowsArgs a) {
     extern __shared__ float vs[];
-    __shared__ float red[4];
+    __shared__ float red[NW];
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
     if (MODE == kModeNorm && a.append && static_cast<int>(blockIdx.x) == static_cast<int>(gridDim.x) - 1) {
-        append_row(a, red);
+        append_row<NW>(a, red);
         return;
     }
     int b = blockIdx.x, s = 0;
     while (s < kRowSets - 1 && b >= a.blocks[s]) b -= a.blocks[s++];
     const int N = a.N[s], K = a.K, nch = K >> 3;
     const uint32_t rowb = static_cast<uint32_t>(K) * 2u;
-    const int n0 = (b * 4 + wave) * R;
+    const int n0 = (b * NW + wave) * R;
     const auto rw = make_rsrc(a.w[s], static_cast<uint32_t>(N) * rowb);
     // 1. the wave's rows
     uint4 wr[R][CH];
@@ -153,7 +160,7 @@ __global__ __launch_bounds__(256) void step_rows_kernel(RowsArgs a) {
             wr[r][u] = buf_load16(rw, (n < N && c < nch) ? static_cast<uint32_t>(n) * rowb + c * 16u : kOobOffset);
         }
     // 2. the input vector
-    stage_vector<MODE>(a, vs, red);
+    stage_vector<MODE, NW>(a, vs, red);
     // 3. row dots
     const float4 *v4 = reinterpret_cast<const float4 *>(vs);
 #pragma unroll
@@ -187,13 +194,16 @@ __global__ __launch_bounds__(256) void step_rows_kernel(RowsArgs a) {
 template <int MODE, int CH>
 int launch_rows_ch(RowsArgs &a, hipStream_t st) {
     constexpr int R = CH >= 16 ? 1 : (CH >= 8 ? 2 : (CH >= 4 ? 4 : 8));
+    // rows of 4097..8192 values: one staged vector serves 8 rows (measured faster); wider
+    // rows keep 4 waves, as their registers and LDS already limit the blocks per CU
+    constexpr int NW = CH == 16 ? 8 : 4;
     int total = 0;
     for (int s = 0; s < kRowSets; ++s) {
-        a.blocks[s] = a.w[s] ? static_cast<int>(cdiv(a.N[s], 4 * R)) : 0;
+        a.blocks[s] = a.w[s] ? static_cast<int>(cdiv(a.N[s], NW * R)) : 0;
         total += a.blocks[s];
     }
     if (MODE == kModeNorm && a.append) ++total;
-    step_rows_kernel<MODE, CH, R><<<dim3(static_cast<unsigned>(total)), 256, static_cast<size_t>(a.K) * 4, st>>>(a);
+    step_rows_kernel<MODE, CH, R, NW><<<dim3(static_cast<unsigned>(total)), 64 * NW, static_cast<size_t>(a.K) * 4, st>>>(a);
     return check_hip(hipGetLastError(), "dense rows launch");
 }
 
