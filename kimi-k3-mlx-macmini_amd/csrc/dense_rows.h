@@ -33,6 +33,7 @@ struct RowsArgs {
     float *y[kRowSets];            // fp32 outputs [N] (when out is null)
     void *out;                     // not null: set 0's outputs go here, fp32 or bf16
     int out_bf16;
+    const float *add;              // with out: added to each output row (null: nothing)
     // kModeNorm, last block: the cache append
     const float *ckv, *kvw;   // ckv [r + rope] fp32, kv_a_layernorm [r]
     uint16_t *lat_row, *rot_row;
@@ -180,10 +181,11 @@ __global__ __launch_bounds__(64 * NW) void step_rows_kernel(RowsArgs a) {
         const int n = n0 + r;
         if (lane == 63 && n < N) {
             if (a.out) {
+                const float t2 = a.add ? t + a.add[n] : t;
                 if (a.out_bf16)
-                    static_cast<uint16_t *>(a.out)[n] = f32_to_bf16(t);
+                    static_cast<uint16_t *>(a.out)[n] = f32_to_bf16(t2);
                 else
-                    static_cast<float *>(a.out)[n] = t;
+                    static_cast<float *>(a.out)[n] = t2;
             } else {
                 a.y[s][n] = t;
             }

@@ -26,6 +26,7 @@
 // in-order vmcnt waits never hold the staging behind the weight stream.
 #include <algorithm>
 
+#include "dense_rows.h"
 #include "moe_common.h"
 #include "mxfp4_dot.h"
 
@@ -79,7 +80,7 @@ constexpr int kMaxExperts = 1024;
 // Arrival counters at the head of the workspace: [0] for L1's router blocks, [1 + r] for the
 // blocks of L3's row range r
 constexpr size_t kCounterBytes = 4096;
-constexpr int kSharedDownRows = 2;  // shared down rows per wave (L2; L4)
+constexpr int kSharedDownRows = 2;  // shared down rows per wave (L2)
 // shared down rows per wave for CHI chunks per lane: one row past 8 chunks (wide shared
 // experts), so the fp32 activation and the rows stay in registers
 constexpr int shared_down_rows(int chi) { return chi > 8 ? 1 : kSharedDownRows; }
@@ -640,69 +641,6 @@ __global__ __launch_bounds__(256, 4) void layer_l3(LayerArgs a) {
 }
 
 
-// ------------------------------------------------------------------ L4 (latent layer)
-// out[n] = W_up[n] . (norm * ylat / sqrt(mean(ylat^2) + eps)) + yshared[n]   (moe.py:129-131;
-// KimiRMSNorm, ops.py:11-14).  Block: 4 waves x kSharedDownRows rows of W_up [H, Hr].  Every
-// wave holds the whole latent vector (lane l: chunks l, l + 64, ... of 8 values), so its
-// sum of squares is one wave reduction and no block barrier is needed.
-template <int CHU>
-__global__ __launch_bounds__(256) void layer_l4(LayerArgs a) {
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const int n0 = (blockIdx.x * 4 + wave) * kSharedDownRows;
-    const uint32_t row_bytes = static_cast<uint32_t>(a.Hr) * 2u;
-    const int nch = a.Hr >> 3;
-    // 1. the latent sum and the norm weight (L2-resident), then the up rows
-    const auto ry = make_rsrc(a.ws.ylat, static_cast<uint32_t>(a.Hr) * 4u);
-    const auto rn = make_rsrc(a.lat_norm, static_cast<uint32_t>(a.Hr) * 4u);
-    float4 yv[CHU][2], nv[CHU][2];
-#pragma unroll
-    for (int u = 0; u < CHU; ++u) {
-        const int c = u * 64 + lane;
-        const bool ok = c < nch;
-#pragma unroll
-        for (int q = 0; q < 2; ++q) {
-            yv[u][q] = __builtin_bit_cast(float4, buf_load16(ry, ok ? c * 32u + q * 16u : kOobOffset));
-            nv[u][q] = __builtin_bit_cast(float4, buf_load16(rn, ok ? c * 32u + q * 16u : kOobOffset));
-        }
-    }
-    const auto rr = make_rsrc(a.lat_up, static_cast<uint32_t>(a.H) * row_bytes);
-    uint4 w[kSharedDownRows][CHU];
-#pragma unroll
-    for (int r = 0; r < kSharedDownRows; ++r)
-#pragma unroll
-        for (int u = 0; u < CHU; ++u) {
-            const int c = u * 64 + lane, n = n0 + r;
-            w[r][u] = buf_load16(rr, (n < a.H && c < nch) ? static_cast<uint32_t>(n) * row_bytes + c * 16u : kOobOffset);
-        }
-    // 2. 1 / rms of the latent sum (every wave, the full vector); norm weight folded in
-    float ss = 0.f;
-#pragma unroll
-    for (int u = 0; u < CHU; ++u)
-#pragma unroll
-        for (int q = 0; q < 2; ++q) {
-            const float4 y = yv[u][q];
-            ss = fmaf(y.x, y.x, fmaf(y.y, y.y, fmaf(y.z, y.z, fmaf(y.w, y.w, ss))));
-            yv[u][q] = make_float4(y.x * nv[u][q].x, y.y * nv[u][q].y, y.z * nv[u][q].z, y.w * nv[u][q].w);
-        }
-    const float rs = 1.0f / sqrtf(wave_sum_all(ss) / static_cast<float>(a.Hr) + a.eps);
-    // 3. up rows . normalised latent, plus the shared experts' row
-#pragma unroll
-    for (int r = 0; r < kSharedDownRows; ++r) {
-        float acc = 0.f;
-#pragma unroll
-        for (int u = 0; u < CHU; ++u) acc = dot8(w[r][u], yv[u][0], yv[u][1], acc);
-        const float t = wave_sum_to_lane63(acc);
-        const int n = n0 + r;
-        if (lane == 63 && n < a.H) {
-            const float y = t * rs + (a.sh_down ? a.ws.yshared[n] : 0.f);
-            if (a.out_bf16)
-                static_cast<uint16_t *>(a.out)[n] = f32_to_bf16(y);
-            else
-                static_cast<float *>(a.out)[n] = y;
-        }
-    }
-}
-
 // ------------------------------------------------------------------ host side
 struct LayerWsLayout {
     size_t logits, scores, corrected, idx, w, shared_act, act, yshared, ptrs, counter, h, ylat, yrow, total;
@@ -750,20 +688,15 @@ static int launch_l1(LayerArgs &a, bool with_shared, hipStream_t st) {
     return set_error(K3_ERR_SHAPE, "moe layer: H=%d too wide", a.H);
 }
 
-// L4 of the latent layer (nothing to do for the plain layer)
+// L4 of the latent layer (nothing to do for the plain layer): the dense rows of W_up against
+// rmsnorm(ylat) * norm (every block normalises the latent sum itself), plus the shared row
 static int launch_l4(const LayerArgs &a, hipStream_t st) {
     if (!a.lat_down) return K3_OK;
-    const dim3 g4(static_cast<unsigned>(cdiv(a.H, 4 * kSharedDownRows)));
-    const int chu = static_cast<int>(cdiv(a.Hr / 8, 64));
-    if (chu <= 4)
-        layer_l4<4><<<g4, 256, 0, st>>>(a);
-    else if (chu <= 8)
-        layer_l4<8><<<g4, 256, 0, st>>>(a);
-    else if (chu <= 16)
-        layer_l4<16><<<g4, 256, 0, st>>>(a);
-    else
-        return set_error(K3_ERR_SHAPE, "moe latent layer: latent width %d too wide", a.Hr);
-    return check_hip(hipGetLastError(), "moe latent layer L4");
+    RowsArgs r{};
+    r.src = a.ws.ylat, r.nw = a.lat_norm, r.eps = a.eps, r.K = a.Hr;
+    r.w[0] = a.lat_up, r.N[0] = a.H;
+    r.out = a.out, r.out_bf16 = a.out_bf16, r.add = a.sh_down ? a.ws.yshared : nullptr;
+    return launch_rows<kModeNorm>(r, st);
 }
 
 template <typename XT>
