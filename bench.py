@@ -1,16 +1,25 @@
 """Benchmark: MXFP4 expert GEMV GB/s (% of HBM peak) and us per MoE layer at batch 1.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--workloads expert,layer,gemv]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--workloads expert,layer,...]
 
 One JSON line on stdout.  The headline workload is one SwiGLU expert at batch 1
 (hidden 7168, intermediate 2048, MXFP4 weights with E8M0 scales in [118, 130], bf16 x):
 a step is one expert FFN (a gate/up + activation launch, then the down GEMV) on a different
 resident expert (64 experts rotate, 1.5 GB, so the 256 MB MALL cannot serve the weights).
-`value` is algorithmic weight bytes per second over the K timed steps.  The same line
-carries the MoE-layer figure (384 resident experts, top-8 softmax routing, one bf16 shared
-expert, a fresh token per step), the grouped-prefill, single-projection GEMV and MLA decode
-figures, K3's latent routed layer at batch 1 (896 experts, top-16), the roofline of the expert step (its two launches) and a CPU baseline
-(torch-CPU restatement of the k3ref path timed on a bounded sample on this host).
+`value` is algorithmic weight bytes per second over the K timed steps; `roofline` is that
+step's (its two launches) and `cpu_baseline` a torch-CPU restatement of the k3ref path
+timed on a bounded sample on this host.  The same line carries, as sub-objects:
+  moe_layer          384 resident experts, top-8 softmax routing, a bf16 shared expert,
+                     a fresh token per step;
+  k3_latent_layer    K3's routed layer with its latent wrapper (896 experts, top-16);
+  checkpoint_ingest  host-to-HBM ingest of K3-shaped experts from safetensors shards;
+  moe_prefill        2048 tokens x top-8 on the grouped MXFP4-MFMA path, Zipf(1.1) load;
+  gemv               one [2048 x 7168] projection;
+  mla_decode         the absorbed MLA core, 64 heads over 32768 cached tokens;
+  mla_step           one token through a whole MLA layer at K3 shapes;
+  kda_decode         one KDA recurrent step (96 heads of 128 x 128 fp32 state);
+  kda_step           one token through a whole KDA layer at K3 shapes;
+  read_ceiling       single streaming-read / copy launches of the same byte counts.
 
 Synthetic, seeded data; weights are random-init with the benchmark shapes.  Steps are
 captured once into a HIP graph and replayed, so the timed region is GPU work plus the

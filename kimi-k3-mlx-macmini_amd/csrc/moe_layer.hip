@@ -21,6 +21,11 @@
 //       finish (an arrival counter per range) combines y = shared + sum_j w_j * down_j in
 //       slot order.
 //
+// K3's latent layer (k3_moe_latent_layer_decode) runs the same launches in a latent mode:
+// L1 also computes h = bf16(W_down x), L2 and L3 read and write the latent width, L3 writes
+// the routed sum ylat, and a fourth launch (the dense row kernel of dense_rows.h) takes the
+// rows of W_up against rmsnorm(ylat) * norm and adds the shared output.
+//
 // Every kernel issues its activation loads, then its whole weight stream, before it stages
 // anything into LDS or registers it consumes, and stages with unconditional stores, so the
 // in-order vmcnt waits never hold the staging behind the weight stream.
