@@ -123,3 +123,17 @@ def test_kda_layer_k3_shapes_one_token():
     r_out, r_S = om.normwise_rel(out.cpu().numpy(), want), om.normwise_rel(S.cpu().numpy(), S_want)
     print(f"kda layer K3 shapes: out {r_out:.2e} state {r_S:.2e}")
     assert r_out <= 2e-5 and r_S <= 2e-5
+
+
+def test_kda_layer_batch_of_two_sequences():
+    """Two sequences share the weights and keep their own recurrent and convolution states."""
+    cfg, w, attn, rng = _layer(23, 256, 2, scale=0.05)
+    x = om.bf16_round(rng.standard_normal((2, 3, 256)).astype(np.float32))
+    out, S, conv = attn(torch.from_numpy(x).to(DEV).to(torch.bfloat16))
+    want, S_want, conv_want = okda.kda_layer(cfg, w, x)
+    assert om.normwise_rel(out.cpu().numpy(), want) <= 2e-5
+    assert om.normwise_rel(S.cpu().numpy(), S_want) <= 2e-5
+    assert max(om.normwise_rel(a.cpu().numpy(), b) for a, b in zip(conv, conv_want)) <= 1e-6
+    # each sequence alone gives the same rows
+    one, _, _ = attn(torch.from_numpy(x[1:]).to(DEV).to(torch.bfloat16))
+    assert om.normwise_rel(one.cpu().numpy(), out[1:].cpu().numpy()) <= 1e-6

@@ -280,3 +280,30 @@ def test_mla_fused_decode_step_errors():
                   attn.wv.data_ptr(), None, wdev["o_proj.weight"].data_ptr(), lat.data_ptr(), 512, rot.data_ptr(),
                   64, cache.capacity, cache.capacity, 1e-5, 0.1, out.data_ptr(), _lib.K3_F32, cfg.hidden_size,
                   cfg.q_lora_rank, cfg.num_attention_heads, 128, 64, 128, 512, ws.data_ptr(), ws.numel(), None)
+
+
+def test_mla_fused_decode_step_fp32_input_and_bf16_output():
+    """The C-ABI step with fp32 x and bf16 out matches the bf16-x / fp32-out step on the
+    same (bf16-representable) input to bf16 output rounding."""
+    from k3hip import _lib
+    from k3hip.mla import MLAAttention, new_cache
+    cfg = Cfg()
+    rng = np.random.default_rng(5)
+    wdev = {k: torch.from_numpy(bf(v)).to(DEV).to(torch.bfloat16) for k, v in omla.random_mla_weights(rng, cfg).items()}
+    attn = MLAAttention(cfg, wdev)
+    x32 = torch.from_numpy(bf(rng.standard_normal(cfg.hidden_size) * 0.5)).to(DEV)
+    outs = []
+    for xin, odt in ((x32.to(torch.bfloat16), _lib.K3_F32), (x32, _lib.K3_BF16)):
+        cache = new_cache(1, 512, 64, 1, torch.bfloat16, DEV)
+        out = torch.empty(cfg.hidden_size, dtype=torch.float32 if odt == _lib.K3_F32 else torch.bfloat16, device=DEV)
+        ws = torch.empty(1 << 22, dtype=torch.uint8, device=DEV)
+        m = attn._mats
+        _lib.call("k3_mla_step_decode", xin.data_ptr(), _lib.K3_BF16 if xin.dtype == torch.bfloat16 else _lib.K3_F32,
+                  m["q_a"].data_ptr(), attn._q_an32.data_ptr(), m["q_b"].data_ptr(), m["kv_a"].data_ptr(),
+                  attn._kv_an32.data_ptr(), attn.wk.data_ptr(), attn.wv.data_ptr(), m["g"].data_ptr(),
+                  m["o"].data_ptr(), cache.latent.data_ptr(), 512, cache.rot.data_ptr(), 64, cache.capacity, 0,
+                  1e-5, cfg.q_head_dim ** -0.5, out.data_ptr(), odt, cfg.hidden_size, cfg.q_lora_rank,
+                  cfg.num_attention_heads, 128, 64, 128, 512, ws.data_ptr(), ws.numel(), None)
+        torch.cuda.synchronize()
+        outs.append(out.float().cpu().numpy())
+    assert om.normwise_rel(outs[1], outs[0]) <= 2 ** -8
