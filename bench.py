@@ -17,7 +17,8 @@ timed on a bounded sample on this host.  The same line carries, as sub-objects:
   gemv               one [2048 x 7168] projection;
   mla_decode         the absorbed MLA core, 64 heads over 32768 cached tokens;
   mla_step           one token through a whole MLA layer at K3 shapes;
-  kda_decode         one KDA recurrent step (96 heads of 128 x 128 fp32 state);
+  kda_decode         one KDA recurrent step (96 heads of 128 x 128 fp32 state), and a
+                     256-token prefill through the recurrence in one launch;
   kda_step           one token through a whole KDA layer at K3 shapes;
   read_ceiling       single streaming-read / copy launches of the same byte counts.
 
@@ -450,8 +451,23 @@ def bench_kda(torch, steps, warmup, dev):
 
     sec, _ = graph_time(torch, step, steps, warmup)
     stats = None if EAGER else step_stats(torch, step, 32)
+    # a 256-token prefill through the same recurrence in one launch (k3_kda_recurrent)
+    Tp = 256
+    qp, kp, vp = (torch.nn.functional.normalize(torch.randn(Tp, KDA_H, KDA_D, device=dev, generator=gen), dim=-1)
+                  for _ in range(3))
+    gp = -5.0 * torch.sigmoid(torch.randn(Tp, KDA_H, KDA_D, device=dev, generator=gen))
+    bp = torch.sigmoid(torch.randn(Tp, KDA_H, device=dev, generator=gen))
+    op = torch.empty(Tp, KDA_H, KDA_D, device=dev)
+
+    def prefill(i):
+        st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+        _lib.call("k3_kda_recurrent", qp.data_ptr(), kp.data_ptr(), vp.data_ptr(), gp.data_ptr(), bp.data_ptr(),
+                  _lib.K3_F32, states[i % 32].data_ptr(), op.data_ptr(), _lib.K3_F32, Tp, KDA_H, KDA_H, KDA_D, KDA_D,
+                  KDA_D ** -0.5, st)
+
+    psec, _ = graph_time(torch, prefill, 16, 2)
     del states
-    return sec, stats
+    return sec, stats, psec / 16, Tp
 
 
 KS_HID, KS_P = 7168, KDA_H * KDA_D
@@ -666,12 +682,15 @@ def main():
                             "step_us": sstats}
     if "kda" in work:
         ks_ = min(K, 256)
-        kdsec, kdstats = bench_kda(torch, ks_, min(W, 32), dev)
+        kdsec, kdstats, kpre, kTp = bench_kda(torch, ks_, min(W, 32), dev)
         kus = kdsec / ks_ * 1e6
         kgb = KDA_BYTES / (kus * 1e-6) / 1e9
         line["kda_decode"] = {"us": round(kus, 3), "GB/s": round(kgb, 1), "pct_hbm_peak": round(100 * kgb / HBM_PEAK_GBS, 1),
                               "bytes": KDA_BYTES, "heads": KDA_H, "key_dim": KDA_D, "value_dim": KDA_D,
-                              "state": "fp32, in place", "launches": 1, "step_us": kdstats}
+                              "state": "fp32, in place", "launches": 1, "step_us": kdstats,
+                              "prefill": {"tokens": kTp, "us": round(kpre * 1e6, 1),
+                                          "us_per_token": round(kpre * 1e6 / kTp, 3),
+                                          "launches": 1, "what": "k3_kda_recurrent, state kept in registers"}}
     if "kdastep" in work:
         kss = min(K, 128)
         ksec, kstats2 = bench_kda_step(torch, kss, min(W, 16), dev)

@@ -253,6 +253,15 @@ int k3_kda_recurrent_decode(const void *q, const void *k, const void *v, const v
                             int in_dtype, float *state, void *out, int out_dtype, int64_t qk_heads,
                             int64_t v_heads, int64_t key_dim, int64_t value_dim, float scale, void *stream);
 
+/* T tokens in order through the same recurrence in one launch (a prefill, or several
+ * decode tokens): q, k [T, qk_heads, key_dim], v [T, v_heads, value_dim], g [T, v_heads,
+ * key_dim], beta [T, v_heads], out [T, v_heads, value_dim].  Each block keeps its state
+ * columns in registers across the tokens, so the state is read and written once.
+ * Replaces the token loop of KDAAttention._recurrent (attention_kda.py:73-90). */
+int k3_kda_recurrent(const void *q, const void *k, const void *v, const void *g, const void *beta, int in_dtype,
+                     float *state, void *out, int out_dtype, int64_t T, int64_t qk_heads, int64_t v_heads,
+                     int64_t key_dim, int64_t value_dim, float scale, void *stream);
+
 /* Workspace bytes k3_kda_step_decode needs for `heads` heads of 128 (projection outputs and
  * the recurrence output).  No initialisation. */
 int64_t k3_kda_step_workspace_size(int64_t heads);

@@ -22,15 +22,15 @@ constexpr int kKdaK = 128;   // key channels (state rows) per head
 constexpr int kKdaVS = 32;   // value columns per block
 
 struct KdaArgs {
-    const void *q, *k;        // [HQ, K]
-    const void *v;            // [HV, V]
-    const void *g;            // [HV, K] log decay
-    const void *beta;         // [HV]
+    const void *q, *k;        // [T, HQ, K]
+    const void *v;            // [T, HV, V]
+    const void *g;            // [T, HV, K] log decay
+    const void *beta;         // [T, HV]
     int in_bf16;              // q, k, v, g, beta: bf16 (1) or fp32 (0)
     float *S;                 // [HV, K, V] fp32, updated in place
-    void *out;                // [HV, V]
+    void *out;                // [T, HV, V]
     int out_bf16;
-    int HV, G, V;             // G = HV / HQ value heads per q/k head
+    int HV, G, V, T;          // G = HV / HQ value heads per q/k head
     float scale;
 };
 
@@ -48,9 +48,10 @@ __device__ __forceinline__ float sum_row_groups(float x) {
 
 // The update of one block's 32 columns of head h's state, given this thread's four rows'
 // key values kk, scaled query values qq and decay factors dk, its four columns' values vv
-// and the head's beta.  x holds the thread's state values (loaded by the caller).
+// and the head's beta.  x holds the thread's state values (loaded by the caller, stored by
+// the caller once its tokens are done).
 // Returns the read-out of column t (valid in threads t < 32).
-__device__ __forceinline__ float kda_apply(float4 (&x)[4], float *const (&Sp)[4], const float (&kk)[4],
+__device__ __forceinline__ float kda_apply(float4 (&x)[4], const float (&kk)[4],
                                            const float (&qq)[4], const float (&dk)[4], const float (&vv)[4], float b,
                                            float (*red)[4][kKdaVS]) {
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6, cg = t & 7;
@@ -86,7 +87,6 @@ __device__ __forceinline__ float kda_apply(float4 (&x)[4], float *const (&Sp)[4]
         x[j].y = fmaf(bk, d[1], x[j].y);
         x[j].z = fmaf(bk, d[2], x[j].z);
         x[j].w = fmaf(bk, d[3], x[j].w);
-        *reinterpret_cast<float4 *>(Sp[j]) = x[j];
     }
 #pragma unroll
     for (int c = 0; c < 4; ++c) p[c] = 0.f;
@@ -107,6 +107,11 @@ __device__ __forceinline__ float kda_apply(float4 (&x)[4], float *const (&Sp)[4]
     return t < kKdaVS ? ((red[1][0][t] + red[1][1][t]) + red[1][2][t]) + red[1][3][t] : 0.f;
 }
 
+__device__ __forceinline__ void kda_store_state(const float4 (&x)[4], float *const (&Sp)[4]) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) *reinterpret_cast<float4 *>(Sp[j]) = x[j];
+}
+
 // the four state rows t/8 + 32j of columns c0 .. c0+3 of head h
 __device__ __forceinline__ void kda_load_state(float *S, int h, int V, int c0, float4 (&x)[4], float *(&Sp)[4]) {
     const int r = threadIdx.x >> 3;
@@ -117,34 +122,55 @@ __device__ __forceinline__ void kda_load_state(float *S, int h, int V, int c0, f
     }
 }
 
+// T tokens in order; the block's state columns stay in registers between them, so the
+// state is read and written once whatever T is.  The next token's inputs are loaded while
+// the current one is reduced.
 __global__ __launch_bounds__(256) void kda_decode_kernel(KdaArgs a) {
     __shared__ float red[2][4][kKdaVS];
     const int nvb = a.V / kKdaVS;
     const int h = blockIdx.x / nvb, vb = blockIdx.x % nvb;
-    const int hq = h / a.G;
+    const int hq = h / a.G, HQ = a.HV / a.G;
     const int t = threadIdx.x, cg = t & 7, r = t >> 3;
     const int c0 = vb * kKdaVS + 4 * cg;
     const int bf = a.in_bf16;
     float *Sp[4];
     float4 x[4];
     kda_load_state(a.S, h, a.V, c0, x, Sp);
-    float kk[4], qq[4], dk[4], vv[4];
+    float kk[4], qq[4], dk[4], vv[4], b;
+    auto load = [&](int i, float(&k_)[4], float(&q_)[4], float(&d_)[4], float(&v_)[4], float &b_) {
+        const int64_t qo = (static_cast<int64_t>(i) * HQ + hq) * kKdaK, go = (static_cast<int64_t>(i) * a.HV + h) * kKdaK;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        kk[j] = ldx(a.k, static_cast<int64_t>(hq) * kKdaK + r + 32 * j, bf);
-        qq[j] = ldx(a.q, static_cast<int64_t>(hq) * kKdaK + r + 32 * j, bf) * a.scale;
-        dk[j] = expf(ldx(a.g, static_cast<int64_t>(h) * kKdaK + r + 32 * j, bf));
-    }
+        for (int j = 0; j < 4; ++j) {
+            k_[j] = ldx(a.k, qo + r + 32 * j, bf);
+            q_[j] = ldx(a.q, qo + r + 32 * j, bf) * a.scale;
+            d_[j] = ldx(a.g, go + r + 32 * j, bf);
+        }
+        const int64_t vo = (static_cast<int64_t>(i) * a.HV + h) * a.V + c0;
 #pragma unroll
-    for (int c = 0; c < 4; ++c) vv[c] = ldx(a.v, static_cast<int64_t>(h) * a.V + c0 + c, bf);
-    const float o = kda_apply(x, Sp, kk, qq, dk, vv, ldx(a.beta, h, bf), red);
-    if (t < kKdaVS) {
-        const int64_t oi = static_cast<int64_t>(h) * a.V + vb * kKdaVS + t;
-        if (a.out_bf16)
-            static_cast<uint16_t *>(a.out)[oi] = f32_to_bf16(o);
-        else
-            static_cast<float *>(a.out)[oi] = o;
+        for (int c = 0; c < 4; ++c) v_[c] = ldx(a.v, vo + c, bf);
+        b_ = ldx(a.beta, static_cast<int64_t>(i) * a.HV + h, bf);
+    };
+    load(0, kk, qq, dk, vv, b);
+    for (int i = 0; i < a.T; ++i) {
+        float nk[4], nq[4], nd[4], nv[4], nb = 0.f;
+        if (i + 1 < a.T) load(i + 1, nk, nq, nd, nv, nb);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) dk[j] = expf(dk[j]);
+        const float o = kda_apply(x, kk, qq, dk, vv, b, red);
+        if (t < kKdaVS) {
+            const int64_t oi = (static_cast<int64_t>(i) * a.HV + h) * a.V + vb * kKdaVS + t;
+            if (a.out_bf16)
+                static_cast<uint16_t *>(a.out)[oi] = f32_to_bf16(o);
+            else
+                static_cast<float *>(a.out)[oi] = o;
+        }
+        if (i + 1 < a.T) {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) kk[j] = nk[j], qq[j] = nq[j], dk[j] = nd[j], vv[j] = nv[j];
+            b = nb;
+        }
     }
+    kda_store_state(x, Sp);
 }
 
 // ------------------------------------------------------------------ whole KDA layer step
@@ -236,7 +262,8 @@ __global__ __launch_bounds__(256) void kda_step_kernel(KdaStepArgs a) {
     }
 #pragma unroll
     for (int c = 0; c < 4; ++c) vv[c] = vsh[4 * cg + c];
-    const float o = kda_apply(x, Sp, kk, qq, dk, vv, b, red);
+    const float o = kda_apply(x, kk, qq, dk, vv, b, red);
+    kda_store_state(x, Sp);
     // the block's share of the head's sum of squares (for the gated RMSNorm), and o gated
     if (t < kKdaVS) {
         float ss = o * o;
@@ -256,23 +283,24 @@ __global__ __launch_bounds__(256) void kda_step_kernel(KdaStepArgs a) {
 
 using namespace k3;
 
-extern "C" int k3_kda_recurrent_decode(const void *q, const void *k, const void *v, const void *g, const void *beta,
-                                       int in_dtype, float *state, void *out, int out_dtype, int64_t qk_heads,
-                                       int64_t v_heads, int64_t key_dim, int64_t value_dim, float scale,
-                                       void *stream) {
-    if (!q || !k || !v || !g || !beta || !state || !out) return set_error(K3_ERR_NULL, "kda decode: null pointer");
-    if (in_dtype != K3_F32 && in_dtype != K3_BF16) return set_error(K3_ERR_DTYPE, "kda decode: in_dtype %d", in_dtype);
+static int kda_recurrent_impl(const void *q, const void *k, const void *v, const void *g, const void *beta,
+                              int in_dtype, float *state, void *out, int out_dtype, int64_t T, int64_t qk_heads,
+                              int64_t v_heads, int64_t key_dim, int64_t value_dim, float scale, void *stream) {
+    if (!q || !k || !v || !g || !beta || !state || !out) return set_error(K3_ERR_NULL, "kda recurrence: null pointer");
+    if (in_dtype != K3_F32 && in_dtype != K3_BF16)
+        return set_error(K3_ERR_DTYPE, "kda recurrence: in_dtype %d", in_dtype);
     if (out_dtype != K3_F32 && out_dtype != K3_BF16)
-        return set_error(K3_ERR_DTYPE, "kda decode: out_dtype %d", out_dtype);
+        return set_error(K3_ERR_DTYPE, "kda recurrence: out_dtype %d", out_dtype);
     if (key_dim != kKdaK)
-        return set_error(K3_ERR_SHAPE, "kda decode: key_dim=%lld; the kernel takes %d", (long long)key_dim, kKdaK);
+        return set_error(K3_ERR_SHAPE, "kda recurrence: key_dim=%lld; the kernel takes %d", (long long)key_dim, kKdaK);
     if (value_dim <= 0 || value_dim % kKdaVS || value_dim > 4096)
-        return set_error(K3_ERR_SHAPE, "kda decode: value_dim=%lld must be a positive multiple of %d, <= 4096",
+        return set_error(K3_ERR_SHAPE, "kda recurrence: value_dim=%lld must be a positive multiple of %d, <= 4096",
                          (long long)value_dim, kKdaVS);
     if (qk_heads <= 0 || v_heads <= 0 || v_heads % qk_heads || v_heads > (1 << 20))
-        return set_error(K3_ERR_SHAPE, "kda decode: v_heads=%lld must be a positive multiple of qk_heads=%lld",
+        return set_error(K3_ERR_SHAPE, "kda recurrence: v_heads=%lld must be a positive multiple of qk_heads=%lld",
                          (long long)v_heads, (long long)qk_heads);
-    if (!aligned16(state)) return set_error(K3_ERR_ALIGN, "kda decode: the state must be 16-byte aligned");
+    if (T <= 0 || T > (1 << 24)) return set_error(K3_ERR_SHAPE, "kda recurrence: T=%lld", (long long)T);
+    if (!aligned16(state)) return set_error(K3_ERR_ALIGN, "kda recurrence: the state must be 16-byte aligned");
     KdaArgs a{};
     a.q = q, a.k = k, a.v = v, a.g = g, a.beta = beta;
     a.in_bf16 = in_dtype == K3_BF16;
@@ -282,10 +310,26 @@ extern "C" int k3_kda_recurrent_decode(const void *q, const void *k, const void 
     a.HV = static_cast<int>(v_heads);
     a.G = static_cast<int>(v_heads / qk_heads);
     a.V = static_cast<int>(value_dim);
+    a.T = static_cast<int>(T);
     a.scale = scale;
     const int64_t blocks = v_heads * (value_dim / kKdaVS);
     kda_decode_kernel<<<dim3(static_cast<unsigned>(blocks)), 256, 0, static_cast<hipStream_t>(stream)>>>(a);
-    return check_hip(hipGetLastError(), "kda decode launch");
+    return check_hip(hipGetLastError(), "kda recurrence launch");
+}
+
+extern "C" int k3_kda_recurrent_decode(const void *q, const void *k, const void *v, const void *g, const void *beta,
+                                       int in_dtype, float *state, void *out, int out_dtype, int64_t qk_heads,
+                                       int64_t v_heads, int64_t key_dim, int64_t value_dim, float scale,
+                                       void *stream) {
+    return kda_recurrent_impl(q, k, v, g, beta, in_dtype, state, out, out_dtype, 1, qk_heads, v_heads, key_dim,
+                              value_dim, scale, stream);
+}
+
+extern "C" int k3_kda_recurrent(const void *q, const void *k, const void *v, const void *g, const void *beta,
+                                int in_dtype, float *state, void *out, int out_dtype, int64_t T, int64_t qk_heads,
+                                int64_t v_heads, int64_t key_dim, int64_t value_dim, float scale, void *stream) {
+    return kda_recurrent_impl(q, k, v, g, beta, in_dtype, state, out, out_dtype, T, qk_heads, v_heads, key_dim,
+                              value_dim, scale, stream);
 }
 
 namespace {

@@ -52,6 +52,7 @@ SIGNATURES: dict[str, list] = {
     "k3_mla_step_decode": [_P, _I32, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _P, _I64, _I64, _I64, _F32,
                            _F32, _P, _I32, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _P, _I64, _P],
     "k3_kda_recurrent_decode": [_P, _P, _P, _P, _P, _I32, _P, _P, _I32, _I64, _I64, _I64, _I64, _F32, _P],
+    "k3_kda_recurrent": [_P, _P, _P, _P, _P, _I32, _P, _P, _I32, _I64, _I64, _I64, _I64, _I64, _F32, _P],
     "k3_kda_step_workspace_size": [_I64],
     "k3_kda_step_decode": [_P, _I32, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I32,
                            _I64, _I64, _I64, _I64, _F32, _F32, _P, _I64, _P],

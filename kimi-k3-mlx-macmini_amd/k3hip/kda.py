@@ -10,8 +10,9 @@ recurrence, gated RMSNorm, o_proj in four launches).  The recurrent state is fp3
 ``kda_recurrent(q, k, v, g, beta, scale, state)`` takes the reference's tensors
 (q, k [B, T, H, K]; v [B, T, HV, V]; g [B, T, HV, K] log decay; beta [B, T, HV]; state
 [B, HV, K, V] or None) and returns ``(o [B, T, HV, V] fp32, state [B, HV, K, V] fp32)``.
-Each token is one launch of ``k3_kda_recurrent_decode`` over all B * HV heads, updating the
-fp32 state in place (the reference allocates a new state per step).  A state passed in is
+All tokens are one launch of ``k3_kda_recurrent`` over all B * HV heads, the state kept in
+registers between tokens and updated in place once (the reference allocates a new state
+per step).  A state passed in is
 used as the output state when it is a contiguous fp32 device tensor, else copied once.
 """
 from __future__ import annotations
@@ -50,11 +51,11 @@ def kda_recurrent(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, g: torch.Te
     o = torch.empty((Tn, B, HV, V), dtype=torch.float32, device=q.device)
     code = T.dtype_code(dt)
     st = T.stream(q)
-    for i in range(Tn):
-        # B sequences are B * HV independent heads: q/k head b * H + h serves value heads
-        # (b * HV + h * G) .. + G, the same grouping as within one sequence
-        _lib.call("k3_kda_recurrent_decode", T.ptr(q[i]), T.ptr(k[i]), T.ptr(v[i]), T.ptr(g[i]), T.ptr(beta[i]),
-                  code, T.ptr(S), T.ptr(o[i]), _lib.K3_F32, B * H, B * HV, K, V, float(scale), st)
+    # B sequences are B * HV independent heads: q/k head b * H + h serves value heads
+    # (b * HV + h * G) .. + G, the same grouping as within one sequence; all tokens in one
+    # launch, the state kept in registers between them
+    _lib.call("k3_kda_recurrent", T.ptr(q), T.ptr(k), T.ptr(v), T.ptr(g), T.ptr(beta), code, T.ptr(S), T.ptr(o),
+              _lib.K3_F32, Tn, B * H, B * HV, K, V, float(scale), st)
     return o.transpose(0, 1), S
 
 

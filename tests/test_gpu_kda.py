@@ -137,3 +137,20 @@ def test_kda_layer_batch_of_two_sequences():
     # each sequence alone gives the same rows
     one, _, _ = attn(torch.from_numpy(x[1:]).to(DEV).to(torch.bfloat16))
     assert om.normwise_rel(one.cpu().numpy(), out[1:].cpu().numpy()) <= 1e-6
+
+
+def test_kda_long_sequence_one_launch():
+    """48 tokens in one launch (the state stays in registers between tokens) against the
+    oracle, and equal to the same tokens split 20 + 28 across two calls."""
+    from k3hip.kda import kda_recurrent
+    rng = np.random.default_rng(31)
+    q, k, v, g, beta, S0 = _inputs(rng, 1, 48, 16, 16)
+    o, S = kda_recurrent(*_dev(q, k, v, g, beta), state=_dev(S0)[0])
+    want_o, want_S = okda.kda_recurrent(q, k, v, g, beta, None, S0)
+    ro, rs = om.normwise_rel(o.cpu().numpy(), want_o), om.normwise_rel(S.cpu().numpy(), want_S)
+    print(f"48 tokens: out {ro:.2e} state {rs:.2e}")
+    assert ro <= TOL and rs <= TOL
+    sl = lambda a, i, j: a[:, i:j]  # noqa: E731
+    o1, S1 = kda_recurrent(*_dev(*(sl(a, 0, 20) for a in (q, k, v, g, beta))), state=_dev(S0)[0])
+    o2, S2 = kda_recurrent(*_dev(*(sl(a, 20, 48) for a in (q, k, v, g, beta))), state=S1)
+    assert torch.equal(torch.cat([o1, o2], 1), o) and torch.equal(S2, S)
