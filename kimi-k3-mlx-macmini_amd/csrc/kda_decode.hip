@@ -125,6 +125,7 @@ __device__ __forceinline__ void kda_load_state(float *S, int h, int V, int c0, f
 // T tokens in order; the block's state columns stay in registers between them, so the
 // state is read and written once whatever T is.  The next token's inputs are loaded while
 // the current one is reduced.
+template <bool MULTI>
 __global__ __launch_bounds__(256) void kda_decode_kernel(KdaArgs a) {
     __shared__ float red[2][4][kKdaVS];
     const int nvb = a.V / kKdaVS;
@@ -151,9 +152,10 @@ __global__ __launch_bounds__(256) void kda_decode_kernel(KdaArgs a) {
         b_ = ldx(a.beta, static_cast<int64_t>(i) * a.HV + h, bf);
     };
     load(0, kk, qq, dk, vv, b);
-    for (int i = 0; i < a.T; ++i) {
+    const int T = MULTI ? a.T : 1;
+    for (int i = 0; i < T; ++i) {
         float nk[4], nq[4], nd[4], nv[4], nb = 0.f;
-        if (i + 1 < a.T) load(i + 1, nk, nq, nd, nv, nb);
+        if (MULTI && i + 1 < T) load(i + 1, nk, nq, nd, nv, nb);
 #pragma unroll
         for (int j = 0; j < 4; ++j) dk[j] = expf(dk[j]);
         const float o = kda_apply(x, kk, qq, dk, vv, b, red);
@@ -164,7 +166,7 @@ __global__ __launch_bounds__(256) void kda_decode_kernel(KdaArgs a) {
             else
                 static_cast<float *>(a.out)[oi] = o;
         }
-        if (i + 1 < a.T) {
+        if (MULTI && i + 1 < T) {
 #pragma unroll
             for (int j = 0; j < 4; ++j) kk[j] = nk[j], qq[j] = nq[j], dk[j] = nd[j], vv[j] = nv[j];
             b = nb;
@@ -313,7 +315,10 @@ static int kda_recurrent_impl(const void *q, const void *k, const void *v, const
     a.T = static_cast<int>(T);
     a.scale = scale;
     const int64_t blocks = v_heads * (value_dim / kKdaVS);
-    kda_decode_kernel<<<dim3(static_cast<unsigned>(blocks)), 256, 0, static_cast<hipStream_t>(stream)>>>(a);
+    if (T == 1)
+        kda_decode_kernel<false><<<dim3(static_cast<unsigned>(blocks)), 256, 0, static_cast<hipStream_t>(stream)>>>(a);
+    else
+        kda_decode_kernel<true><<<dim3(static_cast<unsigned>(blocks)), 256, 0, static_cast<hipStream_t>(stream)>>>(a);
     return check_hip(hipGetLastError(), "kda recurrence launch");
 }
 
