@@ -154,3 +154,12 @@ def test_kda_long_sequence_one_launch():
     o1, S1 = kda_recurrent(*_dev(*(sl(a, 0, 20) for a in (q, k, v, g, beta))), state=_dev(S0)[0])
     o2, S2 = kda_recurrent(*_dev(*(sl(a, 20, 48) for a in (q, k, v, g, beta))), state=S1)
     assert torch.equal(torch.cat([o1, o2], 1), o) and torch.equal(S2, S)
+
+
+def test_kda_layer_other_head_count_and_fp32_input():
+    """Eight heads, hidden 1024, fp32 x: three tokens against the fp64 layer."""
+    cfg, w, attn, rng = _layer(24, 1024, 8, scale=0.05)
+    x = rng.standard_normal((1, 3, 1024)).astype(np.float32)
+    out, S, _ = attn(torch.from_numpy(x).to(DEV))
+    want, S_want, _ = okda.kda_layer(cfg, w, x)
+    assert om.normwise_rel(out.cpu().numpy(), want) <= 2e-5 and om.normwise_rel(S.cpu().numpy(), S_want) <= 2e-5

@@ -307,3 +307,36 @@ def test_mla_fused_decode_step_fp32_input_and_bf16_output():
         torch.cuda.synchronize()
         outs.append(out.float().cpu().numpy())
     assert om.normwise_rel(outs[1], outs[0]) <= 2 ** -8
+
+
+@pytest.mark.parametrize("hidden,heads,q_lora,gate", [(1024, 16, 512, False), (768, 4, 1536, True)])
+def test_mla_fused_decode_step_other_shapes(hidden, heads, q_lora, gate):
+    """Other head counts, q_lora ranks and no output gate: the fused step against the
+    fp64 restatement on the latents it stored, nine tokens from an empty cache."""
+    from k3hip.mla import MLAAttention
+    cfg = Cfg(hidden_size=hidden, num_attention_heads=heads, q_lora_rank=q_lora, mla_use_output_gate=gate)
+    rng = np.random.default_rng(hidden + heads)
+    w32 = {k: bf(v) for k, v in omla.random_mla_weights(rng, cfg).items()}
+    wdev = {k: torch.from_numpy(v).to(DEV).to(torch.bfloat16) for k, v in w32.items()}
+    attn = MLAAttention(cfg, wdev)
+    assert attn.fused_step
+    x = bf((rng.standard_normal((1, 9, hidden)) * 0.5).astype(np.float32))
+    xd = torch.from_numpy(x).to(DEV).to(torch.bfloat16)
+    cache = None
+    w = {k: v.astype(np.float64) for k, v in w32.items()}
+    kb = w["kv_b_proj.weight"].reshape(heads, 256, 512)
+    rms = lambda a, g: g * a / np.sqrt((a * a).mean(-1, keepdims=True) + cfg.rms_norm_eps)  # noqa: E731
+    worst = 0.0
+    for t in range(9):
+        o, cache = attn(xd[:, t:t + 1], cache=cache)
+        lat = cache.latent[0, :t + 1].float().cpu().numpy().astype(np.float64)
+        rot = cache.rot[0, :t + 1].float().cpu().numpy().astype(np.float64)
+        q = (rms(x[0, t].astype(np.float64) @ w["q_a_proj.weight"].T, w["q_a_layernorm.weight"])
+             @ w["q_b_proj.weight"].T).reshape(heads, 192)
+        oo = omla.mla_decode_absorbed(q[:, :128], q[:, 128:], kb[:, :128], kb[:, 128:], lat, rot,
+                                      192 ** -0.5)[0].reshape(-1)
+        if gate:
+            oo = oo / (1.0 + np.exp(-(x[0, t].astype(np.float64) @ w["g_proj.weight"].T)))
+        worst = max(worst, om.normwise_rel(o.float().cpu().numpy().reshape(-1), oo @ w["o_proj.weight"].T))
+    print(f"hidden={hidden} heads={heads} q_lora={q_lora} gate={gate}: {worst:.2e}")
+    assert worst <= 1e-4
