@@ -19,7 +19,8 @@ timed on a bounded sample on this host.  The same line carries, as sub-objects:
   mla_step           one token through a whole MLA layer at K3 shapes;
   kda_decode         one KDA recurrent step (96 heads of 128 x 128 fp32 state), and a
                      256-token prefill through the recurrence in one launch;
-  kda_step           one token through a whole KDA layer at K3 shapes;
+  kda_step           one token through a whole KDA layer at K3 shapes, and a 256-token
+                     prompt through its prefill path;
   read_ceiling       single streaming-read / copy launches of the same byte counts.
 
 Synthetic, seeded data; weights are random-init with the benchmark shapes.  Steps are
@@ -509,8 +510,20 @@ def bench_kda_step(torch, steps, warmup, dev):
 
     sec, _ = graph_time(torch, step, steps, warmup)
     stats = None if EAGER else step_stats(torch, step, 32)
+    # a 256-token prompt through KDAAttention's prefill path (eager: GEMMs on the BLAS
+    # library, one recurrence launch), timed with events
+    xp = torch.randn(1, 256, KS_HID, device=dev, generator=gen).to(torch.bfloat16)
+    attn(xp)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(3):
+        attn(xp)
+    e1.record()
+    torch.cuda.synchronize()
+    pre = e0.elapsed_time(e1) / 3 / 1e3
     del attn
-    return sec, stats
+    return sec, stats, pre
 
 
 def bench_read_ceiling(torch, nbytes, steps, dev):
@@ -693,12 +706,14 @@ def main():
                                           "launches": 1, "what": "k3_kda_recurrent, state kept in registers"}}
     if "kdastep" in work:
         kss = min(K, 128)
-        ksec, kstats2 = bench_kda_step(torch, kss, min(W, 16), dev)
+        ksec, kstats2, kpre2 = bench_kda_step(torch, kss, min(W, 16), dev)
         kus2 = ksec / kss * 1e6
         kgb2 = KS_BYTES / (kus2 * 1e-6) / 1e9
         line["kda_step"] = {"us": round(kus2, 2), "GB/s": round(kgb2, 1), "pct_hbm_peak": round(100 * kgb2 / HBM_PEAK_GBS, 1),
                             "bytes": KS_BYTES, "hidden": KS_HID, "heads": KDA_H, "head_dim": KDA_D, "conv": 4,
-                            "weights": "bf16", "launches": 4, "step_us": kstats2}
+                            "weights": "bf16", "launches": 4, "step_us": kstats2,
+                            "prefill_256_tokens": {"ms": round(kpre2 * 1e3, 3), "tokens_per_s": round(256 / kpre2, 1),
+                                                   "what": "KDAAttention.prefill: BLAS GEMMs + one k3_kda_recurrent"}}
     if "ceiling" in work:
         ce = bench_read_ceiling(torch, EXPERT_BYTES, 256, dev)
         cl = bench_read_ceiling(torch, LAYER_BYTES, 64, dev)

@@ -2,9 +2,11 @@
 (air_llm/models/kimi_k3/attention_kda.py:32-115).
 
 ``KDAAttention(cfg, w)`` keeps the reference constructor, weight names and
-``__call__(x, state=None, conv=None) -> (out, state, (cq, ck, cv))``; every token of every
-sequence is one ``k3_kda_step_decode`` (projections, short convolutions, norms, gate,
-recurrence, gated RMSNorm, o_proj in four launches).  The recurrent state is fp32
+``__call__(x, state=None, conv=None) -> (out, state, (cq, ck, cv))``.  Up to
+``PREFILL_TOKENS`` tokens per call, every token of every sequence is one
+``k3_kda_step_decode`` (projections, short convolutions, norms, gate, recurrence, gated
+RMSNorm, o_proj in four launches); longer calls take ``prefill``: GEMMs over all tokens on
+the BLAS library and the recurrence over all tokens in one ``k3_kda_recurrent`` launch.  The recurrent state is fp32
 [B, H, 128, 128], updated in place; the convolution states come back as fp32 [B, k-1, C].
 
 ``kda_recurrent(q, k, v, g, beta, scale, state)`` takes the reference's tensors
@@ -97,9 +99,57 @@ class KDAAttention:
                   _lib.K3_F32, x1.shape[-1], self.H, self.D, self.K, float(c.kda_gate_lower_bound),
                   float(c.rms_norm_eps), T.ptr(ws), ws.numel(), T.stream(x1))
 
+    PREFILL_TOKENS = 8   # more tokens per call than this take the prefill path
+
+    @staticmethod
+    def _mm(a: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
+        """a [M, K] @ w[N, K]^T with fp32 output on the BLAS library.  A bf16 a (the layer
+        input) meets the bf16 weight directly, with fp32 accumulation and output where torch
+        offers it; an fp32 a (an intermediate) keeps its precision: fp32 operands."""
+        if a.dtype == torch.bfloat16:
+            try:
+                return torch.mm(a, w.t(), out_dtype=torch.float32)
+            except (RuntimeError, TypeError):
+                pass
+        return a.to(torch.float32) @ w.to(torch.float32).t()
+
+    def prefill(self, x: torch.Tensor, state: torch.Tensor | None = None, conv: tuple | None = None):
+        """Many tokens (attention_kda.py:94-115): the projections as GEMMs over all tokens
+        (each weight read once), the convolutions, norms and gates as tensor ops, the
+        recurrence over every token in one k3_kda_recurrent launch, the gated RMSNorm, and
+        o_proj as one GEMM."""
+        c = self.cfg
+        B, Tn, hid = x.shape
+        H, D, K = self.H, self.D, self.K
+        P = H * D
+        xf = x.reshape(B * Tn, hid)
+        proj = lambda w: self._mm(xf, w).reshape(B, Tn, -1)  # noqa: E731
+        outs, states = [], []
+        for m, (w, cw) in enumerate(((self.q_w, self.qc), (self.k_w, self.kc), (self.v_w, self.vc))):
+            y = proj(w)
+            pad = (torch.zeros((B, K - 1, P), dtype=torch.float32, device=x.device) if conv is None
+                   else conv[m].to(torch.float32).reshape(B, K - 1, P))
+            xp = torch.cat([pad, y], dim=1)
+            z = sum(cw[:, j] * xp[:, j:j + Tn] for j in range(K))
+            outs.append(z * torch.sigmoid(z))
+            states.append(xp[:, Tn:].contiguous())
+        q, k, v = (o_.reshape(B, Tn, H, D) for o_ in outs)
+        q = q * torch.rsqrt((q * q).sum(-1, keepdim=True) + 1e-6)
+        k = k * torch.rsqrt((k * k).sum(-1, keepdim=True) + 1e-6)
+        g_raw = self._mm(self._mm(xf, self.fa), self.fb).reshape(B, Tn, H, D) + self.dt_bias.reshape(H, D)
+        g = c.kda_gate_lower_bound * torch.sigmoid(torch.exp(self.A_log[:H]).reshape(H, 1) * g_raw)
+        beta = torch.sigmoid(proj(self.b_w))
+        o, state = kda_recurrent(q, k, v, g, beta, D ** -0.5, state)
+        og = proj(self.g_w).reshape(B, Tn, H, D)
+        o = o * torch.rsqrt((o * o).mean(-1, keepdim=True) + c.rms_norm_eps) * self.o_norm_w * torch.sigmoid(og)
+        out = self._mm(o.reshape(B * Tn, P), self.o_w).reshape(B, Tn, hid)
+        return out, state, tuple(states)
+
     def __call__(self, x: torch.Tensor, state: torch.Tensor | None = None, conv: tuple | None = None):
         T.require_device(x, state)
         B, Tn, hid = x.shape
+        if Tn > self.PREFILL_TOKENS:
+            return self.prefill(x, state, conv)
         H, D, K = self.H, self.D, self.K
         P = H * D
         if state is None:

@@ -163,3 +163,20 @@ def test_kda_layer_other_head_count_and_fp32_input():
     out, S, _ = attn(torch.from_numpy(x).to(DEV))
     want, S_want, _ = okda.kda_layer(cfg, w, x)
     assert om.normwise_rel(out.cpu().numpy(), want) <= 2e-5 and om.normwise_rel(S.cpu().numpy(), S_want) <= 2e-5
+
+
+def test_kda_layer_prefill_path_matches_oracle_and_decode():
+    """Twelve tokens take the prefill path (BLAS GEMMs + one recurrence launch); they match
+    the fp64 layer, and decode tokens continue from the states it returns."""
+    cfg, w, attn, rng = _layer(25, 512, 4, scale=0.05)
+    x = om.bf16_round(rng.standard_normal((1, 14, 512)).astype(np.float32))
+    xd = torch.from_numpy(x).to(DEV).to(torch.bfloat16)
+    out, S, conv = attn(xd[:, :12])
+    want, S_want, conv_want = okda.kda_layer(cfg, w, x[:, :12])
+    r = om.normwise_rel(out.cpu().numpy(), want)
+    print(f"kda prefill 12 tokens: {r:.2e}")
+    assert r <= 2e-5 and om.normwise_rel(S.cpu().numpy(), S_want) <= 2e-5
+    assert max(om.normwise_rel(a.cpu().numpy(), b) for a, b in zip(conv, conv_want)) <= 1e-6
+    o2, S2, _ = attn(xd[:, 12:], state=S, conv=conv)
+    want2, _, _ = okda.kda_layer(cfg, w, x[:, 12:], S_want, conv_want)
+    assert om.normwise_rel(o2.cpu().numpy(), want2) <= 2e-5
