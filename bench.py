@@ -22,6 +22,8 @@ timed on a bounded sample on this host.  The same line carries, as sub-objects:
   kda_step           one token through a whole KDA layer at K3 shapes, and a 256-token
                      prompt through its prefill path;
   read_ceiling       single streaming-read / copy launches of the same byte counts.
+`cpu_baseline` also times the 384-expert layer and the MLA core on the CPU (moe_layer,
+mla_decode sub-objects).
 
 Synthetic, seeded data; weights are random-init with the benchmark shapes.  Steps are
 captured once into a HIP graph and replayed, so the timed region is GPU work plus the
@@ -572,7 +574,10 @@ def bench_cpu(sample_s=12.0):
     from oracle import cpu_baseline
     n = len(os.sched_getaffinity(0))
     torch.set_num_threads(n)
-    return cpu_baseline.time_expert(H, I, sample_s=sample_s, threads=n)
+    out = cpu_baseline.time_expert(H, I, sample_s=sample_s, threads=n)
+    out["moe_layer"] = cpu_baseline.time_layer(H, I, E_LAYER, TOPK, sample_s=sample_s / 2, threads=n)
+    out["mla_decode"] = cpu_baseline.time_mla(MLA_H, MLA_T, sample_s=sample_s / 3, threads=n)
+    return out
 
 
 def traffic_from_profiles():

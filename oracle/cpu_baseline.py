@@ -84,3 +84,80 @@ def time_expert(H: int, I: int, sample_s: float = 12.0, threads: int | None = No
         "matmul_only_ms": round(t_m * 1e3, 3),
         "cpu": _cpu_model(),
     }
+
+
+def _run(fn, budget):
+    fn()
+    times = []
+    t_end = time.perf_counter() + budget
+    while time.perf_counter() < t_end or len(times) < 3:
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+    return float(np.median(times)), len(times)
+
+
+def time_layer(H: int, I: int, E: int, k: int, sample_s: float = 6.0, threads: int | None = None,
+               pool: int = 16, seed: int = 1003) -> dict:
+    """The 384-expert layer at batch 1 on the CPU (k3ref/layers.py:214-261 with the softmax
+    router): router logits, softmax top-k, the k selected experts decoded on access and run
+    in fp32, the bf16 shared expert in fp32.  The expert weights come from a pool of
+    ``pool`` random experts (index mod pool), so each call decodes k experts as k3ref does
+    without 9 GB of host weights."""
+    import torch
+
+    threads = threads or len(os.sched_getaffinity(0))
+    torch.set_num_threads(threads)
+    rng = np.random.default_rng(seed)
+    experts = [(random_mxfp4(rng, I, H), random_mxfp4(rng, I, H), random_mxfp4(rng, H, I)) for _ in range(pool)]
+    wr = torch.from_numpy(bf16_round((rng.standard_normal((E, H)) * 0.02).astype(np.float32)))
+    sh = [torch.from_numpy(bf16_round((rng.standard_normal(s) * 0.02).astype(np.float32)))
+          for s in ((I, H), (I, H), (H, I))]
+    xs = [torch.from_numpy(bf16_round(rng.standard_normal((1, H)).astype(np.float32))) for _ in range(8)]
+    it = [0]
+
+    def layer():
+        x = xs[it[0] % 8]
+        it[0] += 1
+        p = torch.softmax(x @ wr.T, dim=-1)
+        w, idx = torch.topk(p, k, dim=-1)
+        y = torch.zeros(1, H)
+        for j in range(k):
+            g, u, d = experts[int(idx[0, j]) % pool]
+            a = torch.nn.functional.silu(x @ torch.from_numpy(decode_mxfp4(*g)).T) * (x @ torch.from_numpy(decode_mxfp4(*u)).T)
+            y += w[0, j] * (a @ torch.from_numpy(decode_mxfp4(*d)).T)
+        a = torch.nn.functional.silu(x @ sh[0].T) * (x @ sh[1].T)
+        return y + a @ sh[2].T
+
+    t, n = _run(layer, sample_s)
+    return {"ms": round(t * 1e3, 2), "calls": n, "cores": threads,
+            "sample": (f"{n} calls of the {E}-expert top-{k} layer with a bf16 shared expert (softmax router, "
+                       f"{k} experts decoded on access from a pool of {pool}, fp32 torch matmuls), median")}
+
+
+def time_mla(H: int, T: int, sample_s: float = 4.0, threads: int | None = None, seed: int = 1005) -> dict:
+    """The absorbed MLA decode core on the CPU as the reference computes it
+    (attention_mla.py:85-87, 193-212): the bf16 cache upcast to fp32 every step, fp32
+    products and softmax."""
+    import torch
+
+    threads = threads or len(os.sched_getaffinity(0))
+    torch.set_num_threads(threads)
+    g = torch.Generator().manual_seed(seed)
+    lat = torch.randn(T, 512, generator=g).to(torch.bfloat16)
+    rot = torch.randn(T, 64, generator=g).to(torch.bfloat16)
+    wk = (torch.randn(H, 128, 512, generator=g) * 0.02).to(torch.bfloat16)
+    wv = (torch.randn(H, 128, 512, generator=g) * 0.02).to(torch.bfloat16)
+    qn = torch.randn(H, 1, 128, generator=g)
+    qr = torch.randn(H, 1, 64, generator=g)
+
+    def core():
+        latf, rotf = lat.float(), rot.float()
+        qa = qn @ wk.float()                                      # [H, 1, 512]
+        s = (qa @ latf.T + qr @ rotf.T) * 192 ** -0.5             # [H, 1, T]
+        p = torch.softmax(s, dim=-1)
+        return (p @ latf) @ wv.float().transpose(1, 2)            # [H, 1, 128]
+
+    t, n = _run(core, sample_s)
+    return {"ms": round(t * 1e3, 2), "calls": n, "cores": threads,
+            "sample": f"{n} calls of the absorbed core, {H} heads over {T} bf16 cache rows (fp32 upcast per call), median"}
