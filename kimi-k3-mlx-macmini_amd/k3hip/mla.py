@@ -209,6 +209,15 @@ class MLAAttention:
 
     @staticmethod
     def _mm(a: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
+        """a @ w^T with fp32 output.  bf16 a against bf16 w runs as one BLAS GEMM with fp32
+        accumulation and output (the same products as in fp32, no weight copy); otherwise
+        both operands go to fp32."""
+        if a.dtype == torch.bfloat16 and w.dtype == torch.bfloat16 and a.is_cuda:
+            try:
+                return torch.mm(a.reshape(-1, a.shape[-1]), w.t(), out_dtype=torch.float32).reshape(
+                    *a.shape[:-1], w.shape[0])
+            except (RuntimeError, TypeError):
+                pass
         return a.to(torch.float32) @ w.to(torch.float32).T
 
     def __call__(self, x: torch.Tensor, cache: MLACache | None = None):
