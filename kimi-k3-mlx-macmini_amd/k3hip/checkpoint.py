@@ -17,7 +17,8 @@ MoE decode path reads.
   every fetched projection (loader.py:246-247).
 * Reads land in page-locked host buffers and reach the GPU by asynchronous copies on a
   copy stream of default priority, with two staging buffers in flight, so the file read
-  of one projection overlaps the host-to-device copy of the previous one.
+  of one projection overlaps the host-to-device copy of the previous one (four reader
+  threads with their own buffers in ``load_experts``).
   ``load_experts(layer, n)`` makes a layer's experts resident in one device allocation
   (each projection keeps the file's [packed | scales] order) and checks every scale
   region on the device with one host synchronisation per layer.
@@ -225,6 +226,7 @@ class TensorSource:
         """The next page-locked staging buffer, once the copy that last read it is done."""
         if self._copy is None:
             self._copy = torch.cuda.Stream(self._dev())
+        if self._stage is None:
             self._stage = [None, None]
         i = self._next
         self._next ^= 1
@@ -312,9 +314,7 @@ class TensorSource:
         mm = torch.empty((len(names), 2), dtype=torch.int32, device=self._dev())
         views = {}
         before = self.bytes_read
-        for j, (e, w) in enumerate(names):
-            packed, scales = self._fetch_pair(expert_name(layer, e, w), buf[offs[j]:offs[j] + sizes[j]])
-            views[(e, w)] = (packed, scales)
+        self._load_parallel(layer, names, buf, offs, sizes, views)
         self._ready()
         st = torch.cuda.current_stream(self._dev())
         for j, (e, w) in enumerate(names):
@@ -330,6 +330,76 @@ class TensorSource:
         self.experts_loaded += len(names)
         self.expert_bytes += self.bytes_read - before
         return ResidentExperts(layer, n_experts, buf, views)
+
+
+    READERS = 4   # reader threads (and page-locked staging buffers) of load_experts
+
+    def _load_parallel(self, layer, names, buf, offs, sizes, views) -> None:
+        """Read the projections with READERS threads (positional reads on per-file
+        descriptors, no shared file offset), each into its own page-locked buffer; the
+        calling thread uploads them in order on the copy stream.  A buffer is refilled only
+        after the copy that read it has finished."""
+        import os
+        from concurrent.futures import ThreadPoolExecutor
+        if self._copy is None:
+            self._copy = torch.cuda.Stream(self._dev())
+        nr = self.READERS
+        cap = max(sizes)
+        stages = [torch.empty(cap, dtype=torch.uint8, pin_memory=True) for _ in range(nr)]
+        events = [None] * nr
+        fds = {}
+
+        def fd(file):
+            f = fds.get(file)
+            if f is None:
+                f = fds[file] = os.open(self.ckpt / file, os.O_RDONLY)
+            return f
+
+        for e, w in names:                       # open every file on this thread first
+            ra, rb, _ = self._pair(expert_name(layer, e, w))
+            fd(ra["file"]), fd(rb["file"])
+
+        def read(j):
+            e, w = names[j]
+            ra, rb, adjacent = self._pair(expert_name(layer, e, w))
+            i = j % nr
+            if events[i] is not None:
+                events[i].synchronize()
+            hv = memoryview(stages[i].numpy()).cast("B")
+            na, nb = ra["nbytes"], rb["nbytes"]
+            parts = [(ra, 0, na + nb)] if adjacent else [(ra, 0, na), (rb, na, nb)]
+            for r, at, n in parts:
+                got = os.preadv(fds[r["file"]], [hv[at:at + n]], r["offset"])
+                if got != n:
+                    raise ValueError(f"short read from {r['file']} at {r['offset']}: {got} of {n} bytes")
+            return len(parts), na + nb
+
+        try:
+            with ThreadPoolExecutor(nr) as pool:
+                fut = {j: pool.submit(read, j) for j in range(min(nr, len(names)))}
+                for j, (e, w) in enumerate(names):
+                    nreads, n = fut.pop(j).result()
+                    self.reads += nreads
+                    self.bytes_read += n
+                    i = j % nr
+                    ra, rb, _ = self._pair(expert_name(layer, e, w))
+                    dst = buf[offs[j]:offs[j] + sizes[j]]
+                    self._copy.wait_stream(torch.cuda.current_stream(self._dev()))
+                    with torch.cuda.stream(self._copy):
+                        dst.copy_(stages[i][:n], non_blocking=True)
+                        ev = torch.cuda.Event()
+                        ev.record(self._copy)
+                    events[i] = ev
+                    views[(e, w)] = (dst[:ra["nbytes"]].view(ra["shape"]),
+                                     dst[ra["nbytes"]:ra["nbytes"] + rb["nbytes"]].view(rb["shape"]))
+                    if j + nr < len(names):
+                        fut[j + nr] = pool.submit(read, j + nr)
+            for ev in events:
+                if ev is not None:
+                    ev.synchronize()
+        finally:
+            for f in fds.values():
+                os.close(f)
 
 
 class ResidentExperts:
