@@ -2,7 +2,7 @@
 
 TEST INFRASTRUCTURE ONLY.  Nothing in the product path (the ``k3hip`` package and
 ``libk3hip.so``) imports, links or calls this package.  Its only legitimate users are
-``tests/``, ``__graft_entry__.smoke()`` (as the checker of the HIP result) and the
+``tests/``, ``__graft_entry__.smoke()`` (to check the HIP result) and the
 ``cpu_baseline`` leg of ``bench.py`` (a timed CPU restatement of the reference CPU path).
 
 Modules

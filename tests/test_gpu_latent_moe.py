@@ -6,7 +6,7 @@ here (the decode kernel rounds its fp32 row dots; the grouped path uses torch's 
 and the oracle rounds it the same way; a 1-ulp difference in a
 few elements of h (fp32 vs fp64 accumulation before the rounding) and the grouped MFMA
 path's ~1e-4 error set the bar of the grouped path (T > 8): normwise max-relative 5e-4 (its
-own bar), under BASELINE's 1e-3.  The decode path (T <= 8) rounds h exactly as the oracle
+own bar), under the 1e-3 bar of the matvec gate.  The decode path (T <= 8) rounds h exactly as the oracle
 does and accumulates in fp32: 1e-5.  The router result is compared exactly (ids) and to 1e-5 (weights).
 """
 from __future__ import annotations
