@@ -27,8 +27,8 @@ mla_decode sub-objects).
 
 Synthetic, seeded data; weights are random-init with the benchmark shapes.  Steps are
 captured once into a HIP graph and replayed, so the timed region is GPU work plus the
-graph's launch gaps, without Python launch overhead.  `--gpus N` with N > 1 exits: the
-single-GPU build has no multi-GPU path.
+graph's launch gaps, without Python launch overhead.  `--gpus N` with N > 1 exits: k3hip
+has no multi-GPU path.
 """
 from __future__ import annotations
 
@@ -605,7 +605,7 @@ def main():
     global EAGER
     EAGER = args.eager
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
-        print("bench.py: this build runs on one GPU only (no multi-GPU path); use --gpus 1",
+        print("bench.py: k3hip runs on one GPU only (no multi-GPU path); use --gpus 1",
               file=sys.stderr)
         sys.exit(2)
 
