@@ -66,12 +66,6 @@ int k3_scale_minmax(const void *scales, int64_t n, int32_t *minmax, void *stream
 int k3_mxfp4_matvec(const void *x, int x_dtype, const void *packed, const void *scales,
                     void *out, int out_dtype, int64_t M, int64_t N, int64_t K, void *stream);
 
-/* Same as k3_mxfp4_matvec with an explicit launch shape (rows per wave 1/2/4/8, groups of
- * 32 per lane per sweep 1/2/4); used by launch-shape sweeps.  No reference counterpart. */
-int k3_mxfp4_matvec_cfg(const void *x, int x_dtype, const void *packed, const void *scales,
-                        void *out, int out_dtype, int64_t M, int64_t N, int64_t K,
-                        int rows_per_wave, int groups_per_lane, void *stream);
-
 /* ---- MoE expert FFN ---------------------------------------------------------------- */
 
 /* Workspace bytes k3_expert_ffn needs for intermediate size I (the fp32 act vector passed
@@ -118,6 +112,19 @@ int k3_moe_route(const void *x, int x_dtype, const void *router_w, const void *r
                  int route_kind, int renormalize, float scaling, int64_t H, int64_t n_experts,
                  int64_t top_k, void *workspace, int64_t workspace_bytes, void *stream);
 
+/* Selection half of the router for T tokens at once, from router logits computed by the
+ * caller (fp32 [T, E], row stride ld_logits; the prefill path takes them from one GEMM over
+ * all tokens): per token, scores = softmax or sigmoid of the logits, selection on scores
+ * (+ router_bias for K3_ROUTE_SIGMOID_BIAS), exact top-k with ties to the lower expert index,
+ * weights gathered from the raw scores, divided by (sum + 1e-20) when renormalize and
+ * top_k > 1, times scaling.  Outputs: expert_idx int32 [T, top_k] (largest first),
+ * expert_w f32 [T, top_k], scores and corrected f32 [T, E].  One block per token.
+ * Replaces the per-token selection of LatentMoE.route (air_llm/models/kimi_k3/moe.py:67-76;
+ * k3ref/layers.py:214-224), whose logits are one matmul over the flattened tokens. */
+int k3_moe_topk(const float *logits, int64_t ld_logits, int64_t T, int64_t n_experts,
+                const float *router_bias, int route_kind, int renormalize, float scaling, int64_t top_k,
+                int32_t *expert_idx, float *expert_w, float *scores, float *corrected, void *stream);
+
 /* Whole routed MoE layer for one token: route (as k3_moe_route), then
  *   out[H] = shared(x) + sum_j w_j * expert_{idx_j}(x)
  * with no device-to-host synchronisation.  expert_table is a device array of
@@ -144,12 +151,13 @@ int k3_moe_layer_decode(const void *x, int x_dtype, const void *router_w, const 
 int64_t k3_moe_grouped_workspace_size(int64_t T, int64_t top_k, int64_t n_experts, int64_t H, int64_t I);
 
 /* y[t] = sum_j w[t, j] * expert_{idx[t, j]}(x[t]) for T tokens at once:
- *   x bf16 [T, H]; expert_idx int32 [T, top_k] (every id in 0..n_experts-1); expert_w f32
+ *   x [T, H] bf16 or fp32 (x_dtype); expert_idx int32 [T, top_k] (every id in 0..n_experts-1); expert_w f32
  *   [T, top_k]; expert_table as in k3_moe_layer_decode (packed pointers 16-byte aligned,
  *   scale pointers 2-byte aligned, E8M0 bytes 2..252); out [T, H] f32 or bf16.
  * The (token, slot) pairs are grouped by expert on the device and each expert runs as a
  * GEMM with M = its token count on native MXFP4 MFMA (v_mfma_scale_f32_16x16x128_f8f6f4:
- * the weights as stored, x as two E4M3 terms, the activation as three, all with E8M0
+ * the weights as stored, bf16 x as two E4M3 terms (exact), fp32 x and the activation as
+ * three (about 12 bits), all with E8M0
  * scales per 32), so each expert's weights are read once per 64-token tile.  Normwise error
  * about 1e-4 of fp64 (the MFMA's own accumulation).  Deterministic.  H and I must be
  * multiples of 64.
@@ -166,9 +174,11 @@ int k3_moe_grouped_ffn(const void *x, int x_dtype, const int32_t *expert_idx, co
 int64_t k3_moe_latent_layer_workspace_size(int64_t H, int64_t latent, int64_t I, int64_t shared_I,
                                            int64_t n_experts, int64_t top_k);
 
-/* K3's routed layer with its latent wrapper for one token (bf16 x [H]):
+/* K3's routed layer with its latent wrapper for one token (x [H], bf16 or fp32 by x_dtype):
  *   route (sigmoid + bias, as k3_moe_route) on x;
- *   h = bf16(latent_down . x)                         latent_down bf16 [latent, H]
+ *   h = latent_down . x                               latent_down bf16 [latent, H]; h is rounded
+ *                                                     to bf16 for a bf16 x (the reference's bf16
+ *                                                     matmul) and stays fp32 for an fp32 x
  *   y = sum_j w_j * expert_{idx_j}(h)                 experts of width latent (expert_table)
  *   out = latent_up . (latent_norm * y / sqrt(mean(y^2) + eps)) + shared(x)
  * latent_up bf16 [H, latent], latent_norm fp32 [latent]; shared_* as in k3_moe_layer_decode
@@ -177,7 +187,7 @@ int64_t k3_moe_latent_layer_workspace_size(int64_t H, int64_t latent, int64_t I,
  * top_k <= 16, n_experts <= 1024.
  * Replaces LatentMoE.__call__ (air_llm/models/kimi_k3/moe.py:110-132) at batch 1, including
  * the latent down/norm/up wrapper (moe.py:116,129-130). */
-int k3_moe_latent_layer_decode(const void *x, const void *router_w, const void *router_bias, int renormalize,
+int k3_moe_latent_layer_decode(const void *x, int x_dtype, const void *router_w, const void *router_bias, int renormalize,
                                float scaling, const void *expert_table, const void *latent_down,
                                const void *latent_up, const void *latent_norm, float eps,
                                const void *shared_gate, const void *shared_up, const void *shared_down,

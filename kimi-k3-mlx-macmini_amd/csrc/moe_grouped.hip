@@ -12,8 +12,9 @@
 //   plan     one block: exclusive scan of the counts (segment bases) and the list of
 //            64-row tiles (expert, first row) of every non-empty expert
 //   place    block e writes its pairs, in (token, slot) order, into perm[base_e ...]
-//   quant_x  x (bf16) -> two E4M3 terms, one E8M0 scale per 32 elements per term:
-//            x = 2^e1 t1 + 2^e2 t2, exact for every element within 2^13 of its block's max
+//   quant_x  x -> E4M3 terms, one E8M0 scale per 32 elements per term: bf16 x as two,
+//            x = 2^e1 t1 + 2^e2 t2, exact for every element within 2^13 of its block's max;
+//            fp32 x as three (about 12 bits, as act)
 //   gateup   block (tile, 128 intermediate indices): v_mfma_scale_f32_16x16x128_f8f6f4 with
 //            the expert's MXFP4 rows as the FP4 A operand and their E8M0 bytes as the A
 //            scales (no decode), the x terms as the FP8 B operand; act = f(gate, up) in
@@ -165,22 +166,34 @@ __device__ __forceinline__ float shfl_xor_f(float v, int m) { return __shfl_xor(
 
 // ------------------------------------------------------------------ quant_x
 struct QxArgs {
-    const uint16_t *x;    // [T, H] bf16
-    uint8_t *x8;          // [2][T][Hpad] E4M3 codes, MX-B order
-    uint8_t *xs;          // [2][T][Hpad / 32] E8M0
+    const void *x;        // [T, H] bf16 (two terms) or fp32 (three terms)
+    uint8_t *x8;          // [TERMS][T][Hpad] E4M3 codes, MX-B order
+    uint8_t *xs;          // [TERMS][T][Hpad / 32] E8M0
     int T, H, Hpad;
     uint32_t term, sterm; // bytes per term of x8 / xs
 };
 
 // One thread per 16-element half block; the two halves of a block are adjacent lanes.
+// bf16 x is the exact sum of its two terms; fp32 x keeps about 12 bits in three (as act).
+template <bool F32>
 __global__ __launch_bounds__(256) void quant_x_kernel(QxArgs a) {
+    constexpr int TERMS = F32 ? 3 : 2;
     const int halves = a.H >> 4;
     const int idx = blockIdx.x * 256 + threadIdx.x;
     const bool ok = idx < a.T * halves;
     const int t = ok ? idx / halves : 0, hh = ok ? idx % halves : 0;
     float v[16];
-    if (ok) {
-        const uint4 *src = reinterpret_cast<const uint4 *>(a.x + static_cast<int64_t>(t) * a.H + hh * 16);
+    if (ok && F32) {
+        const float4 *src = reinterpret_cast<const float4 *>(static_cast<const float *>(a.x) +
+                                                             static_cast<int64_t>(t) * a.H + hh * 16);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const float4 f = src[i];
+            v[4 * i] = f.x, v[4 * i + 1] = f.y, v[4 * i + 2] = f.z, v[4 * i + 3] = f.w;
+        }
+    } else if (ok) {
+        const uint4 *src = reinterpret_cast<const uint4 *>(static_cast<const uint16_t *>(a.x) +
+                                                           static_cast<int64_t>(t) * a.H + hh * 16);
         const uint4 u0 = src[0], u1 = src[1];
         const uint32_t w[8] = {u0.x, u0.y, u0.z, u0.w, u1.x, u1.y, u1.z, u1.w};
 #pragma unroll
@@ -195,7 +208,7 @@ __global__ __launch_bounds__(256) void quant_x_kernel(QxArgs a) {
     const uint32_t row8 = static_cast<uint32_t>(t) * a.Hpad + mxb_offset(hh >> 1, hh & 1);
     const uint32_t rows = static_cast<uint32_t>(t) * (a.Hpad >> 5) + (hh >> 1);
 #pragma unroll
-    for (int term = 0; term < 2; ++term) {
+    for (int term = 0; term < TERMS; ++term) {
         float amax = 0.f;
 #pragma unroll
         for (int i = 0; i < 16; ++i) amax = fmaxf(amax, fabsf(v[i]));
@@ -246,9 +259,9 @@ __device__ __forceinline__ f32x4 mfma_fp4_fp8(const uint4 &a, const uint4 &b0, c
 // [i0 + 32 w, +32): A tiles j = 0, 1 are their gate rows and j = 2, 3 their up rows, so the
 // activation of a (token, index) pair meets both products in one lane.
 // DOWN == true: wave w owns 64 output rows [n0 + 64 w, +64) of W_down, B = the act terms.
-template <bool DOWN>
+// TERMS: E4M3 terms of B (x: 2 for bf16, 3 for fp32; act: 3).
+template <bool DOWN, int TERMS>
 __global__ __launch_bounds__(kThreads, 1) void mx_gemm_kernel(MxArgs a) {
-    constexpr int TERMS = DOWN ? 3 : 2;
     // two LDS tiles of B: [buffer][ct][term][piece][column] 16-byte pieces, then
     // [buffer][ct][term][column][block pair] scale pairs
     extern __shared__ uint4 smem[];
@@ -335,9 +348,10 @@ __global__ __launch_bounds__(kThreads, 1) void mx_gemm_kernel(MxArgs a) {
         if (rr < rows) brow = DOWN ? pos0 + rr : a.perm[pos0 + rr] / a.top_k;
         bsoff = brow >= 0 ? static_cast<uint32_t>(brow) * (a.Kpad >> 5) + 2u * sg : kOobOffset;
     }
-    // gate/up stages x two super-steps ahead (gathered token rows); down, whose act terms
-    // were written just before and sit in cache, one step ahead, to stay in registers
-    constexpr int XD = DOWN ? 1 : 2;
+    // gate/up stages bf16 x's two terms two super-steps ahead (gathered token rows); down,
+    // whose act terms were written just before and sit in cache, and gate/up over fp32 x's
+    // three terms, one step ahead, to stay in registers
+    constexpr int XD = (DOWN || TERMS == 3) ? 1 : 2;
     uint4 XR[XD][4][TERMS];
     uint16_t XS[XD][TERMS];
     auto load_x = [&](int S, int xs) {
@@ -500,11 +514,14 @@ constexpr size_t mx_lds_bytes(int terms) {
 // Both GEMMs take more than the default 64 KB of dynamic LDS (gfx950 has 160 KB per CU).
 int mx_prepare() {
     static const hipError_t rc = [] {
-        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(&mx_gemm_kernel<false>),
+        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(&mx_gemm_kernel<false, 2>),
                                            hipFuncAttributeMaxDynamicSharedMemorySize,
                                            static_cast<int>(mx_lds_bytes(2)));
         if (e == hipSuccess)
-            e = hipFuncSetAttribute(reinterpret_cast<const void *>(&mx_gemm_kernel<true>),
+            e = hipFuncSetAttribute(reinterpret_cast<const void *>(&mx_gemm_kernel<false, 3>),
+                                    hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(mx_lds_bytes(3)));
+        if (e == hipSuccess)
+            e = hipFuncSetAttribute(reinterpret_cast<const void *>(&mx_gemm_kernel<true, 3>),
                                     hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(mx_lds_bytes(3)));
         return e;
     }();
@@ -567,8 +584,8 @@ GroupedWs grouped_ws_layout(int64_t T, int64_t k, int64_t E, int64_t H, int64_t 
     L.tile_e = o, o += up(static_cast<size_t>(L.max_tiles) * 4);
     L.tile_m0 = o, o += up(static_cast<size_t>(L.max_tiles) * 4);
     L.n_tiles = o, o += up(4);
-    L.x8 = o, o += up(static_cast<size_t>(2) * T * L.Hpad);
-    L.xs = o, o += up(static_cast<size_t>(2) * T * (L.Hpad / 32));
+    L.x8 = o, o += up(static_cast<size_t>(3) * T * L.Hpad);
+    L.xs = o, o += up(static_cast<size_t>(3) * T * (L.Hpad / 32));
     L.a8 = o, o += up(static_cast<size_t>(3) * P * L.Ipad);
     L.as = o, o += up(static_cast<size_t>(3) * P * (L.Ipad / 32));
     L.ypair = o, o += up(static_cast<size_t>(P) * H * 4);
@@ -592,7 +609,8 @@ extern "C" int k3_moe_grouped_ffn(const void *x, int x_dtype, const int32_t *exp
                                   void *workspace, int64_t workspace_bytes, void *stream) {
     if (!x || !expert_idx || !expert_w || !expert_table || !out || !workspace)
         return set_error(K3_ERR_NULL, "moe grouped: null pointer");
-    if (x_dtype != K3_BF16) return set_error(K3_ERR_DTYPE, "moe grouped: x must be bf16 (x_dtype %d)", x_dtype);
+    if (x_dtype != K3_BF16 && x_dtype != K3_F32)
+        return set_error(K3_ERR_DTYPE, "moe grouped: x must be bf16 or fp32 (x_dtype %d)", x_dtype);
     if (out_dtype != K3_F32 && out_dtype != K3_BF16) return set_error(K3_ERR_DTYPE, "moe grouped: out_dtype");
     if (act_kind != K3_ACT_SILU && act_kind != K3_ACT_SITU) return set_error(K3_ERR_SHAPE, "moe grouped: act_kind");
     if (T <= 0 || top_k <= 0 || top_k > 64 || n_experts <= 0 || n_experts > 1024)
@@ -603,7 +621,7 @@ extern "C" int k3_moe_grouped_ffn(const void *x, int x_dtype, const int32_t *exp
     const GroupedWs L = grouped_ws_layout(T, top_k, n_experts, H, I);
     const int64_t P = T * top_k;
     if (P >= (1ll << 30) || H * I / 2 >= (1ll << 31) || 3 * P * L.Ipad >= (1ll << 31) ||
-        2 * T * L.Hpad >= (1ll << 31))
+        3 * T * L.Hpad >= (1ll << 31))
         return set_error(K3_ERR_SHAPE, "moe grouped: problem too large");
     if (workspace_bytes < static_cast<int64_t>(L.total))
         return set_error(K3_ERR_WORKSPACE, "moe grouped: workspace %lld < %zu bytes", (long long)workspace_bytes,
@@ -631,7 +649,7 @@ extern "C" int k3_moe_grouped_ffn(const void *x, int x_dtype, const int32_t *exp
     if (rc) return rc;
 
     QxArgs qa{};
-    qa.x = static_cast<const uint16_t *>(x);
+    qa.x = x;
     qa.x8 = reinterpret_cast<uint8_t *>(ws + L.x8);
     qa.xs = reinterpret_cast<uint8_t *>(ws + L.xs);
     qa.T = static_cast<int>(T);
@@ -639,7 +657,11 @@ extern "C" int k3_moe_grouped_ffn(const void *x, int x_dtype, const int32_t *exp
     qa.Hpad = static_cast<int>(L.Hpad);
     qa.term = static_cast<uint32_t>(T * L.Hpad);
     qa.sterm = static_cast<uint32_t>(T * (L.Hpad / 32));
-    quant_x_kernel<<<dim3(static_cast<unsigned>(cdiv(T * (H / 16), 256))), 256, 0, st>>>(qa);
+    const bool xf32 = x_dtype == K3_F32;
+    if (xf32)
+        quant_x_kernel<true><<<dim3(static_cast<unsigned>(cdiv(T * (H / 16), 256))), 256, 0, st>>>(qa);
+    else
+        quant_x_kernel<false><<<dim3(static_cast<unsigned>(cdiv(T * (H / 16), 256))), 256, 0, st>>>(qa);
     rc = check_hip(hipGetLastError(), "moe grouped: x quantization launch");
     if (rc) return rc;
 
@@ -672,8 +694,11 @@ extern "C" int k3_moe_grouped_ffn(const void *x, int x_dtype, const int32_t *exp
     ma.K = static_cast<int>(H);
     ma.Kpad = static_cast<int>(L.Hpad);
     ma.N = static_cast<int>(I);
-    mx_gemm_kernel<false>
-        <<<dim3(static_cast<unsigned>(L.max_tiles * cdiv(I, 128))), kThreads, mx_lds_bytes(2), st>>>(ma);
+    const dim3 gu_grid(static_cast<unsigned>(L.max_tiles * cdiv(I, 128)));
+    if (xf32)
+        mx_gemm_kernel<false, 3><<<gu_grid, kThreads, mx_lds_bytes(3), st>>>(ma);
+    else
+        mx_gemm_kernel<false, 2><<<gu_grid, kThreads, mx_lds_bytes(2), st>>>(ma);
     rc = check_hip(hipGetLastError(), "moe grouped: gate/up launch");
     if (rc) return rc;
     // down: K = I, weight rows N = H, 256 output rows per block, B = the act terms
@@ -684,7 +709,7 @@ extern "C" int k3_moe_grouped_ffn(const void *x, int x_dtype, const int32_t *exp
     ma.K = static_cast<int>(I);
     ma.Kpad = static_cast<int>(L.Ipad);
     ma.N = static_cast<int>(H);
-    mx_gemm_kernel<true><<<dim3(static_cast<unsigned>(L.max_tiles * cdiv(H, 256))), kThreads, mx_lds_bytes(3), st>>>(ma);
+    mx_gemm_kernel<true, 3><<<dim3(static_cast<unsigned>(L.max_tiles * cdiv(H, 256))), kThreads, mx_lds_bytes(3), st>>>(ma);
     rc = check_hip(hipGetLastError(), "moe grouped: down launch");
     if (rc) return rc;
 

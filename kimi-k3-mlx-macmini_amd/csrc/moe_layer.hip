@@ -51,7 +51,7 @@ struct LayerWs {
     uint32_t *counter;   // [0] router blocks done (L1), [1 + r] blocks of L3 row range r
                          // done; every launch returns them to 0
     float *yrow;         // [k][Hr] per-slot down-row totals (L3)
-    uint16_t *h;         // [Hr] bf16 latent state (latent layer)
+    void *h;             // [Hr] latent state (latent layer): bf16 for a bf16 x, fp32 for an fp32 x
     float *ylat;         // [Hr] routed sum in latent space (latent layer)
 };
 
@@ -73,7 +73,7 @@ struct LayerArgs {
     int l2_shared_blocks;          // L2: blocks [0, l2_shared_blocks) do shared down rows
     // K3's latent wrapper (moe.py:116,129-130); lat_down == null: the plain layer
     int Hr;                        // width the routed experts read and write (H, or the latent width)
-    const uint16_t *lat_down;      // [Hr, H] bf16: h = x W_down^T, rounded to bf16
+    const uint16_t *lat_down;      // [Hr, H] bf16: h = x W_down^T (bf16 for a bf16 x, as the reference)
     const uint16_t *lat_up;        // [H, Hr] bf16
     const float *lat_norm;         // [Hr] KimiRMSNorm weight
     float eps;
@@ -323,6 +323,21 @@ __device__ void route_block(const LayerArgs &a) {
     }
 }
 
+// ------------------------------------------------------------------ batched selection
+// One block per token: route_block on router logits computed elsewhere (the prefill path
+// takes them from a GEMM over all tokens), with the token's records at its row of each
+// output array.  No pointer table: a.table is null.
+__global__ __launch_bounds__(256) void topk_kernel(LayerArgs a, int64_t ld_logits) {
+    const int64_t t = blockIdx.x;
+    LayerArgs b = a;
+    b.ws.logits = a.ws.logits + t * ld_logits;
+    b.ws.scores = a.ws.scores + t * a.E;
+    b.ws.corrected = a.ws.corrected + t * a.E;
+    b.ws.topk_idx = a.ws.topk_idx + t * a.k;
+    b.ws.topk_w = a.ws.topk_w + t * a.k;
+    route_block(b);
+}
+
 // ------------------------------------------------------------------ L1
 // CHH: bf16 chunks (8 elements) per lane over H.
 template <typename XT, int CHH>
@@ -373,7 +388,8 @@ __global__ __launch_bounds__(256) void layer_l1(LayerArgs a) {
         __syncthreads();
         if (last_s) route_block(a);
     } else if (static_cast<int>(blockIdx.x) < a.l1_router_blocks + a.l1_latent_blocks) {
-        // latent down rows: h[l] = bf16(W_down[l] . x), the reference's bf16 matmul
+        // latent down rows: h[l] = W_down[l] . x, rounded to bf16 for a bf16 x (the reference's
+        // bf16 matmul) and kept in fp32 for an fp32 x (its bf16 x fp32 promotion)
         const int l = (blockIdx.x - a.l1_router_blocks) * 4 + wave;
         const auto r = make_rsrc(a.lat_down, static_cast<uint32_t>(a.Hr) * row_bytes);
         uint4 w[CHH];
@@ -396,7 +412,12 @@ __global__ __launch_bounds__(256) void layer_l1(LayerArgs a) {
             }
         }
         const float tot = wave_sum_to_lane63(acc0 + acc1);
-        if (lane == 63 && l < a.Hr) a.ws.h[l] = f32_to_bf16(tot);
+        if (lane == 63 && l < a.Hr) {
+            if constexpr (sizeof(XT) == 2)
+                static_cast<uint16_t *>(a.ws.h)[l] = f32_to_bf16(tot);
+            else
+                static_cast<float *>(a.ws.h)[l] = tot;
+        }
     } else {
         // ~0.2 us head start for the router rows' loads (issued by the first blocks): the
         // router blocks then finish early and the routing block runs under this stream
@@ -474,7 +495,7 @@ __global__ __launch_bounds__(256) void layer_l2(LayerArgs a) {
         return;
     }
     // routed gate/up: kRoutedPairs (slot j, row i) pairs per wave, over the routed input
-    // (x, or the bf16 latent state h, which the host pairs with XT = bf16)
+    // (x, or the latent state h, which has x's dtype)
     constexpr int CPGX = XTile<XT>::kChunks;
     constexpr int XREG = x_regs<XT>();
     const int GH = a.Hr >> 5;
@@ -669,7 +690,7 @@ static LayerWsLayout layer_ws_layout(int64_t H, int64_t I, int64_t Is, int64_t E
     L.act = o, o += up256(k * I * 4);
     L.yshared = o, o += up256(H * 4);
     L.ptrs = o, o += up256(k * 6 * 8);
-    L.h = o, o += up256(Hr * 2);
+    L.h = o, o += up256(Hr * 4);
     L.ylat = o, o += up256(Hr * 4);
     L.yrow = o, o += up256(k * std::max(H, Hr) * 4);
     L.total = o;
@@ -769,7 +790,6 @@ static int layer_impl(const void *x, int x_dtype, const void *router_w, const vo
     const bool lat = lat_down != nullptr;
     if (lat) {
         if (!lat_up || !lat_norm) return set_error(K3_ERR_NULL, "moe latent layer: null pointer");
-        if (x_dtype != K3_BF16) return set_error(K3_ERR_DTYPE, "moe latent layer: x must be bf16");
         if (latent <= 0 || latent % 128 || latent > 8192)
             return set_error(K3_ERR_SHAPE, "moe latent layer: latent=%lld must be a positive multiple of 128, <= 8192",
                              (long long)latent);
@@ -828,7 +848,7 @@ static int layer_impl(const void *x, int x_dtype, const void *router_w, const vo
         a.lat_up = static_cast<const uint16_t *>(lat_up);
         a.lat_norm = static_cast<const float *>(lat_norm);
         a.eps = eps;
-        a.ws.h = reinterpret_cast<uint16_t *>(w + L.h);
+        a.ws.h = w + L.h;
         a.ws.ylat = reinterpret_cast<float *>(w + L.ylat);
     }
     a.I = static_cast<int>(I);
@@ -864,7 +884,7 @@ extern "C" int64_t k3_moe_latent_layer_workspace_size(int64_t H, int64_t latent,
     return static_cast<int64_t>(layer_ws_layout(H, I, shared_I, n_experts, top_k, latent).total);
 }
 
-extern "C" int k3_moe_latent_layer_decode(const void *x, const void *router_w, const void *router_bias,
+extern "C" int k3_moe_latent_layer_decode(const void *x, int x_dtype, const void *router_w, const void *router_bias,
                                           int renormalize, float scaling, const void *expert_table,
                                           const void *latent_down, const void *latent_up, const void *latent_norm,
                                           float eps, const void *shared_gate, const void *shared_up,
@@ -873,7 +893,7 @@ extern "C" int k3_moe_latent_layer_decode(const void *x, const void *router_w, c
                                           int64_t top_k, int act_kind, float beta, float linear_beta,
                                           void *workspace, int64_t workspace_bytes, void *stream) {
     if (!latent_down) return set_error(K3_ERR_NULL, "moe latent layer: null pointer");
-    return layer_impl(x, K3_BF16, router_w, router_bias, K3_ROUTE_SIGMOID_BIAS, renormalize, scaling, expert_table,
+    return layer_impl(x, x_dtype, router_w, router_bias, K3_ROUTE_SIGMOID_BIAS, renormalize, scaling, expert_table,
                       shared_gate, shared_up, shared_down, out, out_dtype, H, I, shared_I, n_experts, top_k, act_kind,
                       beta, linear_beta, workspace, workspace_bytes, stream, false, latent_down, latent_up,
                       latent_norm, eps, latent);
@@ -885,6 +905,36 @@ extern "C" int k3_moe_route(const void *x, int x_dtype, const void *router_w, co
     return layer_impl(x, x_dtype, router_w, router_bias, route_kind, renormalize, scaling, nullptr, nullptr, nullptr,
                       nullptr, nullptr, K3_F32, H, 128, 0, n_experts, top_k, K3_ACT_SILU, 1.f, 0.f, workspace,
                       workspace_bytes, stream, true);
+}
+
+extern "C" int k3_moe_topk(const float *logits, int64_t ld_logits, int64_t T, int64_t n_experts,
+                           const float *router_bias, int route_kind, int renormalize, float scaling, int64_t top_k,
+                           int32_t *expert_idx, float *expert_w, float *scores, float *corrected, void *stream) {
+    if (T < 0) return set_error(K3_ERR_SHAPE, "moe topk: T=%lld", (long long)T);
+    if (route_kind != K3_ROUTE_SOFTMAX && route_kind != K3_ROUTE_SIGMOID_BIAS)
+        return set_error(K3_ERR_SHAPE, "moe topk: route_kind");
+    if (n_experts <= 0 || n_experts > kMaxExperts || top_k <= 0 || top_k > kMaxTopK || top_k > n_experts)
+        return set_error(K3_ERR_SHAPE, "moe topk: n_experts must be in 1..%d and top_k in 1..min(%d, n_experts)",
+                         kMaxExperts, kMaxTopK);
+    if (ld_logits < n_experts) return set_error(K3_ERR_SHAPE, "moe topk: ld_logits < n_experts");
+    if (T == 0) return K3_OK;
+    if (!logits || !expert_idx || !expert_w || !scores || !corrected)
+        return set_error(K3_ERR_NULL, "moe topk: null pointer");
+    if (T > (1ll << 31) - 1) return set_error(K3_ERR_SHAPE, "moe topk: T too large");
+    LayerArgs a{};
+    a.router_bias = router_bias;
+    a.E = static_cast<int>(n_experts);
+    a.k = static_cast<int>(top_k);
+    a.route_kind = route_kind;
+    a.renorm = renormalize;
+    a.scaling = scaling;
+    a.ws.logits = const_cast<float *>(logits);
+    a.ws.scores = scores;
+    a.ws.corrected = corrected;
+    a.ws.topk_idx = expert_idx;
+    a.ws.topk_w = expert_w;
+    topk_kernel<<<dim3(static_cast<unsigned>(T)), 256, 0, static_cast<hipStream_t>(stream)>>>(a, ld_logits);
+    return check_hip(hipGetLastError(), "moe topk launch");
 }
 
 extern "C" int k3_moe_layer_workspace_offsets(int64_t H, int64_t I, int64_t shared_I, int64_t n_experts,

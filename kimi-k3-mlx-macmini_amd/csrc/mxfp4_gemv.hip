@@ -254,12 +254,12 @@ int gemv_validate(const void *x, int x_dtype, const void *packed, const void *sc
 using namespace k3;
 
 static int matvec_impl(const void *x, int x_dtype, const void *packed, const void *scales, void *out,
-                       int out_dtype, int64_t M, int64_t N, int64_t K, int rpw, int gpl,
-                       void *stream) {
+                       int out_dtype, int64_t M, int64_t N, int64_t K, void *stream) {
     int rc = gemv_validate(x, x_dtype, packed, scales, out, out_dtype, M, N, K);
     if (rc) return rc;
     if (M == 0 || N == 0) return K3_OK;
-    if (rpw <= 0 || gpl <= 0) gemv_default_cfg(N, K, &rpw, &gpl);
+    int rpw, gpl;
+    gemv_default_cfg(N, K, &rpw, &gpl);
     if (M > 1 && rpw == 8) rpw = 4;
     const size_t xsz = x_dtype == K3_BF16 ? 2 : 4;
     const size_t osz = out_dtype == K3_BF16 ? 2 : 4;
@@ -290,13 +290,5 @@ static int matvec_impl(const void *x, int x_dtype, const void *packed, const voi
 extern "C" int k3_mxfp4_matvec(const void *x, int x_dtype, const void *packed, const void *scales,
                                void *out, int out_dtype, int64_t M, int64_t N, int64_t K,
                                void *stream) {
-    return matvec_impl(x, x_dtype, packed, scales, out, out_dtype, M, N, K, 0, 0, stream);
-}
-
-extern "C" int k3_mxfp4_matvec_cfg(const void *x, int x_dtype, const void *packed,
-                                   const void *scales, void *out, int out_dtype, int64_t M,
-                                   int64_t N, int64_t K, int rows_per_wave, int groups_per_lane,
-                                   void *stream) {
-    return matvec_impl(x, x_dtype, packed, scales, out, out_dtype, M, N, K, rows_per_wave,
-                       groups_per_lane, stream);
+    return matvec_impl(x, x_dtype, packed, scales, out, out_dtype, M, N, K, stream);
 }

@@ -33,17 +33,17 @@ SIGNATURES: dict[str, list] = {
     "k3_mxfp4_decode": [_P, _P, _P, _I32, _I64, _I64, _P],
     "k3_scale_minmax": [_P, _I64, _P, _P],
     "k3_mxfp4_matvec": [_P, _I32, _P, _P, _P, _I32, _I64, _I64, _I64, _P],
-    "k3_mxfp4_matvec_cfg": [_P, _I32, _P, _P, _P, _I32, _I64, _I64, _I64, _I32, _I32, _P],
     "k3_expert_ffn_workspace_size": [_I64],
     "k3_expert_ffn": [_P, _I32, _P, _P, _P, _P, _P, _P, _P, _I32, _I64, _I64, _I32, _F32, _F32,
                       _P, _I64, _P],
     "k3_moe_layer_workspace_size": [_I64, _I64, _I64, _I64, _I64],
     "k3_moe_layer_workspace_offsets": [_I64, _I64, _I64, _I64, _I64, _P],
     "k3_moe_route": [_P, _I32, _P, _P, _I32, _I32, _F32, _I64, _I64, _I64, _P, _I64, _P],
+    "k3_moe_topk": [_P, _I64, _I64, _I64, _P, _I32, _I32, _F32, _I64, _P, _P, _P, _P, _P],
     "k3_moe_layer_decode": [_P, _I32, _P, _P, _I32, _I32, _F32, _P, _P, _P, _P, _P, _I32, _I64, _I64,
                             _I64, _I64, _I64, _I32, _F32, _F32, _P, _I64, _P],
     "k3_moe_latent_layer_workspace_size": [_I64, _I64, _I64, _I64, _I64, _I64],
-    "k3_moe_latent_layer_decode": [_P, _P, _P, _I32, _F32, _P, _P, _P, _P, _F32, _P, _P, _P, _P, _I32, _I64, _I64,
+    "k3_moe_latent_layer_decode": [_P, _I32, _P, _P, _I32, _F32, _P, _P, _P, _P, _F32, _P, _P, _P, _P, _I32, _I64, _I64,
                                    _I64, _I64, _I64, _I64, _I32, _F32, _F32, _P, _I64, _P],
     "k3_mla_workspace_size": [_I64, _I64],
     "k3_mla_decode_absorbed": [_P, _P, _I64, _I64, _I32, _P, _P, _P, _I64, _P, _I64, _I64, _I64, _I64, _I64,

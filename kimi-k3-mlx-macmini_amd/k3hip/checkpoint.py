@@ -343,6 +343,7 @@ class TensorSource:
         from concurrent.futures import ThreadPoolExecutor
         if self._copy is None:
             self._copy = torch.cuda.Stream(self._dev())
+        buf.record_stream(self._copy)  # written on the copy stream: not reused before those copies end
         nr = self.READERS
         cap = max(sizes)
         stages = [torch.empty(cap, dtype=torch.uint8, pin_memory=True) for _ in range(nr)]
@@ -394,10 +395,12 @@ class TensorSource:
                                      dst[ra["nbytes"]:ra["nbytes"] + rb["nbytes"]].view(rb["shape"]))
                     if j + nr < len(names):
                         fut[j + nr] = pool.submit(read, j + nr)
+        finally:
+            # every issued copy has finished before the staging buffers are reused or the
+            # error propagates (buf is also marked as used on the copy stream)
             for ev in events:
                 if ev is not None:
                     ev.synchronize()
-        finally:
             for f in fds.values():
                 os.close(f)
 

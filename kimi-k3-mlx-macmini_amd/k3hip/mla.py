@@ -18,6 +18,12 @@ bf16 projection weights (the checkpoint dtype) the decode step (one token, batch
 gate and o_proj in six HIP launches.  With other weight dtypes the projections are torch
 fp32 matmuls around the HIP core.  Prefill (T > 1) keeps the reference's dense masked form
 in torch on the GPU.
+
+The cache defaults to bf16 (``cfg.mla_cache_dtype``), which the HIP core reads in place; the
+reference's default is an fp32 cache (``attention_mla.py:164``), which it calls lossless.
+An fp32 cache (``mla_cache_dtype=torch.float32``, or a caller's fp32 ``MLACache``) is
+accepted: every step on it, one token included, runs the fp32 masked form on the GPU (no
+HIP core), the exact-but-slower validation route.
 """
 from __future__ import annotations
 
@@ -193,8 +199,10 @@ class MLAAttention:
         self.g_w, self.o_w = w.get("g_proj.weight"), w["o_proj.weight"]
         nh, nope = cfg.num_attention_heads, cfg.qk_nope_head_dim
         kb = self.kv_b.to(torch.bfloat16).reshape(nh, nope + cfg.v_head_dim, cfg.kv_lora_rank)
-        self.wk = kb[:, :nope, :].contiguous()        # [H, nope, r]
+        self.wk = kb[:, :nope, :].contiguous()        # [H, nope, r], bf16 for the HIP core
         self.wv = kb[:, nope:, :].contiguous()        # [H, v, r]
+        kb32 = self.kv_b.to(torch.float32).reshape(nh, nope + cfg.v_head_dim, cfg.kv_lora_rank)
+        self._wk32, self._wv32 = kb32[:, :nope, :], kb32[:, nope:, :]   # the fp32 form uses kv_b as given
         self.cache_dtype = getattr(cfg, "mla_cache_dtype", torch.bfloat16)
         mats = [self.q_a, self.q_b, self.kv_a, self.o_w] + ([self.g_w] if self.g_w is not None else [])
         self.fused_step = (all(m.dtype == torch.bfloat16 and m.is_cuda for m in mats)
@@ -238,7 +246,7 @@ class MLAAttention:
         cache.append(c_new, r_new)
         lat, rot = cache.view()
         scale = qhd ** -0.5
-        if Tn == 1 and B == 1:
+        if Tn == 1 and B == 1 and lat.dtype == torch.bfloat16:
             o = mla_decode_absorbed(q[0, :, 0, :nope], q[0, :, 0, nope:], self.wk, self.wv,
                                     lat[0], rot[0], scale).reshape(1, 1, nh * vhd)
         else:
@@ -279,7 +287,7 @@ class MLAAttention:
         """Multi-token form (prefill): absorbed scores with the causal mask, fp32."""
         nope = self.cfg.qk_nope_head_dim
         latf, rotf = lat.to(torch.float32), rot.to(torch.float32)
-        qa = q[..., :nope] @ self.wk.to(torch.float32)               # [B, H, T, r]
+        qa = q[..., :nope] @ self._wk32                              # [B, H, T, r]
         s = (qa @ latf.unsqueeze(1).transpose(-1, -2).contiguous()
              + q[..., nope:] @ rotf.unsqueeze(1).transpose(-1, -2).contiguous())
         s = s * scale
@@ -289,4 +297,4 @@ class MLAAttention:
         s = s.masked_fill(ki > qi, float("-inf"))
         p = torch.softmax(s, dim=-1)
         ctx = p @ latf.unsqueeze(1)
-        return ctx @ self.wv.to(torch.float32).transpose(-1, -2).contiguous()
+        return ctx @ self._wv32.transpose(-1, -2).contiguous()

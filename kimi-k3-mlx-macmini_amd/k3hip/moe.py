@@ -58,7 +58,10 @@ def expert_ffn_fused(x: torch.Tensor, gate, up, down, act: str = "silu", beta: f
 from dataclasses import dataclass  # noqa: E402
 from typing import Callable  # noqa: E402
 
+from . import _blas  # noqa: E402
+
 ROUTES = {"softmax": _lib.K3_ROUTE_SOFTMAX, "sigmoid_bias": _lib.K3_ROUTE_SIGMOID_BIAS}
+_DENSE_DTYPES = (torch.bfloat16, torch.float32)
 
 
 @dataclass
@@ -87,38 +90,65 @@ class MoEConfig:
     situ_linear_beta: float | None = None
 
 
+def route_tokens(x: torch.Tensor, gate_w: torch.Tensor, bias: torch.Tensor | None, kind: int,
+                 renormalize: bool, scaling: float, top_k: int) -> RouterResult:
+    """Router + top-k for every token of x [..., H] (moe.py:65-76): the logits of all tokens
+    as one GEMM with exact products and fp32 accumulation (the reference's fp32 router), then
+    the selection for all tokens in one launch (k3_moe_topk)."""
+    flat = x.reshape(-1, x.shape[-1])
+    n, E = flat.shape[0], gate_w.shape[0]
+    dev = gate_w.device
+    idx = torch.empty((n, top_k), dtype=torch.int32, device=dev)
+    w = torch.empty((n, top_k), dtype=torch.float32, device=dev)
+    scores = torch.empty((n, E), dtype=torch.float32, device=dev)
+    corrected = torch.empty((n, E), dtype=torch.float32, device=dev)
+    if n:
+        logits = _blas.mm_f32(flat, gate_w).contiguous()
+        _lib.call("k3_moe_topk", T.ptr(logits), E, n, E, T.ptr(bias), kind, int(bool(renormalize)),
+                  float(scaling), top_k, T.ptr(idx), T.ptr(w), T.ptr(scores), T.ptr(corrected), T.stream(logits))
+    return RouterResult(idx.to(torch.int64), w, scores, corrected)
+
+
+def _dense(t: torch.Tensor | None, name: str) -> torch.Tensor | None:
+    if t is not None and t.dtype not in _DENSE_DTYPES:
+        raise TypeError(f"{name} must be bfloat16 (the checkpoint dtype) or float32 (validation mode); got {t.dtype}")
+    return t
+
+
 class RoutedMoE:
     """Drop-in for the routed path of LatentMoE (air_llm/models/kimi_k3/moe.py:40-132).
 
     ``RoutedMoE(cfg, layer, w, expert_source, fused=True)`` keeps the reference
-    constructor: ``w`` holds ``gate.weight`` (bf16 [E, H]), optionally
-    ``gate.e_score_correction_bias`` and ``shared_experts.{gate,up,down}_proj.weight``
-    (bf16); ``expert_source(layer, expert, which)`` returns ``(packed, scales)`` device
-    tensors for ``which`` in ``w1`` (gate), ``w3`` (up), ``w2`` (down).
+    constructor: ``w`` holds ``gate.weight`` ([E, H]), optionally
+    ``gate.e_score_correction_bias`` and ``shared_experts.{gate,up,down}_proj.weight``;
+    ``expert_source(layer, expert, which)`` returns ``(packed, scales)`` device tensors for
+    ``which`` in ``w1`` (gate), ``w3`` (up), ``w2`` (down).  Dense weights are bf16 (the
+    checkpoint dtype) or fp32 (the reference loader's validation mode, loader.py:90-95).
 
-    All experts are made resident once (the source is called E x 3 times at build) and
-    addressed through a device pointer table, so a decode step is three launches with no
-    host synchronisation; ``fused=False`` keeps the reference's unfused definition
-    (decode to bf16, BLAS matmul) for debugging, as ``moe.py:79-88`` does.
+    With ``fused=True`` and bf16 dense weights, every expert is made resident once (the
+    source is called E x 3 times at build) and addressed through a device pointer table, so
+    a decode step is three launches with no host synchronisation.  ``fused=False`` (or fp32
+    dense weights) runs the reference's own structure instead: ``route``, then a host loop
+    over the distinct routed experts with ``expert_forward`` built on ``_proj``, whose
+    unfused form is the HIP decode to bf16 followed by a BLAS matmul (moe.py:79-88), and the
+    shared expert with the reference's dtype promotion.
     """
 
     def __init__(self, cfg, layer: int, w: dict, expert_source: Callable, fused: bool = True):
         self.cfg, self.L = cfg, layer
         self.src = expert_source
         self.fused = fused
-        self.gate_w = w["gate.weight"]
+        self.gate_w = _dense(w["gate.weight"], "gate.weight")
         self.gate_b = w.get("gate.e_score_correction_bias")
-        self.sh_gate = w.get("shared_experts.gate_proj.weight")
-        self.sh_up = w.get("shared_experts.up_proj.weight")
-        self.sh_down = w.get("shared_experts.down_proj.weight")
+        self.sh_gate = _dense(w.get("shared_experts.gate_proj.weight"), "shared_experts.gate_proj.weight")
+        self.sh_up = _dense(w.get("shared_experts.up_proj.weight"), "shared_experts.up_proj.weight")
+        self.sh_down = _dense(w.get("shared_experts.down_proj.weight"), "shared_experts.down_proj.weight")
         self.device = self.gate_w.device
-        if self.gate_w.dtype != torch.bfloat16:
-            raise TypeError("gate.weight must be bfloat16")
         if self.gate_b is not None:
             self.gate_b = self.gate_b.to(torch.float32).contiguous()
-        for t in (self.sh_gate, self.sh_up, self.sh_down):
-            if t is not None and t.dtype != torch.bfloat16:
-                raise TypeError("shared expert weights must be bfloat16")
+        dense = [self.gate_w] + [t for t in (self.sh_gate, self.sh_up, self.sh_down) if t is not None]
+        # the fused decode kernels read bf16 router / shared rows
+        self._fast = fused and all(t.dtype == torch.bfloat16 for t in dense)
         self._table = None
         self._keep = []
 
@@ -198,49 +228,69 @@ class RoutedMoE:
 
     # ------------------------------------------------------------------ API
     def route(self, x: torch.Tensor) -> RouterResult:
-        """Router + top-k for each token of x [..., H] (moe.py:65-76)."""
-        flat = x.reshape(-1, x.shape[-1])
+        """Router + top-k for each token of x [..., H] (moe.py:65-76), on x as given."""
         kind, bias = self._route_args()
-        results = []
-        for t in range(flat.shape[0]):
-            xt = self._x1(flat[t])
-            ws = self._workspace()
-            _lib.call("k3_moe_route", T.ptr(xt), T.dtype_code(xt.dtype), T.ptr(self.gate_w), T.ptr(bias), kind,
-                      int(bool(self.cfg.moe_renormalize)), float(self.cfg.routed_scaling_factor), self._H,
-                      self._E, self._k, T.ptr(ws), ws.numel(), T.stream(xt))
-            results.append(self._records(ws))
-        return RouterResult(*(torch.cat([getattr(r, f) for r in results]) for f in
-                              ("expert_indices", "expert_weights", "raw_scores", "corrected_scores")))
+        return route_tokens(x, self.gate_w, bias, kind, bool(self.cfg.moe_renormalize),
+                            float(self.cfg.routed_scaling_factor), self._k)
+
+    def _proj(self, h: torch.Tensor, e: int, which: str) -> torch.Tensor:
+        """h @ W.T for one MXFP4 projection of expert e (moe.py:79-88): fused, the MXFP4
+        matvec (weights decoded in registers, fp32 out); unfused, the HIP decode to bf16
+        then a BLAS matmul in h's dtype, as the reference's ``h @ decode(...).T.astype(h.dtype)``."""
+        p, s = self.src(self.L, e, which)
+        if h.dtype not in (torch.float32, torch.bfloat16):
+            h = h.to(torch.float32)
+        if self.fused:
+            from .mxfp4_matvec import mxfp4_matvec_fused
+            return mxfp4_matvec_fused(h, p, s)
+        from .mxfp4 import decode_mxfp4
+        return h @ decode_mxfp4(p, s, out_dtype=torch.bfloat16).t().to(h.dtype)
 
     def expert_forward(self, h: torch.Tensor, e: int) -> torch.Tensor:
-        """One routed expert on h [N, H] (moe.py:90-103)."""
-        gate, up, down = (self.src(self.L, e, w) for w in ("w1", "w3", "w2"))
+        """One routed expert on h [N, H] (moe.py:90-103): gate and up projections, the
+        activation in fp32, the down projection.  One fused token runs the two-launch expert
+        kernel; otherwise the three projections go through ``_proj``."""
         act, beta, lb = self._act()
-        if not self.fused:
-            from .mxfp4 import decode_mxfp4
-            ws = [decode_mxfp4(p, s, out_dtype=torch.bfloat16) for p, s in (gate, up, down)]
-            hf = h.to(torch.float32)
-            g, u = hf @ ws[0].float().T, hf @ ws[1].float().T
-            return _act_torch(g, u, act, beta, lb) @ ws[2].float().T
-        return torch.cat([expert_ffn_fused(h[t:t + 1], gate, up, down, act, beta, lb)
-                          for t in range(h.shape[0])])
+        if self.fused and h.shape[0] == 1:
+            gate, up, down = (self.src(self.L, e, w) for w in ("w1", "w3", "w2"))
+            return expert_ffn_fused(h, gate, up, down, act, beta, lb)
+        g = self._proj(h, e, "w1")
+        u = self._proj(h, e, "w3")
+        return self._proj(_act_torch(g.float(), u.float(), act, beta, lb), e, "w2")
 
     def shared_forward(self, x: torch.Tensor) -> torch.Tensor:
-        """Shared expert on the original hidden (moe.py:105-107), via the bf16 path of the
-        unfused definition; inside a decode step it runs fused in the layer kernels."""
+        """Shared expert on the original hidden state (moe.py:105-107).  Fused: exact
+        products with fp32 accumulation and fp32 intermediates on the BLAS library, no weight
+        copy (inside a decode step it runs in the layer kernels).  Unfused: the reference's
+        dtype promotion (a bf16 input against bf16 weights gives bf16 gate / up)."""
         act, beta, lb = self._act()
-        xf = x.to(torch.float32)
-        g = xf @ self.sh_gate.float().T
-        u = xf @ self.sh_up.float().T
-        return _act_torch(g, u, act, beta, lb) @ self.sh_down.float().T
+        mm = _blas.mm_f32 if self.fused else _blas.mm_ref
+        g = mm(x, self.sh_gate)
+        u = mm(x, self.sh_up)
+        return mm(_act_torch(g.float(), u.float(), act, beta, lb), self.sh_down).float()
+
+    def _combine_loop(self, h: torch.Tensor, r: RouterResult, width: int) -> torch.Tensor:
+        """The reference's dispatch loop (moe.py:119-127): for each distinct routed expert,
+        gather its tokens, run expert_forward, scale by the gate weight, scatter-add."""
+        n = h.shape[0]
+        y = torch.zeros((n, width), dtype=torch.float32, device=h.device)
+        idx = r.expert_indices.tolist()   # drives host control flow, as np_indices does
+        for e in sorted({v for row in idx for v in row}):
+            tok = [t for t, row in enumerate(idx) if e in row]
+            slot = [idx[t].index(e) for t in tok]
+            ti = torch.tensor(tok, device=h.device)
+            out = self.expert_forward(h[ti], e).float()
+            wts = r.expert_weights[ti, torch.tensor(slot, device=h.device)].reshape(-1, 1)
+            y.index_add_(0, ti, out * wts)
+        return y
 
     def grouped_forward(self, x: torch.Tensor, router: RouterResult | None = None,
                         out_dtype=torch.float32) -> torch.Tensor:
-        """Prefill form of __call__ for x [..., H] bf16: route every token (or take the given
-        RouterResult), then run the routed experts grouped by expert (moe_grouped_ffn); the
-        shared expert, if any, is a dense bf16 FFN through the BLAS library in fp32."""
+        """Prefill form of __call__ for x [..., H]: route every token on x as given (or take
+        the given RouterResult), then run the routed experts grouped by expert on the device
+        (moe_grouped_ffn); the shared expert, if any, runs on the BLAS library."""
         orig = x.shape
-        flat = x.reshape(-1, orig[-1]).to(torch.bfloat16)
+        flat = x.reshape(-1, orig[-1])
         if router is None:
             router = self.route(flat)
         act, beta, lb = self._act()
@@ -253,6 +303,13 @@ class RoutedMoE:
     def __call__(self, x: torch.Tensor, return_router: bool = False, out_dtype=torch.float32):
         orig = x.shape
         flat = x.reshape(-1, orig[-1])
+        if not self._fast:
+            r = self.route(flat)
+            y = self._combine_loop(flat, r, self._H)
+            if self.sh_gate is not None:
+                y = y + self.shared_forward(flat)
+            y = y.to(out_dtype).reshape(*orig[:-1], self._H)
+            return (y, r) if return_router else y
         kind, bias = self._route_args()
         act, beta, lb = self._act()
         table = self.expert_table()
@@ -277,26 +334,37 @@ class RoutedMoE:
         return y, r
 
 
+def _rmsnorm32(y: torch.Tensor, w32: torch.Tensor, eps: float) -> torch.Tensor:
+    """KimiRMSNorm in fp32 (ops.py:11-14)."""
+    y = y.float()
+    return w32 * (y * torch.rsqrt((y * y).mean(dim=-1, keepdim=True) + eps))
+
+
 class LatentMoE:
     """Drop-in for K3's routed layer, LatentMoE (air_llm/models/kimi_k3/moe.py:40-132).
 
     ``LatentMoE(cfg, layer, w, expert_source, fused=True)`` keeps the reference constructor
     and weight names: ``gate.weight`` [E, H] and ``gate.e_score_correction_bias`` [E]
     (sigmoid + bias routing), ``routed_expert_down_proj.weight`` [L, H] and
-    ``routed_expert_up_proj.weight`` [H, L] (the latent projections, bf16),
-    ``routed_expert_norm.weight`` [L], ``shared_experts.{gate,up,down}_proj.weight`` (bf16;
-    K3's two shared experts are one MLP of twice the width).  ``expert_source(layer, e, which)``
+    ``routed_expert_up_proj.weight`` [H, L] (the latent projections),
+    ``routed_expert_norm.weight`` [L], ``shared_experts.{gate,up,down}_proj.weight`` (K3's two
+    shared experts are one MLP of twice the width).  Dense weights are bf16 (the checkpoint
+    dtype) or fp32 (validation mode, loader.py:90-95).  ``expert_source(layer, e, which)``
     returns latent-width MXFP4 experts (gate/up [I, L], down [L, I]).  cfg carries the
     K3Config fields hidden_size, routed_expert_hidden_size, moe_intermediate_size,
     num_experts, num_experts_per_token, moe_renormalize, routed_scaling_factor, situ_beta,
     situ_linear_beta and rms_norm_eps.
 
-    ``__call__(x)`` (moe.py:110-132): route on x; h = x W_down^T in bf16 (the reference's
-    dtype); the routed experts (SiTU) on h; KimiRMSNorm of their weighted sum in fp32; the up
-    projection in fp32; plus the shared expert on the original x.  Up to DECODE_TOKENS
-    tokens run one by one through k3_moe_latent_layer_decode (four launches per token);
-    more tokens run the routed experts grouped by expert (k3_moe_grouped_ffn).  Neither
-    path synchronises with the host."""
+    ``__call__(x)`` (moe.py:110-132): route on x; h = x W_down^T (bf16 for a bf16 x, as the
+    reference's bf16 matmul gives; fp32 for an fp32 x); the routed experts (SiTU) on h;
+    KimiRMSNorm of their weighted sum in fp32; the up projection in fp32; plus the shared
+    expert on the original x.  With ``fused=True`` and bf16 dense weights, up to
+    DECODE_TOKENS tokens run one by one through k3_moe_latent_layer_decode (four launches
+    per token) and more tokens run the routed experts grouped by expert
+    (k3_moe_grouped_ffn); neither synchronises with the host.  ``fused=False`` or fp32 dense
+    weights run the reference's structure (``RoutedMoE`` describes it)."""
+
+    DECODE_TOKENS = 8  # up to this many tokens: one fused decode per token; more: grouped
 
     def __init__(self, cfg, layer: int, w: dict, expert_source: Callable, fused: bool = True):
         self.cfg, self.L = cfg, layer
@@ -314,21 +382,25 @@ class LatentMoE:
         self._routed = RoutedMoE(rcfg, layer, {"gate.weight": w["gate.weight"],
                                                "gate.e_score_correction_bias": w["gate.e_score_correction_bias"],
                                                **shared}, expert_source, fused)
-        self.down = w["routed_expert_down_proj.weight"]
-        self.up = w["routed_expert_up_proj.weight"]
+        self.src = expert_source
+        self.down = _dense(w["routed_expert_down_proj.weight"], "routed_expert_down_proj.weight")
+        self.up = _dense(w["routed_expert_up_proj.weight"], "routed_expert_up_proj.weight")
         self.norm_w = w["routed_expert_norm.weight"]
         if tuple(self.down.shape) != (self.latent, H) or tuple(self.up.shape) != (H, self.latent):
             raise ValueError(f"latent projections must be [{self.latent}, {H}] and [{H}, {self.latent}]; got "
                              f"{tuple(self.down.shape)}, {tuple(self.up.shape)}")
-        if self.down.dtype != torch.bfloat16 or self.up.dtype != torch.bfloat16:
-            raise TypeError("latent projections must be bfloat16")
         T.require_device(self.down, self.up, self.norm_w)
-        self._up32 = self.up.float()      # the reference applies W_up to the fp32 normalised sum
-        self._norm32 = self.norm_w.float()
+        self._norm32 = self.norm_w.float().contiguous()
+        self._fast = (self._routed._fast and self.down.dtype == torch.bfloat16
+                      and self.up.dtype == torch.bfloat16)
 
     def route(self, x: torch.Tensor) -> RouterResult:
         """Sigmoid + bias router on the hidden state (moe.py:65-76)."""
         return self._routed.route(x)
+
+    def _proj(self, h: torch.Tensor, e: int, which: str) -> torch.Tensor:
+        """h @ W.T for one MXFP4 projection of expert e, fused or unfused (moe.py:79-88)."""
+        return self._routed._proj(h, e, which)
 
     def expert_forward(self, h: torch.Tensor, e: int) -> torch.Tensor:
         """One routed expert on latent rows h [N, L] (moe.py:90-103)."""
@@ -338,14 +410,27 @@ class LatentMoE:
         """Shared expert(s) on the original hidden state (moe.py:105-107)."""
         return self._routed.shared_forward(x)
 
-    DECODE_TOKENS = 8  # up to this many tokens: one fused decode per token; more: grouped
-
     def __call__(self, x: torch.Tensor, return_router: bool = False, out_dtype=torch.float32):
         orig = x.shape
         flat = x.reshape(-1, orig[-1])
+        if not self._fast:
+            return self._forward_loop(flat, orig, return_router, out_dtype)
         if flat.shape[0] <= self.DECODE_TOKENS:
             return self._decode(flat, orig, return_router, out_dtype)
         return self.grouped_forward(flat, return_router, out_dtype, orig)
+
+    def _forward_loop(self, flat, orig, return_router, out_dtype):
+        """The reference's structure (moe.py:110-132) with ``fused`` choosing _proj's form."""
+        c, R = self.cfg, self._routed
+        r = self.route(flat)
+        h = _blas.mm_ref(flat, self.down)                                  # hidden -> latent
+        y = R._combine_loop(h, r, self.latent)
+        y = _rmsnorm32(y, self._norm32, float(c.rms_norm_eps))
+        y = _blas.mm_f32(y, self.up)                                       # latent -> hidden
+        if R.sh_gate is not None:
+            y = y + self.shared_forward(flat)
+        y = y.to(out_dtype).reshape(*orig[:-1], orig[-1])
+        return (y, r) if return_router else y
 
     def _decode(self, flat, orig, return_router, out_dtype):
         """Per token: k3_moe_latent_layer_decode (route, latent down, routed experts,
@@ -357,14 +442,14 @@ class LatentMoE:
         nbytes = int(_lib.lib().k3_moe_latent_layer_workspace_size(H, Lw, I, Is, E, k))
         outs, recs = [], []
         for t in range(flat.shape[0]):
-            xt = T.contiguous_aligned(flat[t].reshape(1, -1).to(torch.bfloat16))
+            xt = R._x1(flat[t])
             ws = _workspace.get(R.device, nbytes, "moe_latent")
             out = torch.empty((1, H), dtype=out_dtype, device=R.device)
-            _lib.call("k3_moe_latent_layer_decode", T.ptr(xt), T.ptr(R.gate_w), T.ptr(R.gate_b),
-                      int(bool(c.moe_renormalize)), float(c.routed_scaling_factor), T.ptr(table), T.ptr(self.down),
-                      T.ptr(self.up), T.ptr(self._norm32), float(c.rms_norm_eps), T.ptr(R.sh_gate), T.ptr(R.sh_up),
-                      T.ptr(R.sh_down), T.ptr(out), T.dtype_code(out_dtype), H, Lw, I, Is, E, k, ACTS[act],
-                      float(beta), float(lb or 0.0), T.ptr(ws), ws.numel(), T.stream(xt))
+            _lib.call("k3_moe_latent_layer_decode", T.ptr(xt), T.dtype_code(xt.dtype), T.ptr(R.gate_w),
+                      T.ptr(R.gate_b), int(bool(c.moe_renormalize)), float(c.routed_scaling_factor), T.ptr(table),
+                      T.ptr(self.down), T.ptr(self.up), T.ptr(self._norm32), float(c.rms_norm_eps), T.ptr(R.sh_gate),
+                      T.ptr(R.sh_up), T.ptr(R.sh_down), T.ptr(out), T.dtype_code(out_dtype), H, Lw, I, Is, E, k,
+                      ACTS[act], float(beta), float(lb or 0.0), T.ptr(ws), ws.numel(), T.stream(xt))
             outs.append(out)
             if return_router:
                 recs.append(R._records(ws))
@@ -375,20 +460,22 @@ class LatentMoE:
                                  ("expert_indices", "expert_weights", "raw_scores", "corrected_scores")))
 
     def grouped_forward(self, flat, return_router=False, out_dtype=torch.float32, orig=None):
-        """Many tokens: route every token, h in bf16 through the BLAS library, the routed
-        experts grouped by expert on the device (k3_moe_grouped_ffn), the norm and the up
-        projection in fp32, the shared experts in fp32."""
+        """Many tokens: route every token on x as given; h = x W_down^T on the BLAS library
+        (bf16 for a bf16 x, fp32 for an fp32 x); the routed experts grouped by expert on the
+        device (k3_moe_grouped_ffn); the norm in fp32; the up projection and the shared
+        experts on the BLAS library with exact products and fp32 accumulation."""
         c = self.cfg
         orig = orig if orig is not None else flat.shape
         flat = flat.reshape(-1, flat.shape[-1])
         r = self.route(flat)
-        h = flat.to(torch.bfloat16) @ self.down.T                         # hidden -> latent
+        h = _blas.mm_f32(flat, self.down)                                 # hidden -> latent
+        if flat.dtype == torch.bfloat16:
+            h = h.to(torch.bfloat16)                                      # the reference's bf16 matmul
         act, beta, lb = self._routed._act()
         y = moe_grouped_ffn(h.contiguous(), r.expert_indices, r.expert_weights, self._routed.expert_table(),
                             int(c.moe_intermediate_size), act, beta, lb, out_dtype=torch.float32, validate=False)
-        eps = float(c.rms_norm_eps)
-        y = self._norm32 * (y * torch.rsqrt((y * y).mean(dim=-1, keepdim=True) + eps))
-        y = y @ self._up32.T                                              # latent -> hidden
+        y = _rmsnorm32(y, self._norm32, float(c.rms_norm_eps))
+        y = _blas.mm_f32(y, self.up)                                      # latent -> hidden
         if self._routed.sh_gate is not None:
             y = y + self.shared_forward(flat)
         y = y.to(out_dtype).reshape(*orig[:-1], orig[-1])
@@ -408,8 +495,8 @@ def moe_grouped_ffn(x: torch.Tensor, expert_indices: torch.Tensor, expert_weight
     if x.dim() != 2 or expert_indices.shape != expert_weights.shape or expert_indices.shape[0] != x.shape[0]:
         raise ValueError(f"x [T, H] with expert_indices/expert_weights [T, k] expected; got {tuple(x.shape)}, "
                          f"{tuple(expert_indices.shape)}, {tuple(expert_weights.shape)}")
-    if x.dtype != torch.bfloat16:
-        raise TypeError("the grouped path takes bf16 hidden states")
+    if x.dtype not in (torch.bfloat16, torch.float32):
+        x = x.to(torch.float32)
     T.require_device(x, expert_indices, expert_weights, table)
     n_tok, H = x.shape
     k = expert_indices.shape[1]

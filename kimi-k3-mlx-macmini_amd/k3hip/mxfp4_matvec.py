@@ -24,8 +24,7 @@ def _prep_x(x: torch.Tensor) -> torch.Tensor:
 
 
 def mxfp4_matvec_fused(x: torch.Tensor, packed: torch.Tensor, scales: torch.Tensor,
-                       out_dtype: torch.dtype = torch.float32, *, rows_per_wave: int = 0,
-                       groups_per_lane: int = 0) -> torch.Tensor:
+                       out_dtype: torch.dtype = torch.float32) -> torch.Tensor:
     """y = x @ W.T with W given by (packed, scales); fp32 accumulation."""
     if x.dim() != 2:
         raise ValueError(f"x must be [M, K]; got shape {tuple(x.shape)}")
@@ -42,12 +41,8 @@ def mxfp4_matvec_fused(x: torch.Tensor, packed: torch.Tensor, scales: torch.Tens
     packed = T.contiguous_aligned(packed)
     scales = scales.contiguous()
     out = torch.empty((M, N), dtype=out_dtype, device=x.device)
-    args = (T.ptr(x), T.dtype_code(x.dtype), T.ptr(packed), T.ptr(scales), T.ptr(out),
-            T.dtype_code(out_dtype), M, N, x.shape[1])
-    if rows_per_wave or groups_per_lane:
-        _lib.call("k3_mxfp4_matvec_cfg", *args, rows_per_wave, groups_per_lane, T.stream(x))
-    else:
-        _lib.call("k3_mxfp4_matvec", *args, T.stream(x))
+    _lib.call("k3_mxfp4_matvec", T.ptr(x), T.dtype_code(x.dtype), T.ptr(packed), T.ptr(scales), T.ptr(out),
+              T.dtype_code(out_dtype), M, N, x.shape[1], T.stream(x))
     return out
 
 

@@ -249,6 +249,11 @@ def test_mla_fused_decode_step_matches_torch_step_and_oracle():
             2 ** -7 * cref.rot[0, t].float().abs().max().item()
         lat = cache.latent[0, :t + 1].float().cpu().numpy().astype(np.float64)
         rot = cache.rot[0, :t + 1].float().cpu().numpy().astype(np.float64)
+        # the new cache row against fp64 directly: bf16(rmsnorm(kv_a x)) and bf16(rope part)
+        ckv = xb[t] @ w["kv_a_proj_with_mqa.weight"].T
+        lat_want = rms(ckv[:klr], w["kv_a_layernorm.weight"])
+        assert np.abs(lat[t] - lat_want).max() <= 2 ** -8 * np.abs(lat_want).max()   # one bf16 rounding
+        assert np.abs(rot[t] - ckv[klr:]).max() <= 2 ** -8 * np.abs(ckv[klr:]).max()
         q = (rms(xb[t] @ w["q_a_proj.weight"].T, w["q_a_layernorm.weight"]) @ w["q_b_proj.weight"].T
              ).reshape(nh, cfg.q_head_dim)
         oo = omla.mla_decode_absorbed(q[:, :nope], q[:, nope:], kb[:, :nope], kb[:, nope:], lat, rot,

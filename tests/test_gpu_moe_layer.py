@@ -115,8 +115,11 @@ def test_route_only_matches_layer_record_and_invariants():
     assert torch.equal(idx.sort(-1).values, r.corrected_scores.topk(8, -1).indices.sort(-1).values)
     raw_k = r.raw_scores.gather(1, idx)
     assert torch.allclose(raw_k / raw_k.sum(-1, keepdim=True) * 2.5, r.expert_weights, atol=1e-6)
+    # the layer kernel's own records (its in-kernel router rows) against route(), whose logits
+    # come from one GEMM over all tokens: same experts, weights to fp32 accumulation-order noise
     _, r2 = moe(x, return_router=True)
-    assert torch.equal(r2.expert_indices, idx) and torch.equal(r2.expert_weights, r.expert_weights)
+    assert torch.equal(r2.expert_indices, idx)
+    assert torch.allclose(r2.expert_weights, r.expert_weights, rtol=1e-5, atol=1e-7)
 
 
 def test_layer_deterministic_and_graph_replay():

@@ -116,16 +116,23 @@ def test_matvec_shapes_vs_oracle(n, k, xdt):
         assert om.normwise_rel(got, want) <= om.normwise_rel(unfused, want)
 
 
-@pytest.mark.parametrize("rpw,gpl", [(1, 4), (2, 4), (1, 2), (2, 2), (4, 2), (1, 1), (2, 1), (4, 1), (8, 1)])
+# (N, K) pairs that select every default launch shape (rows per wave, 32-element groups per
+# lane per sweep): gpl 1 / 2 / 4 by K, rows per wave by N; K = 16384 sweeps each row twice.
+LAUNCH_SHAPES = [(500, 2048), (1040, 2048), (4100, 1024), (8200, 512), (500, 3072), (2100, 3072), (4100, 3072),
+                 (500, 7168), (8200, 7168), (300, 16384)]
+
+
+@pytest.mark.parametrize("N,K", LAUNCH_SHAPES)
 @pytest.mark.parametrize("xdt", [torch.bfloat16, torch.float32])
-def test_matvec_every_launch_shape(rpw, gpl, xdt):
+def test_matvec_every_launch_shape(N, K, xdt):
+    """Every (rows per wave, groups per lane) the default configuration picks, with N not
+    a multiple of the rows per block (tail rows read zeros and are not stored)."""
     from k3hip.mxfp4_matvec import mxfp4_matvec_fused
-    packed, scales, x32 = _case(rpw * 10 + gpl, 203, 7168, 1)
+    packed, scales, x32 = _case(N + K, N, K, 1)
     if xdt == torch.bfloat16:
         x32 = om.bf16_round(x32)
     x = torch.from_numpy(x32).to(DEV).to(xdt)
-    got = mxfp4_matvec_fused(x, _t(packed), _t(scales), rows_per_wave=rpw,
-                             groups_per_lane=gpl).cpu().numpy()
+    got = mxfp4_matvec_fused(x, _t(packed), _t(scales)).cpu().numpy()
     assert om.normwise_rel(got, om.matvec_f64(x32, packed, scales)) < 2e-6
 
 
