@@ -86,6 +86,18 @@ int k3_expert_ffn(const void *x, int x_dtype, const void *gate_packed, const voi
                   int act_kind, float beta, float linear_beta, void *workspace,
                   int64_t workspace_bytes, void *stream);
 
+/* k3_expert_ffn without a caller workspace and without any allocation: for callers that
+ * cannot allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc).  No counterpart in the reference.  act lives in a
+ * static device array of 16384 fp32 values (64 KiB per GPU, held until the process ends);
+ * I > 16384 returns K3_ERR_WORKSPACE.  Every call on a GPU shares that array, so calls that
+ * overlap on one GPU (on different streams, or from different threads without ordering)
+ * race; calls on one stream never overlap.  Same results as k3_expert_ffn. */
+int k3_expert_ffn_noalloc(const void *x, int x_dtype, const void *gate_packed, const void *gate_scales,
+                          const void *up_packed, const void *up_scales, const void *down_packed,
+                          const void *down_scales, void *out, int out_dtype, int64_t H, int64_t I,
+                          int act_kind, float beta, float linear_beta, void *stream);
+
 /* ---- routed MoE layer at batch 1 ------------------------------------------------------ */
 
 /* Workspace bytes for k3_moe_layer_decode / k3_moe_route (pass shared_I = 0 without a

@@ -14,6 +14,7 @@
 // Measured on MI355X, a same-stream kernel boundary costs ~1 us, against ~2.6 us for a
 // grid barrier inside one persistent launch plus the re-staging of act after it.
 #include <algorithm>
+#include <mutex>
 
 #include "moe_common.h"
 #include "mxfp4_dot.h"
@@ -121,11 +122,60 @@ static int dispatch_gateup(const GateUpArgs &a, hipStream_t st) {
     return set_error(K3_ERR_SHAPE, "expert ffn: H=%d exceeds 8192", a.H);
 }
 
+// Scratch of the allocation-free entry point: act for I <= kNoAllocMaxI.  One copy per GPU,
+// held until the process ends; host code addresses it only through the pointer that
+// hipGetSymbolAddress returns for the current device (the array's name is a host-side
+// stand-in, not a device address).
+constexpr int64_t kNoAllocMaxI = 16384;
+static __device__ __align__(256) float scratch[kNoAllocMaxI];
+
+constexpr int kMaxDevices = 64;
+static std::mutex g_scratch_mu;
+static void *g_scratch_ptr[kMaxDevices];
+
+// Device address of `scratch` on the current device, resolved once per device.
+static int scratch_ptr(void **ptr) {
+    int dev = 0;
+    int rc = check_hip(hipGetDevice(&dev), "no-alloc expert ffn: current device");
+    if (rc) return rc;
+    if (dev < 0 || dev >= kMaxDevices) return set_error(K3_ERR_HIP, "no-alloc expert ffn: device %d", dev);
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+        void *p = nullptr;
+        rc = check_hip(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)), "no-alloc expert ffn: scratch address");
+        if (rc) return rc;
+        g_scratch_ptr[dev] = p;
+    }
+    *ptr = g_scratch_ptr[dev];
+    return K3_OK;
+}
+
 }  // namespace k3
 
 using namespace k3;
 
 extern "C" int64_t k3_expert_ffn_workspace_size(int64_t I) { return ((I * 4 + 255) / 256) * 256; }
+
+extern "C" int k3_expert_ffn(const void *x, int x_dtype, const void *gate_packed, const void *gate_scales,
+                             const void *up_packed, const void *up_scales, const void *down_packed,
+                             const void *down_scales, void *out, int out_dtype, int64_t H, int64_t I,
+                             int act_kind, float beta, float linear_beta, void *workspace,
+                             int64_t workspace_bytes, void *stream);
+
+extern "C" int k3_expert_ffn_noalloc(const void *x, int x_dtype, const void *gate_packed, const void *gate_scales,
+                                     const void *up_packed, const void *up_scales, const void *down_packed,
+                                     const void *down_scales, void *out, int out_dtype, int64_t H, int64_t I,
+                                     int act_kind, float beta, float linear_beta, void *stream) {
+    if (I > kNoAllocMaxI)
+        return set_error(K3_ERR_WORKSPACE, "no-alloc expert ffn: I=%lld exceeds the %lld values of its scratch",
+                         (long long)I, (long long)kNoAllocMaxI);
+    void *ws = nullptr;
+    const int rc = scratch_ptr(&ws);
+    if (rc) return rc;
+    return k3_expert_ffn(x, x_dtype, gate_packed, gate_scales, up_packed, up_scales, down_packed, down_scales, out,
+                         out_dtype, H, I, act_kind, beta, linear_beta, ws,
+                         static_cast<int64_t>(sizeof(float)) * kNoAllocMaxI, stream);
+}
 
 extern "C" int k3_expert_ffn(const void *x, int x_dtype, const void *gate_packed, const void *gate_scales,
                              const void *up_packed, const void *up_scales, const void *down_packed,

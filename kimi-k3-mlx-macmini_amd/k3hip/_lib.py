@@ -36,6 +36,7 @@ SIGNATURES: dict[str, list] = {
     "k3_expert_ffn_workspace_size": [_I64],
     "k3_expert_ffn": [_P, _I32, _P, _P, _P, _P, _P, _P, _P, _I32, _I64, _I64, _I32, _F32, _F32,
                       _P, _I64, _P],
+    "k3_expert_ffn_noalloc": [_P, _I32, _P, _P, _P, _P, _P, _P, _P, _I32, _I64, _I64, _I32, _F32, _F32, _P],
     "k3_moe_layer_workspace_size": [_I64, _I64, _I64, _I64, _I64],
     "k3_moe_layer_workspace_offsets": [_I64, _I64, _I64, _I64, _I64, _P],
     "k3_moe_route": [_P, _I32, _P, _P, _I32, _I32, _F32, _I64, _I64, _I64, _P, _I64, _P],
