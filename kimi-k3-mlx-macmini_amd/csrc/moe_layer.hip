@@ -78,6 +78,7 @@ struct LayerArgs {
     const float *lat_norm;         // [Hr] KimiRMSNorm weight
     float eps;
     int l1_latent_blocks;          // L1: the next blocks do latent down rows (4 per block)
+    int l3_ranges;                 // L3: row ranges (one arrival counter each)
 };
 
 constexpr int kMaxTopK = 16;
@@ -379,11 +380,21 @@ __global__ __launch_bounds__(256) void layer_l1(LayerArgs a) {
         __builtin_amdgcn_s_waitcnt(0);  // each wave's logit store is complete ...
         __syncthreads();
         if (threadIdx.x == 0) {         // ... before the block counts itself done
-            // modular, so that one block of every call routes even if the counter did not
-            // start at zero (the routing then reads this call's own pointer table either way)
+            // The logits are agent-scope atomic stores (written through to the coherence
+            // point) and every wave has waited for their completion above, so the count is
+            // made after they are visible device-wide; the block that brings it to the number
+            // of router blocks runs an agent-scope acquire and routes on every block's
+            // logits.  (A release RMW per block would add an L2 writeback per router block:
+            // measured 62 -> 95 us per layer when the L3 blocks did the same.)  The counter is
+            // zero at the start of a call: that block returns it to zero, and L2 of every
+            // call zeroes it as well (a workspace that started with garbage there routes
+            // correctly from its second call on).
             const uint32_t old = __hip_atomic_fetch_add(a.ws.counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            last_s = (old + 1) % static_cast<uint32_t>(a.l1_router_blocks) == 0;
-            if (last_s) __hip_atomic_store(a.ws.counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            last_s = old + 1 == static_cast<uint32_t>(a.l1_router_blocks);
+            if (last_s) {
+                __hip_atomic_store(a.ws.counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+            }
         }
         __syncthreads();
         if (last_s) route_block(a);
@@ -457,6 +468,10 @@ template <typename XT, int GA, int CHI>
 __global__ __launch_bounds__(256) void layer_l2(LayerArgs a) {
     extern __shared__ uint4 smem[];
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+    // L1 is complete and L3 has not started: zero L1's counter and L3's range counters, so
+    // each call starts from zeros whatever the counter bytes held before
+    if (blockIdx.x == 0)
+        for (int c = threadIdx.x; c < 1 + a.l3_ranges; c += 256) a.ws.counter[c] = 0u;
     if (static_cast<int>(blockIdx.x) < a.l2_shared_blocks) {
         // shared down: kSharedDownRows bf16 rows [H, Is] per wave against the fp32 shared act,
         // which each lane holds in registers for its own chunks (L2-resident after the first
@@ -625,15 +640,20 @@ __global__ __launch_bounds__(256, 4) void layer_l3(LayerArgs a) {
             __hip_atomic_store(a.ws.yrow + static_cast<int64_t>(j) * a.Hr + n, tot, __ATOMIC_RELAXED,
                                __HIP_MEMORY_SCOPE_AGENT);
     }
-    // 3. the block counts itself done once its row stores are complete; the last of the
-    //    range's k blocks resets the counter and combines
+    // 3. the block counts itself done once its row stores (agent-scope atomic stores) have
+    //    completed; the last of the range's k blocks runs an agent-scope acquire, resets the
+    //    counter and combines.  L2 zeroed every range counter before this launch, so stale
+    //    counter bytes cannot skip or misplace the combine.
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
     if (threadIdx.x == 0) {
         uint32_t *c = a.ws.counter + 1 + rr;
         const uint32_t old = __hip_atomic_fetch_add(c, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         last_s = old + 1 == static_cast<uint32_t>(a.k);
-        if (last_s) __hip_atomic_store(c, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (last_s) {
+            __hip_atomic_store(c, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+        }
     }
     __syncthreads();
     if (!last_s) return;
@@ -733,9 +753,14 @@ static int launch_layer(LayerArgs &a, hipStream_t st) {
     const int gb = GI <= 64 ? 1 : (GI <= 128 ? 2 : 0);
     if (!ga || !gb || (a.sh_down && chi > 16))
         return set_error(K3_ERR_SHAPE, "moe layer: H=%d I=%d Is=%d outside the kernels' range", a.H, a.I, a.Is);
+    const int rb = GI <= 64 ? 4 * 14 : (GI <= 96 ? 4 * 7 : 4 * 4);  // L3 rows per block
+    a.l3_ranges = static_cast<int>(cdiv(a.Hr, rb));
+    if (1 + a.l3_ranges > static_cast<int>(kCounterBytes / 4))
+        return set_error(K3_ERR_SHAPE, "moe layer: %d rows need more row-range counters than the workspace holds",
+                         a.Hr);
     int rc = launch_l1<XT>(a, a.sh_gate != nullptr, st);
     if (rc) return rc;
-    // L2
+    // L2 (zeroes the arrival counters L3 uses)
     const int chi_l2 = chi <= 4 ? 4 : (chi <= 8 ? 8 : 16);
     a.l2_shared_blocks = a.sh_down ? static_cast<int>(cdiv(a.H, 4 * shared_down_rows(chi_l2))) : 0;
     const int routed_blocks = static_cast<int>(cdiv(static_cast<int64_t>(a.k) * a.I, 4 * kRoutedPairs));
@@ -754,11 +779,7 @@ static int launch_layer(LayerArgs &a, hipStream_t st) {
     if (rc) return rc;
     // L3: pieces of a down row per lane and rows per wave, so a lane's act values and its
     // rows' weights fit in about 128 registers (four blocks per CU)
-    const int rb = GI <= 64 ? 4 * 14 : (GI <= 96 ? 4 * 7 : 4 * 4);
-    if (1 + cdiv(a.Hr, rb) > static_cast<int64_t>(kCounterBytes / 4))
-        return set_error(K3_ERR_SHAPE, "moe layer: %d rows need more row-range counters than the workspace holds",
-                         a.Hr);
-    const dim3 g3(static_cast<unsigned>(a.k * cdiv(a.Hr, rb)));
+    const dim3 g3(static_cast<unsigned>(a.k * a.l3_ranges));
     if (GI <= 64)
         layer_l3<32, 1, 14><<<g3, 256, 0, st>>>(a);
     else if (GI <= 96)

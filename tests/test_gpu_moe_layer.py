@@ -158,3 +158,27 @@ def test_layer_multi_token_and_unfused_expert():
     b = moe.expert_forward(h, 3).cpu().numpy()
     want = omoe.expert_ffn(x32[:1], *experts[3])[0]
     assert om.normwise_rel(a, want) < 1e-4 and om.normwise_rel(b, want) < 1e-5
+
+
+def test_layer_counter_bytes_garbage():
+    """Arrival counters holding garbage: L2 zeroes L3's range counters inside the call, so a
+    layer whose workspace starts with garbage there is exact on its first call; garbage in
+    L1's router counter is cleared by the first call (L2 zeroes it too), so the second call
+    is exact."""
+    from k3hip.moe import RoutedMoE
+    cfg, w, source, router_w, bias, experts, shared = make_layer(21, 2048, 512, 64, 8, 512, 8)
+    moe = RoutedMoE(cfg, 0, w, source)
+    x32 = om.bf16_round(np.random.default_rng(22).standard_normal((1, 2048)).astype(np.float32))
+    x = torch.from_numpy(x32).to(DEV).to(torch.bfloat16)
+    want = oracle_layer(x32, router_w, bias, experts, shared, cfg)[0]
+    moe(x)                                            # workspace exists
+    ws = moe._workspace()
+    ctr = ws[:4096].view(torch.int32)
+    ctr[1:].fill_(0x5A5A5A5A)                         # every L3 range counter word
+    assert om.normwise_rel(moe(x).cpu().numpy(), want) < 2e-5
+    ranges = -(-2048 // 56)                           # L3 row ranges at I = 512 (56 rows each)
+    assert int(ctr[1:1 + ranges].abs().max()) == 0
+    ctr[0] = 7                                        # L1's router counter
+    moe(x)
+    assert int(ctr[0]) == 0
+    assert om.normwise_rel(moe(x).cpu().numpy(), want) < 2e-5
