@@ -210,7 +210,8 @@ int k3_moe_latent_layer_decode(const void *x, int x_dtype, const void *router_w,
 /* ---- latent-MLA absorbed decode (one query token, batch 1) ------------------------------ */
 
 /* Workspace bytes k3_mla_decode_absorbed needs for H heads over T cached tokens (qa
- * hi/lo rows and one (ctx, max, sum) record per head per token split).  No initialisation. */
+ * hi/lo rows, one (ctx, max, sum) record per head per token split, and the W_UV products
+ * of the four column quarters for v up to 1024).  No initialisation. */
 int64_t k3_mla_workspace_size(int64_t H, int64_t T);
 
 /* o[h] = W_UV[h] @ (softmax_t(scale * (q_nope[h] W_UK[h] . lat[t] + q_rot[h] . rot[t])) @ lat)
@@ -250,7 +251,7 @@ int64_t k3_mla_step_workspace_size(int64_t hidden, int64_t q_lora_rank, int64_t 
  * row-major; q_a_norm [q_lora_rank], kv_a_norm [r]: fp32; w_uk / w_uv as for
  * k3_mla_decode_absorbed; lat / rot the bf16 cache with cache_rows rows (pos < cache_rows).
  * hidden, q_lora_rank and heads*v: multiples of 8, <= 12288.  fp32 accumulation and
- * norms.  Six stream-ordered launches. */
+ * norms.  Seven stream-ordered launches. */
 int k3_mla_step_decode(const void *x, int x_dtype, const void *q_a, const float *q_a_norm, const void *q_b,
                        const void *kv_a, const float *kv_a_norm, const void *w_uk, const void *w_uv,
                        const void *g_proj, const void *o_proj, void *lat, int64_t ld_lat, void *rot,

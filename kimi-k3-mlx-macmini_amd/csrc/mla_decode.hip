@@ -25,8 +25,10 @@
 //       ctx^T += rows^T [P_hi; P_lo] on the same MFMA.  The streams merge in the block,
 //       which writes its unnormalised (ctx, max, sum) record per head.
 //   M   per (head, quarter of the latent columns): log-sum-exp merge of the split records
-//       in a fixed order into the normalised ctx.
-//   U   o = W_UV[h] @ ctx[h] in fp32, 32 output rows per block.
+//       in a fixed order into the normalised ctx, then the W_UV product over that quarter,
+//       o_q = W_UV[h][:, quarter] @ ctx[h][quarter] in fp32; every record and W_UV element is
+//       read by one block.
+//   O   o = o_0 + o_1 + o_2 + o_3 in quarter order (then the optional output gate).
 //
 // Numerics: lat, rot, W_UK, W_UV and bf16 queries are exact in the MFMA inputs; the fp32
 // operands (qa, P) are carried as hi + lo bf16 pairs, so each product is represented to
@@ -475,11 +477,8 @@ struct MergeArgs {
     const float *part;     // [NS, H, 512]
     const float2 *ml;      // [NS, H]
     const uint16_t *w_uv;  // [H, V, 512] bf16
-    void *out;             // [H, V] rows of ld_out elements
-    int64_t ld_out;
+    float *opart;          // [4, H, V] W_UV products over each quarter of the columns
     int H, NS, V;
-    int out_bf16;
-    const float *gate;     // [H, V] logits or null: o *= sigmoid(gate) (the MLA output gate)
 };
 
 __device__ __forceinline__ float block_sum256(float v, float *red) {
@@ -499,71 +498,69 @@ __device__ __forceinline__ float block_max256(float v, float *red) {
     return r;
 }
 
-constexpr int kMergeChunk = 64;  // splits whose record columns are in flight at once
-constexpr int kMergeRows = 64;   // W_UV rows per merge block (16 per wave)
+constexpr int kMergeQ = 4;                   // column quarters per head
+constexpr int kMQCols = kR / kMergeQ;        // 128 columns per merge block
+constexpr int kMergeChunk = 16;              // record loads per thread in flight at once
+constexpr int kUvBatch = 8;                  // W_UV row groups (16 rows) in flight at once
 
-// grid: H * cdiv(V, kMergeRows); block (h, vb): every block of head h merges the split
-// records of h into ctx[h], then computes o[h][v] = W_UV[h][v] . ctx[h] for its rows.  All
-// loads of a chunk of 64 splits are issued at once, behind the W_UV rows and the split
-// maxima, so the block waits for memory about once per chunk.
-//   merge:  thread t owns columns 4 (t % 128) .. +3 of the splits s = t / 128 (mod 2);
-//           ctx = sum_s 2^(m_s - M) ctx_s / L with M = max_s m_s, L = sum_s 2^(m_s - M) l_s,
-//           summed in split order within each half, then half 0 + half 1
-//   W_UV:   wave w, rows vb * kMergeRows + 8 w .. +8; lane l covers columns 8 l .. +8
-__global__ __launch_bounds__(256) void mla_merge_uv_kernel(MergeArgs a) {
-    __shared__ float4 half1[kR / 4];
-    __shared__ float ctx[kR];
+// grid: H * 4; block (h, q) owns columns 128 q .. +128 of head h.  Each record column is read
+// by exactly one block, and so is each W_UV element.
+//   merge:  ctx = sum_s 2^(m_s - M) ctx_s / L with M = max_s m_s, L = sum_s 2^(m_s - M) l_s;
+//           thread t owns columns 4 (t % 32) .. +3 of the splits s = t / 32 (mod 8), the eight
+//           partial sums meet in LDS and add in split-group order
+//   W_UV:   opart[q][h][v] = W_UV[h][v][128 q ..] . ctx; 16 lanes per row (8 columns each),
+//           so one wave instruction reads four whole 256-byte row pieces
+__global__ __launch_bounds__(256) void mla_merge_kernel(MergeArgs a) {
+    __shared__ float4 red8[8][kMQCols / 4];
+    __shared__ float ctx[kMQCols];
     __shared__ float wsplit[kMaxSplits];
     __shared__ float red[4];
-    const int vb_n = (a.V + kMergeRows - 1) / kMergeRows;
-    const int h = blockIdx.x / vb_n, vb = blockIdx.x % vb_n;
+    const int h = blockIdx.x / kMergeQ, q = blockIdx.x % kMergeQ;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int c4 = tid & 127, g = tid >> 7;
+    const int c4 = tid & 31, g = tid >> 5;
+    const int sub = lane & 15;  // W_UV: lane covers columns 8 sub .. +8 of the quarter
 
-    // W_UV rows of this block
-    const int r0 = vb * kMergeRows + wave * (kMergeRows / 4);
-    uint4 w[kMergeRows / 4];
+    // first batch of W_UV rows: wave w, rows 16 i + 4 w + lane / 16
+    const uint16_t *wbase = a.w_uv + static_cast<int64_t>(h) * a.V * kR + q * kMQCols + sub * 8;
+    auto w_row = [&](int v) -> uint4 {
+        return v < a.V ? *reinterpret_cast<const uint4 *>(wbase + static_cast<int64_t>(v) * kR) : make_uint4(0u, 0u, 0u, 0u);
+    };
+    const int vrow = 4 * wave + (lane >> 4);
+    uint4 w[kUvBatch];
 #pragma unroll
-    for (int u = 0; u < kMergeRows / 4; ++u) {
-        const int v = r0 + u;
-        w[u] = v < a.V ? *reinterpret_cast<const uint4 *>(a.w_uv + (static_cast<int64_t>(h) * a.V + v) * kR + lane * 8)
-                       : make_uint4(0u, 0u, 0u, 0u);
-    }
-    // output-gate logit of row r0 + lane (lanes below kMergeRows / 4), read with the rows
-    float gv = 0.f;
-    if (a.gate && lane < kMergeRows / 4 && r0 + lane < a.V) gv = a.gate[static_cast<int64_t>(h) * a.V + r0 + lane];
+    for (int i = 0; i < kUvBatch; ++i) w[i] = w_row(16 * i + vrow);
     // split maxima and sums
     float2 mlv[kMaxSplits / 256];
 #pragma unroll
-    for (int q = 0; q < kMaxSplits / 256; ++q) {
-        const int sidx = tid + 256 * q;
-        mlv[q] = sidx < a.NS ? a.ml[static_cast<int64_t>(sidx) * a.H + h] : make_float2(-INFINITY, 0.f);
+    for (int u = 0; u < kMaxSplits / 256; ++u) {
+        const int sidx = tid + 256 * u;
+        mlv[u] = sidx < a.NS ? a.ml[static_cast<int64_t>(sidx) * a.H + h] : make_float2(-INFINITY, 0.f);
     }
-    // record columns of the first chunk
-    const float *col = a.part + static_cast<int64_t>(h) * kR + 4 * c4;
+    // record columns of the first chunk of splits
+    const float *col = a.part + static_cast<int64_t>(h) * kR + q * kMQCols + 4 * c4;
     const int64_t sstride = static_cast<int64_t>(a.H) * kR;
-    auto load_chunk = [&](float4(&c)[kMergeChunk / 2], int s0) {
+    auto load_chunk = [&](float4(&c)[kMergeChunk], int s0) {
 #pragma unroll
-        for (int u = 0; u < kMergeChunk / 2; ++u) {
-            const int sidx = s0 + 2 * u + g;
+        for (int u = 0; u < kMergeChunk; ++u) {
+            const int sidx = s0 + 8 * u + g;
             c[u] = sidx < a.NS ? *reinterpret_cast<const float4 *>(col + sidx * sstride) : make_float4(0.f, 0.f, 0.f, 0.f);
         }
     };
-    float4 c[kMergeChunk / 2];
+    float4 c[kMergeChunk];
     load_chunk(c, 0);
 
     float mx = -INFINITY;
 #pragma unroll
-    for (int q = 0; q < kMaxSplits / 256; ++q) mx = fmaxf(mx, mlv[q].x);
+    for (int u = 0; u < kMaxSplits / 256; ++u) mx = fmaxf(mx, mlv[u].x);
     const float M = block_max256(mx, red);  // finite: every split has a token
     float ls = 0.f;
 #pragma unroll
-    for (int q = 0; q < kMaxSplits / 256; ++q) {
-        const int sidx = tid + 256 * q;
+    for (int u = 0; u < kMaxSplits / 256; ++u) {
+        const int sidx = tid + 256 * u;
         if (sidx < a.NS) {
-            const float e = exp2f(mlv[q].x - M);
+            const float e = exp2f(mlv[u].x - M);
             wsplit[sidx] = e;
-            ls += e * mlv[q].y;
+            ls += e * mlv[u].y;
         }
     }
     const float inv_l = 1.0f / block_sum256(ls, red);  // block_sum256 synchronises wsplit
@@ -571,50 +568,80 @@ __global__ __launch_bounds__(256) void mla_merge_uv_kernel(MergeArgs a) {
     float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
     for (int s0 = 0;;) {
 #pragma unroll
-        for (int u = 0; u < kMergeChunk / 2; ++u) {
-            const int sidx = s0 + 2 * u + g;
+        for (int u = 0; u < kMergeChunk; ++u) {
+            const int sidx = s0 + 8 * u + g;
             const float ws = sidx < a.NS ? wsplit[sidx] : 0.f;
             acc.x = fmaf(ws, c[u].x, acc.x);
             acc.y = fmaf(ws, c[u].y, acc.y);
             acc.z = fmaf(ws, c[u].z, acc.z);
             acc.w = fmaf(ws, c[u].w, acc.w);
         }
-        s0 += kMergeChunk;
+        s0 += 8 * kMergeChunk;
         if (s0 >= a.NS) break;
         load_chunk(c, s0);
     }
-    if (g == 1) half1[c4] = acc;
+    red8[g][c4] = acc;
     __syncthreads();
-    if (g == 0) {
-        const float4 o = half1[c4];
-        *reinterpret_cast<float4 *>(ctx + 4 * c4) =
-            make_float4((acc.x + o.x) * inv_l, (acc.y + o.y) * inv_l, (acc.z + o.z) * inv_l, (acc.w + o.w) * inv_l);
+    if (tid < kMQCols / 4) {
+        float4 t = red8[0][tid];
+#pragma unroll
+        for (int j = 1; j < 8; ++j) {
+            const float4 o = red8[j][tid];
+            t.x += o.x, t.y += o.y, t.z += o.z, t.w += o.w;
+        }
+        *reinterpret_cast<float4 *>(ctx + 4 * tid) = make_float4(t.x * inv_l, t.y * inv_l, t.z * inv_l, t.w * inv_l);
     }
     __syncthreads();
 
-    const float4 c0 = *reinterpret_cast<const float4 *>(ctx + lane * 8);
-    const float4 c1 = *reinterpret_cast<const float4 *>(ctx + lane * 8 + 4);
-    const float c8[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
+    const float4 x0 = *reinterpret_cast<const float4 *>(ctx + sub * 8);
+    const float4 x1 = *reinterpret_cast<const float4 *>(ctx + sub * 8 + 4);
+    const float x8[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+    float *orow = a.opart + (static_cast<int64_t>(q) * a.H + h) * a.V;
+    for (int vb = 0; vb < a.V; vb += 16 * kUvBatch) {
+        if (vb > 0) {
 #pragma unroll
-    for (int u = 0; u < kMergeRows / 4; ++u) {
-        const int v = r0 + u;
-        const uint32_t wd[4] = {w[u].x, w[u].y, w[u].z, w[u].w};
-        float o = 0.f;
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            o = fmaf(__uint_as_float(wd[q] << 16), c8[2 * q], o);
-            o = fmaf(__uint_as_float(wd[q] & 0xffff0000u), c8[2 * q + 1], o);
+            for (int i = 0; i < kUvBatch; ++i) w[i] = w_row(vb + 16 * i + vrow);
         }
-        o = wave_sum_to_lane63(o);
-        if (a.gate) o /= 1.0f + expf(-readlane_f(gv, u));
-        if (lane == 63 && v < a.V) {
-            const int64_t oi = static_cast<int64_t>(h) * a.ld_out + v;
-            if (a.out_bf16)
-                static_cast<uint16_t *>(a.out)[oi] = f32_to_bf16(o);
-            else
-                static_cast<float *>(a.out)[oi] = o;
+#pragma unroll
+        for (int i = 0; i < kUvBatch; ++i) {
+            const uint32_t wd[4] = {w[i].x, w[i].y, w[i].z, w[i].w};
+            float o = 0.f;
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                o = fmaf(__uint_as_float(wd[k] << 16), x8[2 * k], o);
+                o = fmaf(__uint_as_float(wd[k] & 0xffff0000u), x8[2 * k + 1], o);
+            }
+            o = row16_sum(o);
+            const int v = vb + 16 * i + vrow;
+            if (sub == 0 && v < a.V) orow[v] = o;
         }
     }
+}
+
+struct OutArgs {
+    const float *opart;  // [4, H, V]
+    void *out;           // [H, V] rows of ld_out elements
+    int64_t ld_out;
+    int H, V;
+    int out_bf16;
+    const float *gate;   // [H, V] logits or null: o *= sigmoid(gate) (the MLA output gate)
+};
+
+// o[h][v] = the four column-quarter products added in quarter order (then the output gate)
+__global__ __launch_bounds__(256) void mla_out_kernel(OutArgs a) {
+    const int i = blockIdx.x * 256 + threadIdx.x;
+    const int n = a.H * a.V;
+    if (i >= n) return;
+    float o = a.opart[i];
+#pragma unroll
+    for (int q = 1; q < kMergeQ; ++q) o += a.opart[static_cast<int64_t>(q) * n + i];
+    if (a.gate) o /= 1.0f + expf(-a.gate[i]);
+    const int h = i / a.V, v = i % a.V;
+    const int64_t oi = static_cast<int64_t>(h) * a.ld_out + v;
+    if (a.out_bf16)
+        static_cast<uint16_t *>(a.out)[oi] = f32_to_bf16(o);
+    else
+        static_cast<float *>(a.out)[oi] = o;
 }
 
 // ------------------------------------------------------------------ host side
@@ -632,8 +659,10 @@ void mla_splits(int64_t H, int64_t T, int *Ts, int *NS) {
     *NS = static_cast<int>(cdiv(T, ts));
 }
 
+constexpr int kMaxV = 1024;  // largest v_head_dim the merge takes
+
 struct MlaWs {
-    size_t qa_hi, qa_lo, ml, part, total;
+    size_t qa_hi, qa_lo, ml, part, opart, total;
 };
 
 MlaWs mla_ws_layout(int64_t H, int64_t T) {
@@ -646,6 +675,7 @@ MlaWs mla_ws_layout(int64_t H, int64_t T) {
     L.qa_lo = o, o += up(static_cast<size_t>(H) * kQaLd * 2);
     L.ml = o, o += up(static_cast<size_t>(NS) * H * 8);
     L.part = o, o += up(static_cast<size_t>(NS) * H * kR * 4);
+    L.opart = o, o += up(static_cast<size_t>(kMergeQ) * H * kMaxV * 4);
     L.total = o;
     return L;
 }
@@ -685,7 +715,7 @@ int k3::mla_decode_core(const void *q_nope, const void *q_rot, int64_t ld_q, int
         return set_error(K3_ERR_SHAPE, "mla decode: kv_lora_rank=%lld rope=%lld; the kernels take 512 and 64",
                          (long long)kv_lora_rank, (long long)rope_dim);
     if (H <= 0 || H > 4096) return set_error(K3_ERR_SHAPE, "mla decode: H=%lld must be in 1..4096", (long long)H);
-    if (nope_dim <= 0 || nope_dim > 256 || v_dim <= 0 || v_dim > 1024)
+    if (nope_dim <= 0 || nope_dim > 256 || v_dim <= 0 || v_dim > kMaxV)
         return set_error(K3_ERR_SHAPE, "mla decode: nope=%lld must be in 1..256 and v=%lld in 1..1024",
                          (long long)nope_dim, (long long)v_dim);
     if (T <= 0) return set_error(K3_ERR_SHAPE, "mla decode: empty cache (T=%lld)", (long long)T);
@@ -749,8 +779,13 @@ int k3::mla_decode_core(const void *q_nope, const void *q_rot, int64_t ld_q, int
     rc = check_hip(hipGetLastError(), "mla decode: attention launch");
     if (rc) return rc;
 
-    MergeArgs ma{part, ml, static_cast<const uint16_t *>(w_uv), out, ld_out, static_cast<int>(H), NS,
-                 static_cast<int>(v_dim), out_dtype == K3_BF16, gate};
-    mla_merge_uv_kernel<<<dim3(static_cast<unsigned>(H * cdiv(v_dim, kMergeRows))), 256, 0, st>>>(ma);
-    return check_hip(hipGetLastError(), "mla decode: merge and W_UV launch");
+    float *opart = reinterpret_cast<float *>(ws + L.opart);
+    MergeArgs ma{part, ml, static_cast<const uint16_t *>(w_uv), opart, static_cast<int>(H), NS,
+                 static_cast<int>(v_dim)};
+    mla_merge_kernel<<<dim3(static_cast<unsigned>(H * kMergeQ)), 256, 0, st>>>(ma);
+    rc = check_hip(hipGetLastError(), "mla decode: merge and W_UV launch");
+    if (rc) return rc;
+    OutArgs oa{opart, out, ld_out, static_cast<int>(H), static_cast<int>(v_dim), out_dtype == K3_BF16, gate};
+    mla_out_kernel<<<dim3(static_cast<unsigned>(cdiv(H * v_dim, 256))), 256, 0, st>>>(oa);
+    return check_hip(hipGetLastError(), "mla decode: output launch");
 }

@@ -8,12 +8,12 @@
 //   o   = absorbed attention core over the cache                     (attention_mla.py:193-212)
 //   o   = o * sigmoid(x @ g_proj.T)  (mla_use_output_gate);  out = o @ o_proj.T
 //
-// Six stream-ordered launches, no host synchronisation:
+// Seven stream-ordered launches, no host synchronisation:
 //   S1  rows of q_a, kv_a and g_proj against x (one grid, three block ranges);
 //   S2  rows of q_b against the normalised q_a output (every block normalises the 1536-wide
 //       vector itself, so no launch is spent on it), and one block that normalises the kv
 //       latent and writes the new cache row (bf16) at position pos;
-//   core  the absorbed core of k3_mla_decode_absorbed (three launches) over the pos + 1
+//   core  the absorbed core of k3_mla_decode_absorbed (four launches) over the pos + 1
 //       cache rows, its last launch multiplying o by sigmoid(gate) as it writes it;
 //   S3  rows of o_proj against the gated o.
 // The row launches are the dense row kernels of dense_rows.h.

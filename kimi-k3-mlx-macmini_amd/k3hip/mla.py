@@ -15,7 +15,7 @@ by default: the kernel reads the valid prefix directly, so ``view`` does not upc
 ``MLAAttention(cfg, w)`` keeps the reference constructor and ``__call__(x, cache)``.  With
 bf16 projection weights (the checkpoint dtype) the decode step (one token, batch 1) is
 ``k3_mla_step_decode``: the projections, RMSNorms, cache append, attention core, output
-gate and o_proj in six HIP launches.  With other weight dtypes the projections are torch
+gate and o_proj in seven HIP launches.  With other weight dtypes the projections are torch
 fp32 matmuls around the HIP core.  Prefill (T > 1) keeps the reference's dense masked form
 in torch on the GPU.
 
