@@ -160,6 +160,49 @@ def bench_expert(torch, steps, warmup, dev):
     return sec, wall, stats
 
 
+def bench_expert_sustained(torch, steps, dev, reps=8):
+    """Independent experts back to back: expert i runs on stream i % 2, so one expert's
+    gate/up launch overlaps the other's down GEMV (no dependency between experts, as in a
+    layer's top-k).  The graph of `steps` experts is replayed `reps` times; returns seconds
+    per expert."""
+    from k3hip.moe import expert_ffn_fused
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(1002)
+    experts = [(rand_mxfp4(torch, gen, I, H, dev), rand_mxfp4(torch, gen, I, H, dev),
+                rand_mxfp4(torch, gen, H, I, dev)) for _ in range(ROTATE)]
+    x = torch.randn(1, H, device=dev, generator=gen).to(torch.bfloat16)
+    main = torch.cuda.current_stream()
+    side = [torch.cuda.Stream(device=dev) for _ in range(2)]
+    outs = [None, None]
+
+    def run(n):
+        cur = torch.cuda.current_stream()   # the capture stream inside torch.cuda.graph
+        for s in side:
+            s.wait_stream(cur)
+        for i in range(n):
+            with torch.cuda.stream(side[i & 1]):
+                outs[i & 1] = expert_ffn_fused(x, *experts[i % ROTATE])
+        for s in side:
+            cur.wait_stream(s)
+
+    run(4)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        run(steps)
+    g.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(main)
+    for _ in range(reps):
+        g.replay()
+    e1.record(main)
+    torch.cuda.synchronize()
+    sec = e0.elapsed_time(e1) * 1e-3 / (reps * steps)
+    del g, experts
+    return sec
+
+
 def bench_gemv(torch, steps, warmup, dev):
     from k3hip.mxfp4_matvec import mxfp4_matvec_fused
     gen = torch.Generator(device=dev)
@@ -225,6 +268,8 @@ def bench_layer(torch, steps, warmup, dev):
 K3_H, K3_L, K3_I, K3_E, K3_K, K3_IS = 7168, 3584, 3072, 896, 16, 6144
 K3_LAYER_BYTES = (K3_E * K3_H * 2 + 2 * K3_L * K3_H * 2 + K3_K * 3 * proj_bytes(K3_I, K3_L)
                   + 3 * K3_IS * K3_H * 2)                                 # 660,602,880
+K3_PF_T = 2048
+K3_PREFILL = True
 
 
 def bench_k3_layer(torch, steps, warmup, dev):
@@ -263,8 +308,32 @@ def bench_k3_layer(torch, steps, warmup, dev):
     touched = set()
     for i in range(min(steps, 32)):
         touched.update(moe.route(xs[i:i + 1]).expert_indices.view(-1).tolist())
+    prefill = None
+    if K3_PREFILL:
+        # K3 prefill: 2048 tokens through the same layer, routing included (one router GEMM
+        # plus one top-k launch), the experts grouped on the device; no host sync inside
+        xp = rn(K3_PF_T, K3_H).to(bf)
+        r = moe.route(xp)
+        counts = torch.bincount(r.expert_indices.view(-1), minlength=K3_E)
+        used = int((counts > 0).sum())
+
+        def pstep(i):
+            moe(xp)
+
+        psec, _ = graph_time(torch, pstep, 4, 1)
+        pbytes = (used * 3 * proj_bytes(K3_I, K3_L) + K3_E * K3_H * 2 + 2 * K3_L * K3_H * 2
+                  + 3 * K3_IS * K3_H * 2 + K3_PF_T * K3_H * (2 + 4))
+        pflops = 2 * K3_PF_T * (K3_K * 3 * K3_I * K3_L + K3_E * K3_H + 2 * K3_L * K3_H + 3 * K3_IS * K3_H)
+        prefill = {"tokens": K3_PF_T, "ms": round(psec / 4 * 1e3, 3),
+                   "tokens_per_s": round(K3_PF_T / (psec / 4), 1),
+                   "GB/s": round(pbytes / (psec / 4) / 1e9, 1), "bytes": pbytes,
+                   "useful_TFLOP/s": round(pflops / (psec / 4) / 1e12, 1),
+                   "experts_used": used, "expert_load_max": int(counts.max()),
+                   "what": "LatentMoE.__call__ on 2048 tokens: router GEMM + k3_moe_topk, latent down "
+                           "GEMM, k3_moe_grouped_ffn, RMSNorm, up GEMM, shared-expert GEMMs"}
+        del xp
     del moe, experts, w
-    return sec, len(touched), stats
+    return sec, len(touched), stats, prefill
 
 
 def bench_ingest(torch, dev, n_experts=32):
@@ -580,15 +649,31 @@ def bench_cpu(sample_s=12.0):
     return out
 
 
-def traffic_from_profiles():
-    """HBM bytes per expert step (both launches) from the committed rocprofv3 --pmc summary."""
-    f = ROOT / "profiles" / "expert_ffn_b1_traffic.json"
-    if f.exists():
-        try:
-            return json.loads(f.read_text()).get("bytes_per_step")
-        except (ValueError, OSError):
-            return None
-    return None
+def counters_from_profiles():
+    """Per-workload counter figures (rocprofv3 FETCH_SIZE / WRITE_SIZE / MFMA counts over the
+    same workloads, calibrated bytes, kernel times) from the committed profiles/counters.json."""
+    f = ROOT / "profiles" / "counters.json"
+    try:
+        return json.loads(f.read_text()).get("workloads", {})
+    except (ValueError, OSError):
+        return {}
+
+
+def counter_fields(rec):
+    """`traffic` (counter bytes / algorithmic bytes per step) and, for the MFMA workloads,
+    `mfma_util`, from one profiles/counters.json record."""
+    if not rec:
+        return {}
+    out = {"traffic": {"ratio": rec["traffic_ratio"], "counter_bytes": rec["counter_bytes"],
+                       "algorithmic_bytes": rec["algorithmic_bytes"], "source": "profiles/counters.json"}}
+    m = rec.get("mfma")
+    if m:
+        u = {"mfma": m["type"], "executed_TFLOP/s": m["executed_TFLOP/s"],
+             "frac_of_issue_peak": m["executed_frac_of_issue_peak"], "issue_peak_TFLOP/s": m["issue_peak_TFLOP/s"]}
+        if "useful_frac_of_mxfp4_peak" in m:
+            u["useful_frac_of_mxfp4_peak"] = m["useful_frac_of_mxfp4_peak"]
+        out["mfma_util"] = u
+    return out
 
 
 def main():
@@ -598,7 +683,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=64)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
-    ap.add_argument("--workloads", default="expert,layer,k3layer,ingest,prefill,gemv,mla,mlastep,kda,kdastep,ceiling")
+    ap.add_argument("--workloads",
+                    default="expert,sustained,layer,k3layer,ingest,prefill,gemv,mla,mlastep,kda,kdastep,ceiling")
     ap.add_argument("--eager", action="store_true",
                     help="launch steps one by one instead of replaying a HIP graph (profiler counter runs)")
     args = ap.parse_args()
@@ -619,6 +705,7 @@ def main():
     work = set(args.workloads.split(","))
     K, W = args.steps, args.warmup
 
+    cnt = counters_from_profiles()
     sec, wall, estats = bench_expert(torch, K, W, dev)
     per_step = sec / K
     gbs = EXPERT_BYTES / per_step / 1e9
@@ -639,13 +726,21 @@ def main():
                    "experts_rotated": ROTATE, "act": "silu", "x": "bf16", "out": "f32"},
         "pct_hbm_peak": round(100 * gbs / HBM_PEAK_GBS, 1),
         "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": traffic_from_profiles(),
+                     "frac": round(gbs / HBM_PEAK_GBS, 4),
+                     "traffic": cnt.get("expert_swiglu_ffn_b1", {}).get("counter_bytes"),
                      "kernel": "expert FFN step: expert_gateup_kernel then gemv_kernel (down)",
                      "launches_per_step": 2, "bytes_per_step": EXPERT_BYTES,
                      "avg_step_us": round(per_step * 1e6, 3)},
         "wall_s": round(wall, 4),
         "step_us": estats,
     }
+    if "sustained" in work:
+        ssec_ = bench_expert_sustained(torch, ROTATE, dev)
+        sgbs_ = EXPERT_BYTES / ssec_ / 1e9
+        line["sustained"] = {"us_per_expert": round(ssec_ * 1e6, 3), "GB/s": round(sgbs_, 1),
+                             "pct_hbm_peak": round(100 * sgbs_ / HBM_PEAK_GBS, 1),
+                             "what": "independent experts back to back on two streams (expert i on "
+                                     "stream i % 2), graph of 64 replayed 8 times"}
     if "layer" in work:
         lsec, touched, lstats = bench_layer(torch, min(K, 256), min(W, 32), dev)
         lus = lsec / min(K, 256) * 1e6
@@ -654,10 +749,11 @@ def main():
                              "pct_hbm_peak": round(100 * lgbs / HBM_PEAK_GBS, 1),
                              "bytes_per_layer": LAYER_BYTES, "experts": E_LAYER, "top_k": TOPK,
                              "shared_expert": "bf16", "distinct_experts_routed_first32": touched,
-                             "launches_per_layer": 3, "step_us": lstats}
+                             "launches_per_layer": 3, "step_us": lstats,
+                             **counter_fields(cnt.get("moe_layer_b1"))}
     if "k3layer" in work:
         ks = min(K, 256)
-        ksec, ktouched, kstats = bench_k3_layer(torch, ks, min(W, 32), dev)
+        ksec, ktouched, kstats, kpre = bench_k3_layer(torch, ks, min(W, 32), dev)
         kus = ksec / ks * 1e6
         kgbs = K3_LAYER_BYTES / (kus * 1e-6) / 1e9
         line["k3_latent_layer"] = {"us_per_token": round(kus, 2), "GB/s": round(kgbs, 1),
@@ -666,7 +762,11 @@ def main():
                                    "expert_intermediate": K3_I, "experts": K3_E, "top_k": K3_K,
                                    "shared_intermediate": K3_IS, "router": "sigmoid + bias",
                                    "act": "situ", "distinct_experts_routed_first32": ktouched,
-                                   "launches_per_token": 4, "step_us": kstats}
+                                   "launches_per_token": 4, "step_us": kstats, "prefill": kpre,
+                                   **counter_fields(cnt.get("k3_latent_layer_b1"))}
+        if kpre is not None:
+            kpre.update({"grouped_experts_" + k_: v_ for k_, v_ in
+                         counter_fields(cnt.get("k3_prefill_t2048_e896_grouped")).items()})
     if "ingest" in work:
         line["checkpoint_ingest"] = bench_ingest(torch, dev)
     if "prefill" in work:
@@ -679,7 +779,8 @@ def main():
             "pct_fp8_mfma_peak": round(100 * PF_FLOPS / pst / 5.0e15, 1),
             "tokens": PF_T, "top_k": PF_K, "experts": E_LAYER, "routing": "zipf(1.1), seeded",
             "expert_load": {"max": int(counts.max()), "mean": round(float(counts.mean()), 1),
-                            "empty": int((counts == 0).sum())}}
+                            "empty": int((counts == 0).sum())},
+            **counter_fields(cnt.get("moe_prefill_t2048_e384"))}
     if "mla" in work:
         ms = min(K, 256)
         msec, mstats = bench_mla(torch, ms, min(W, 32), dev)
@@ -688,7 +789,8 @@ def main():
         line["mla_decode"] = {"us": round(mus, 2), "GB/s": round(mgbs, 1),
                               "pct_hbm_peak": round(100 * mgbs / HBM_PEAK_GBS, 1), "bytes": MLA_BYTES,
                               "heads": MLA_H, "tokens": MLA_T, "kv_lora_rank": 512, "rope": 64,
-                              "cache": "bf16", "launches": 3, "step_us": mstats}
+                              "cache": "bf16", "launches": 4, "step_us": mstats,
+                              **counter_fields(cnt.get("mla_decode_h64_t32768"))}
     if "mlastep" in work:
         ms_ = min(K, 128)
         ssec, sstats = bench_mla_step(torch, ms_, min(W, 16), dev)
@@ -696,7 +798,7 @@ def main():
         sgbs = MS_BYTES / (sus * 1e-6) / 1e9
         line["mla_step"] = {"us": round(sus, 2), "GB/s": round(sgbs, 1), "pct_hbm_peak": round(100 * sgbs / HBM_PEAK_GBS, 1),
                             "bytes": MS_BYTES, "hidden": MS_HID, "q_lora_rank": MS_QL, "heads": MLA_H,
-                            "tokens": MLA_T, "weights": "bf16", "output_gate": True, "launches": 6,
+                            "tokens": MLA_T, "weights": "bf16", "output_gate": True, "launches": 7,
                             "step_us": sstats}
     if "kda" in work:
         ks_ = min(K, 256)
@@ -738,6 +840,11 @@ def main():
         gus = gsec / K * 1e6
         line["gemv"] = {"us": round(gus, 3), "GB/s": round(GEMV_BYTES / (gus * 1e-6) / 1e9, 1),
                         "shape": [I, H], "x": "bf16", "out": "bf16", "bytes": GEMV_BYTES, "step_us": gstats}
+        if "ceiling" in work:
+            cg = bench_read_ceiling(torch, GEMV_BYTES, 256, dev)
+            line["gemv"]["read_ceiling_us"] = round(cg * 1e6, 3)
+            line["gemv"]["read_ceiling_GB/s"] = round(GEMV_BYTES / cg / 1e9, 1)
+            line["gemv"]["pct_of_measured_read"] = round(100 * cg * 1e6 / gus, 1)
     if not args.no_cpu:
         cpu = bench_cpu(args.cpu_seconds)
         line["cpu_baseline"] = cpu
