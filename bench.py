@@ -644,6 +644,12 @@ def bench_cpu(sample_s=12.0):
     n = len(os.sched_getaffinity(0))
     torch.set_num_threads(n)
     out = cpu_baseline.time_expert(H, I, sample_s=sample_s, threads=n)
+    one = cpu_baseline.time_expert(H, I, sample_s=sample_s / 4, threads=1)
+    out["single_thread"] = {k: one[k] for k in ("value", "unit", "cores", "ms_per_expert", "matmul_only_GB/s",
+                                                "matmul_only_ms", "sample")}
+    out["projection"] = cpu_baseline.time_projection(I, H, sample_s=sample_s / 6, threads=n)
+    out["projection_single_thread"] = cpu_baseline.time_projection(I, H, sample_s=sample_s / 6, threads=1)
+    torch.set_num_threads(n)
     out["moe_layer"] = cpu_baseline.time_layer(H, I, E_LAYER, TOPK, sample_s=sample_s / 2, threads=n)
     out["mla_decode"] = cpu_baseline.time_mla(MLA_H, MLA_T, sample_s=sample_s / 3, threads=n)
     return out

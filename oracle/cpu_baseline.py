@@ -161,3 +161,31 @@ def time_mla(H: int, T: int, sample_s: float = 4.0, threads: int | None = None, 
     t, n = _run(core, sample_s)
     return {"ms": round(t * 1e3, 2), "calls": n, "cores": threads,
             "sample": f"{n} calls of the absorbed core, {H} heads over {T} bf16 cache rows (fp32 upcast per call), median"}
+
+
+def time_projection(N: int, K: int, sample_s: float = 3.0, threads: int | None = None, seed: int = 1001) -> dict:
+    """One MXFP4 projection y = x W^T (C1), the reference's own one-projection timing
+    (tests/test_mxfp4_kernel.py:87-119): decode on every call (k3ref) then one fp32 matvec,
+    plus the matvec alone on pre-decoded weights."""
+    import torch
+
+    threads = threads or len(os.sched_getaffinity(0))
+    torch.set_num_threads(threads)
+    rng = np.random.default_rng(seed)
+    packed, scales = random_mxfp4(rng, N, K)
+    x = torch.from_numpy(bf16_round(rng.standard_normal((1, K)).astype(np.float32)))
+    nbytes = packed.nbytes + scales.nbytes
+
+    def faithful():
+        return x @ torch.from_numpy(decode_mxfp4(packed, scales)).T
+
+    Wd = torch.from_numpy(decode_mxfp4(packed, scales))
+
+    def matmul_only():
+        return x @ Wd.T
+
+    t_f, n_f = _run(faithful, sample_s * 0.75)
+    t_m, n_m = _run(matmul_only, sample_s * 0.25)
+    return {"ms": round(t_f * 1e3, 3), "GB/s": round(nbytes / t_f / 1e9, 3), "calls": n_f, "cores": threads,
+            "matmul_only_ms": round(t_m * 1e3, 4), "matmul_only_GB/s": round(nbytes / t_m / 1e9, 3),
+            "sample": f"{n_f} calls of one [{N} x {K}] projection (decode + fp32 matvec), median"}
