@@ -73,29 +73,6 @@ __device__ __forceinline__ float group_dot(const uint4 w, const float4 *xc) {
 template <typename XT>
 using XChunk = typename std::conditional<std::is_same<XT, float>::value, float4, uint4>::type;
 
-// E8M0 bytes staged per wave.  A wave needs the scale bytes of NS row slices (slice s: SW
-// consecutive bytes from byte offset off_s of a scale matrix).  One byte load per (row, group)
-// makes a 64-byte request per wave instruction, as many instructions as weight loads; instead
-// lane l < NS * kCPR loads the 16-byte chunk l % kCPR of slice l / kCPR (chunks start at
-// off_s rounded down to 16, hence one extra chunk), the wave stores its chunks in its own LDS
-// area, and every lane reads its bytes there (consecutive lanes read consecutive bytes).
-template <int SW>
-struct ScaleStage {
-    static constexpr int kCPR = SW / 16 + 1;  // 16-byte chunks per slice
-    __device__ static int slice_of(int lane) { return lane / kCPR; }
-    // byte offset (in the scale matrix) of the chunk `lane` loads for a slice at `off`
-    __device__ static uint32_t chunk_off(uint32_t off, int lane) { return (off & ~15u) + 16u * (lane % kCPR); }
-    // byte offset, in the wave's LDS area, of byte j of slice s (slice at `off`)
-    __device__ static uint32_t at(int s, uint32_t off, int j) { return s * (kCPR * 16) + (off & 15u) + j; }
-};
-
-// Buffer resource over a scale matrix of `bytes` bytes whose base is rounded down to 16, so
-// that every chunk load is 16-byte aligned; `mis` (0..15) is added to every byte offset.
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_scale_rsrc(const void *scales, uint32_t bytes, uint32_t &mis) {
-    mis = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(scales) & 15u);
-    return make_rsrc(static_cast<const uint8_t *>(scales) - mis, bytes + mis);
-}
-
 // Stage n_chunks 16-byte activation chunks of one token into the swizzled LDS tile.
 template <typename XT>
 __device__ __forceinline__ void stage_x_tile(uint4 *xs, const void *x, int n_chunks) {
