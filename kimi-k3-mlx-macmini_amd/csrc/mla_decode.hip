@@ -15,15 +15,13 @@
 //       (hi = rne(qa), lo = rne(qa - hi)), together with q_rot in columns 512..575, so the
 //       score contraction is one K = 576 product against the [lat | rot] cache rows.
 //   A   split-T flash decoding.  A block owns 16 heads and a contiguous token range (one
-//       block per CU); its wave pairs are independent streams over interleaved 16-token
-//       steps, the two waves of a pair splitting the score contraction and the context
-//       columns in halves.  Cache rows go HBM -> registers (MFMA operand layout, a ring of
-//       buffers) -> a wave-private LDS copy for the transposed context operand.  Scores
-//       S^T[16 tokens x 16 heads] come from bf16 MFMAs (v_mfma_f32_16x16x32_bf16) of the
-//       rows against the hi and the lo half of qa; the pair adds its partials across one
-//       barrier; a base-2 softmax turns them into P, split again into a bf16 hi/lo pair;
-//       ctx^T += rows^T [P_hi; P_lo] on the same MFMA.  The streams merge in the block,
-//       which writes its unnormalised (ctx, max, sum) record per head.
+//       block per CU, eight waves).  Cache rows arrive as whole 1 KB rows per load
+//       instruction into an LDS ring; four score waves take S^T[16 tokens x 16 heads] as bf16
+//       MFMAs (v_mfma_f32_16x16x32_bf16) of the rows against the hi and the lo half of qa,
+//       in K halves that meet through LDS, and a base-2 softmax turns them into P, split
+//       again into a bf16 hi/lo pair; four context waves take ctx^T += rows^T [P_hi; P_lo]
+//       on the same MFMA from transposed LDS reads.  The two tile classes merge in the
+//       block, which writes its unnormalised (ctx, max, sum) record per head.
 //   M   per (head, quarter of the latent columns): log-sum-exp merge of the split records
 //       in a fixed order into the normalised ctx, then the W_UV product over that quarter,
 //       o_q = W_UV[h][:, quarter] @ ctx[h][quarter] in fp32; every record and W_UV element is
@@ -182,57 +180,60 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
     return __builtin_bit_cast(uint32_t, v);
 }
 
-// Block: 16 heads x one split of Ts tokens, run by P pairs of waves.  Pair p is one
-// flash-decoding stream over the 16-token steps p, p + P, p + 2P, ... of the split; its two
-// waves split the score contraction and the context columns in halves:
-//   wave j of the pair owns latent columns 256 j .. +256 and rope columns 32 j .. +32.
-// Per step and wave:
-//   load    its 9 column blocks of the 16 cache rows straight into MFMA operand layout
-//           (lane (token r16, group q4) holds 8 consecutive columns of its row per block),
-//           into a ring of RING register buffers, so RING - 1 steps are in flight
-//   scores  partial S^T[token][head] = rows . qa over its columns (A = cache rows, B = qa hi
-//           and lo, which stay in registers); the two partials meet through LDS across one
-//           block barrier, and both waves add them in the same order, so both hold
-//           identical scores.  Lane (head r16, q4) has tokens 4 q4 .. +3.
-//   softmax per lane over its 4 tokens, the max reduced over the 4 lane rows; identical in
-//           the two waves.  The max used for the exponentials moves only at the first step
-//           of a pass; a later score above it by more than kSlack restarts the pass (of the
-//           whole block, so every wave meets the same barriers).
-//   ctx     ctx^T[col][head] += rows^T . P on the 16x16x32 bf16 MFMA with k-slots 0..3 =
-//           P_hi and 4..7 = P_lo of the lane's own 4 tokens, so P needs no data movement;
-//           the transposed rows come from a wave-private LDS copy via ds_read_b64_tr_b16,
-//           duplicated into both k halves.  Lane (head r16, q4) accumulates ctx[head][256 j
-//           + 16 n + 4 q4 .. +3] for its 16 column tiles n.
-// The P streams meet once, in the final in-block merge.
-constexpr int kStepT = 16;              // tokens per step
-constexpr int kHalfK = 9;               // column blocks (of 32) per wave: 8 latent + 1 rope
-constexpr int kHalfCols = kR / 2;       // latent columns per wave
-constexpr int kCopyRow = kHalfCols + 8; // padded LDS row of the wave's copy (528 B)
-constexpr size_t kCopyBytes = kStepT * kCopyRow * 2;  // 8448 B per wave and slot
-constexpr float kSlack = 64.f;          // log2 headroom before the pass restarts
-constexpr int kMaxPairs = 4;
-constexpr int kTrBatch = 16;            // transposed reads issued ahead of their products
-constexpr int kCsRow = kR + 4;          // padded LDS row of the merged context (floats)
+typedef short s4_t __attribute__((ext_vector_type(4)));
 
-template <int P>
-constexpr size_t attn_lds_bytes() {  // two copy slots per wave; the merge reuses them
-    return 2 * P * 2 * kCopyBytes;
-}
+// Block: 16 heads x one split of Ts tokens, eight waves (two per SIMD) in two roles.  The
+// split is walked in rounds of two 16-token tiles; tile c of a round belongs to tile class c.
+//   staging (all waves): the round's latent rows arrive one whole 1 KB row per load
+//           instruction (whole 128-byte lines), through registers (D rounds in flight) into
+//           an LDS ring of four rounds, rows padded (kLatStride) for the operand reads.
+//   score waves (0..3), class c = w / 2, half h = w % 2: the partial S^T[token][head] of tile
+//           c over latent columns 256 h .. +256 and rope columns 32 h .. +32, on 16x16x32 bf16
+//           MFMAs (A = the staged rows read with ds_read_b128, rope rows loaded directly in
+//           operand layout; B = qa hi and lo for those columns, in registers for the whole
+//           split), four accumulator chains.  The two halves' partials meet through LDS; both
+//           waves add them in the same order, so both hold identical scores.  Lane (head r16,
+//           q4) holds tokens 4 q4 .. +3.  Softmax per lane over its 4 tokens, the max reduced
+//           over the 4 lane rows; each head keeps a reference max per class: exponentials
+//           are 2^(s - ref) <= 2^kSlack, and a score above the reference by more than kSlack
+//           (log2 units) moves it, with the factor 2^(old - new) for the accumulators.  P
+//           (hi/lo bf16, in the B-operand layout) and the factors go to LDS.
+//   context waves (4..7), class c, half h: ctx^T[col][head] += rows^T . [P_hi; P_lo] over
+//           latent columns 256 h .. +256 of tile c on the 16x16x32 MFMA, k-slots 0..3 = P_hi
+//           and 4..7 = P_lo of the lane's own 4 tokens; the transposed rows come from the
+//           staged tile (ds_read_b64_tr_b16), duplicated into both k halves.
+// One barrier per round: in iteration r the score waves finish round r's softmax and start
+// round r + 1's partial scores, while the context waves take round r - 1's products.  At the
+// end the two classes merge (common reference, fixed order) and the block writes its
+// unnormalised context per head and (reference max, sum) for the merge kernel.
+constexpr int kStepT = 16;                          // tokens per tile
+constexpr int kLatStride = 1056;                    // LDS bytes per staged latent row (1024 + 32)
+constexpr int kTileLds = kStepT * kLatStride;       // 16896 B per staged tile
+constexpr int kRoundTiles = 2;                      // tiles per round (tile classes)
+constexpr int kRoundLds = kRoundTiles * kTileLds;
+constexpr int kSlots = 4;                           // staged rounds in LDS
+constexpr int kChunks = kRoundTiles * kStepT;       // 1 KB row loads per round
+constexpr int kPerWave = (kChunks + 7) / 8;         // row loads per wave and round
+constexpr int kHalfKb = kR / 64;                    // latent k-blocks (of 32) per score half: 8
+constexpr int kColTiles = kR / 2 / 16;              // context column tiles per context wave: 16
+constexpr float kSlack = 64.f;                      // log2 headroom before a reference moves
+constexpr size_t kAttnLds = static_cast<size_t>(kSlots) * kRoundLds;  // 135168 B
+static_assert(static_cast<size_t>(kHG) * kR * 4 <= kAttnLds, "class merge staging fits");
 
-template <int P, int RING>
-__global__ __launch_bounds__(128 * P, 1) void mla_attn_kernel(AttnArgs a) {
-    static_assert(P == 2 || P == 4, "pairs per block");
-    static_assert(attn_lds_bytes<P>() >= static_cast<size_t>(P / 2) * 2 * 16 * 64 * 16, "merge buffers fit");
-    static_assert(attn_lds_bytes<P>() >= static_cast<size_t>(kHG) * kCsRow * 4, "context staging fits");
+template <int D>
+__global__ __launch_bounds__(512, 1) void mla_attn_kernel(AttnArgs a) {
+    static_assert(D >= 2, "rounds 0 and 1 are staged from two register slots");
     extern __shared__ uint4 smem[];
-    __shared__ f32x4_t xs[P][2][2][64];  // partial scores: [pair][member][slot][lane]
-    __shared__ int req[2];                         // restart requests by step parity (pass number)
-    __shared__ float m_s[P][kHG], l_s[P][kHG];
+    __shared__ f32x4_t xs[2][kRoundTiles][2][64];   // partial scores [parity][class][half][lane]
+    __shared__ uint4 xp[2][kRoundTiles][64];        // P hi/lo [parity][class][lane]
+    __shared__ float xf[2][kRoundTiles][kHG];       // rescale factors [parity][class][head]
+    __shared__ float2 xm[kRoundTiles][kHG];         // final (reference, sum) [class][head]
+    char *lds = reinterpret_cast<char *>(smem);
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int pr = wave >> 1, j = wave & 1;
+    const bool ctx_role = wave >= 4;
+    const int cls = (wave & 3) >> 1, half = wave & 1;
     const int r16 = lane & 15, q4 = lane >> 4;
-    uint16_t *copy = reinterpret_cast<uint16_t *>(reinterpret_cast<char *>(smem) + wave * 2 * kCopyBytes);
 
     // blocks b, b+8, b+16, ... share an XCD (and its L2): give them consecutive work items,
     // so the head groups of one split read the same rows through one L2
@@ -243,232 +244,232 @@ __global__ __launch_bounds__(128 * P, 1) void mla_attn_kernel(AttnArgs a) {
     const int h0 = hg * kHG;
     const int t_begin = split * a.Ts;
     const int t_end = min(a.T, t_begin + a.Ts);
-    // every pair runs the block's step count (pair 0's): a step past a pair's tokens is all
-    // masked and adds nothing, and the barriers of all waves stay matched
-    const int nsteps = (t_end - t_begin + P * kStepT - 1) / (P * kStepT);
+    const int nsteps = (t_end - t_begin + kStepT - 1) / kStepT;   // tiles of the split
+    const int nrounds = (nsteps + kRoundTiles - 1) / kRoundTiles;
+    const int nloop = (nrounds + 1 + D - 1) / D * D;              // one more for the context waves
+    auto slot = [&](int rd) { return lds + (rd % kSlots) * kRoundLds; };
 
-    if (tid < 2) req[tid] = 0;
-
+    // ---- staging, all eight waves: row load q = wave + 8 i of a round (tile q / 16, row
+    // q % 16); tiles and rows past the split load zeros (out-of-range offsets), so every
+    // round issues the same loads
     const auto rl = make_rsrc(a.lat, a.lat_bytes);
-    const auto rr = make_rsrc(a.rot, a.rot_bytes);
-    // Steps past nsteps and rows past T load zeros (out-of-range offsets), so every step
-    // issues the same loads and the ring needs no guard; masked rows score -inf.
-    auto load = [&](uint4(&buf)[kHalfK], int st) {
-        const int t = t_begin + (st * P + pr) * kStepT + r16;
-        const bool ok = t < t_end;
-        const uint32_t ol = ok ? static_cast<uint32_t>(t) * a.lat_row_bytes + (j * kHalfCols + q4 * 8) * 2u : kOobOffset;
-        const uint32_t orr = ok ? static_cast<uint32_t>(t) * a.rot_row_bytes + (j * 32 + q4 * 8) * 2u : kOobOffset;
+    auto load_round = [&](uint4 (&g)[kPerWave], int rd) {
 #pragma unroll
-        for (int k = 0; k < kHalfK - 1; ++k) buf[k] = buf_load16(rl, ol + k * 64u);
-        buf[kHalfK - 1] = buf_load16(rr, orr);
-    };
-    // qa operands of head h0 + r16 over this wave's columns (heads past H load zeros),
-    // issued before the ring so that waiting for a ring buffer also covers them
-    bf16x8 qhi[kHalfK], qlo[kHalfK];
-    {
-        const uint32_t qbytes = static_cast<uint32_t>(a.H) * kQaLd * 2;
-        const auto rqh = make_rsrc(a.qa_hi, qbytes), rql = make_rsrc(a.qa_lo, qbytes);
-        const uint32_t qrow = h0 + r16 < a.H ? static_cast<uint32_t>((h0 + r16) * kQaLd + q4 * 8) * 2 : kOobOffset;
-#pragma unroll
-        for (int k = 0; k < kHalfK; ++k) {
-            const uint32_t col = k < kHalfK - 1 ? j * kHalfCols + k * 32 : kR + j * 32;
-            qhi[k] = __builtin_bit_cast(bf16x8, buf_load16(rqh, qrow + col * 2));
-            qlo[k] = __builtin_bit_cast(bf16x8, buf_load16(rql, qrow + col * 2));
+        for (int i = 0; i < kPerWave; ++i) {
+            const int q = wave + 8 * i;
+            const int tile = rd * kRoundTiles + q / kStepT;
+            const int t = t_begin + tile * kStepT + q % kStepT;
+            const bool ok = q < kChunks && tile < nsteps && t < t_end;
+            g[i] = buf_load16(rl, ok ? static_cast<uint32_t>(t) * a.lat_row_bytes + lane * 16u : kOobOffset);
         }
-    }
-    uint4 buf[RING][kHalfK];
-
-    __syncthreads();  // requests cleared
-
-    f32x4_t cacc[kHalfCols / 16];
+    };
+    auto store_round = [&](const uint4 (&g)[kPerWave], int rd) {
+        char *base = slot(rd);
 #pragma unroll
-    for (int n = 0; n < kHalfCols / 16; ++n) cacc[n] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-    float m_used = -INFINITY, l_run = 0.f;
-    int pass = 0;  // restarts so far (block-uniform)
+        for (int i = 0; i < kPerWave; ++i) {
+            const int q = wave + 8 * i;
+            if (q < kChunks)
+                *reinterpret_cast<uint4 *>(base + (q / kStepT) * kTileLds + (q % kStepT) * kLatStride + lane * 16) = g[i];
+        }
+    };
+    uint4 stg[D][kPerWave];
+    load_round(stg[0], 0);
+    load_round(stg[1], 1);
+    store_round(stg[0], 0);
+    store_round(stg[1], 1);
+#pragma unroll
+    for (int d = 0; d < D; ++d) load_round(stg[(2 + d) % D], 2 + d);
 
-    // transposed-read source of this lane: row 4 q4 + r16 / 4, columns 4 (r16 % 4) .. +3
-    typedef short s4_t __attribute__((ext_vector_type(4)));
+    float *cs = reinterpret_cast<float *>(lds);  // class 1's scaled context at the end, [16][kR]
     typedef __attribute__((address_space(3))) s4_t *lds_s4;
-    const uint16_t *tsrc = copy + (q4 * 4 + (r16 >> 2)) * kCopyRow + (r16 & 3) * 4;
-    uint16_t *tdst = copy + r16 * kCopyRow + q4 * 8;
 
-    // A step is split in two halves, software-pipelined one step apart: the front half of
-    // step st + 1 (LDS copy, score products, refill of its buffer) is issued before the back
-    // half of step st (exchange across the barrier, softmax, context products), so the
-    // score products run on the matrix cores while the wave waits at the barrier and works
-    // through the softmax.  The LDS copy has two slots (step parity): the front half writes
-    // one while the back half reads the other.
-    // A wave whose scores exceed its max by more than kSlack accumulates nothing from that
-    // step on and posts a restart request; every wave sees it after the next barrier and
-    // skips the rest of the pass too.
-    bool again = false;
-    f32x4_t mine = {0.f, 0.f, 0.f, 0.f};  // this wave's partial scores of the pending step
-    auto front = [&](uint4(&bf)[kHalfK], int st) -> f32x4_t {
-        // ---- partial scores over this wave's columns: hi and lo chains
-        f32x4_t s0 = {0.f, 0.f, 0.f, 0.f}, s1 = s0;
+    if (!ctx_role) {
+        // ================= score waves
+        // qa operands of head h0 + r16 over this half's columns (heads past H load zeros):
+        // latent k-blocks 8 half .. +8 and rope k-block half
+        bf16x8 qhi[kHalfKb + 1], qlo[kHalfKb + 1];
+        {
+            const uint32_t qbytes = static_cast<uint32_t>(a.H) * kQaLd * 2;
+            const auto rqh = make_rsrc(a.qa_hi, qbytes), rql = make_rsrc(a.qa_lo, qbytes);
+            const uint32_t qrow = h0 + r16 < a.H ? static_cast<uint32_t>((h0 + r16) * kQaLd) * 2u : kOobOffset;
 #pragma unroll
-        for (int k = 0; k < kHalfK; ++k) {
-            const bf16x8 rk = __builtin_bit_cast(bf16x8, bf[k]);
-            s0 = mfma_bf16(rk, qhi[k], s0);
-            s1 = mfma_bf16(rk, qlo[k], s1);
+            for (int k = 0; k <= kHalfKb; ++k) {
+                const int col = k < kHalfKb ? (half * kHalfKb + k) * 32 + q4 * 8 : kR + half * 32 + q4 * 8;
+                qhi[k] = __builtin_bit_cast(bf16x8, buf_load16(rqh, qrow + static_cast<uint32_t>(col) * 2u));
+                qlo[k] = __builtin_bit_cast(bf16x8, buf_load16(rql, qrow + static_cast<uint32_t>(col) * 2u));
+            }
         }
-        // ---- latent columns of the rows -> the wave's LDS copy slot st & 1 (read last by
-        // step st - 2, earlier in program order), then refill the buffer RING steps ahead
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        uint16_t *dst = tdst + (st & 1) * (kCopyBytes / 2);
+        // rope operand of a round's tile, loaded straight into operand layout (lane (token
+        // r16, q4): 16 bytes of the row at rope column 32 half + 8 q4), D rounds ahead
+        const auto rr = make_rsrc(a.rot, a.rot_bytes);
+        auto load_rope = [&](int rd) -> uint4 {
+            const int tile = rd * kRoundTiles + cls;
+            const int t = t_begin + tile * kStepT + r16;
+            const bool ok = tile < nsteps && t < t_end;
+            return buf_load16(rr, ok ? static_cast<uint32_t>(t) * a.rot_row_bytes + (half * 32 + q4 * 8) * 2u
+                                     : kOobOffset);
+        };
+        // ring of D: slot s holds the round r with r % D == s; round 0 separately
+        uint4 rope[D];
 #pragma unroll
-        for (int k = 0; k < kHalfK - 1; ++k) *reinterpret_cast<uint4 *>(dst + k * 32) = bf[k];
-        load(bf, st + RING);
-        return s0 + s1;
-    };
-    auto back = [&](int st) {
-        // ---- exchange the partials with the pair partner (slots alternate by step, so a
-        // write never meets the partner's read of the previous step)
-        const int slot = st & 1;
-        xs[pr][j][slot][lane] = mine;
-        __syncthreads();
-        again = again || req[slot] > pass;  // requests of step st - 1 are visible here
-        if (again) return;
-        const f32x4_t other = xs[pr][j ^ 1][slot][lane];
-        const f32x4_t sc = j == 0 ? mine + other : other + mine;
+        for (int d = 1; d <= D; ++d) rope[d % D] = load_rope(d);
+        const uint4 rope0 = load_rope(0);
 
-        // ---- softmax weights of this lane's tokens 4 q4 .. +3 of head r16
-        const int tb = t_begin + (st * P + pr) * kStepT + q4 * 4;
-        float s[4];
-        float mt = -INFINITY;
+        float m_ref = -INFINITY, l_run = 0.f;  // head h0 + r16, class cls (both halves alike)
+        // partial scores of round rd over this half's columns
+        auto partial = [&](int rd, const uint4 &rp) -> f32x4_t {
+            const char *arow = slot(rd) + cls * kTileLds + r16 * kLatStride + half * 512 + q4 * 16;
+            auto rdk = [&](int k) { return __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4 *>(arow + k * 64)); };
+            f32x4_t s0 = {0.f, 0.f, 0.f, 0.f}, s1 = s0, s2 = s0, s3 = s0;
+            bf16x8 c[kHalfKb];
 #pragma unroll
-        for (int v = 0; v < 4; ++v) {
-            s[v] = tb + v < t_end ? sc[v] * a.scale_log2 : -INFINITY;
-            mt = fmaxf(mt, s[v]);
-        }
-        mt = rows4_max(mt);  // -inf only for a step past the pair's tokens
-        if (__any(mt > m_used + kSlack)) {
-            m_used = fmaxf(m_used, mt);
-            if (st != 0) {  // earlier steps used a smaller max: the block restarts
-                req[slot ^ 1] = pass + 1;
-                again = true;
-                return;
+            for (int k = 0; k < 4; ++k) c[k] = rdk(k);
+#pragma unroll
+            for (int k = 0; k < kHalfKb; k += 2) {
+                if (k + 4 < kHalfKb) {
+                    c[k + 4] = rdk(k + 4);
+                    c[k + 5] = rdk(k + 5);
+                }
+                s0 = mfma_bf16(c[k], qhi[k], s0);
+                s1 = mfma_bf16(c[k], qlo[k], s1);
+                s2 = mfma_bf16(c[k + 1], qhi[k + 1], s2);
+                s3 = mfma_bf16(c[k + 1], qlo[k + 1], s3);
+                __builtin_amdgcn_sched_barrier(0);
+            }
+            const bf16x8 rk = __builtin_bit_cast(bf16x8, rp);
+            s0 = mfma_bf16(rk, qhi[kHalfKb], s0);
+            s1 = mfma_bf16(rk, qlo[kHalfKb], s1);
+            return (s0 + s2) + (s1 + s3);
+        };
+        // softmax of round rd from the two halves' partials; half 0 publishes P and factors
+        auto softmax = [&](int rd) {
+            const f32x4_t sc = xs[rd & 1][cls][0][lane] + xs[rd & 1][cls][1][lane];
+            const int tbeg = t_begin + (rd * kRoundTiles + cls) * kStepT + q4 * 4;
+            float sv[4];
+            float mt = -INFINITY;
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                sv[v] = tbeg + v < t_end ? sc[v] * a.scale_log2 : -INFINITY;
+                mt = fmaxf(mt, sv[v]);
+            }
+            mt = rows4_max(mt);  // this head's max over the tile; -inf for a fully masked tile
+            float f = 1.f;
+            if (__any(mt > m_ref + kSlack)) {
+                const float m_new = mt > m_ref + kSlack ? mt : m_ref;
+                if (m_new != m_ref) {
+                    f = m_ref == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m_ref - m_new);
+                    l_run *= f;
+                    m_ref = m_new;
+                }
+            }
+            // p <= 2^kSlack; exponents below -126 flush to 0, far below the head's largest p.
+            // Before the class's first token of the head the reference is -inf and every p is 0.
+            const float mref = m_ref == -INFINITY ? 0.f : m_ref;
+            uint32_t pw[4];
+#pragma unroll
+            for (int v = 0; v < 4; v += 2) {
+                const float p0 = __builtin_amdgcn_exp2f(sv[v] - mref), p1 = __builtin_amdgcn_exp2f(sv[v + 1] - mref);
+                l_run += p0 + p1;
+                const uint32_t hi = pack_bf16x2(p0, p1);
+                pw[v / 2] = hi;
+                pw[2 + v / 2] = pack_bf16x2(p0 - __uint_as_float(hi << 16), p1 - __uint_as_float(hi & 0xffff0000u));
+            }
+            if (half == 0) {
+                xp[rd & 1][cls][lane] = make_uint4(pw[0], pw[1], pw[2], pw[3]);
+                if (q4 == 0) xf[rd & 1][cls][r16] = f;
+            }
+        };
+        __syncthreads();  // rounds 0 and 1 staged
+        xs[0][cls][half][lane] = partial(0, rope0);
+        __syncthreads();  // partials of round 0 published
+        for (int r0 = 0; r0 < nloop; r0 += D) {
+#pragma unroll
+            for (int d = 0; d < D; ++d) {
+                const int rd = r0 + d;
+                store_round(stg[(d + 2) % D], rd + 2);
+                load_round(stg[(d + 2) % D], rd + 2 + D);
+                // round rd + 1's rope sits in rope[(rd + 1) % D] (r0 is a multiple of D)
+                const int rs = (d + 1) % D;
+                const f32x4_t pnext = partial(rd + 1, rope[rs]);
+                softmax(rd);
+                xs[(rd + 1) & 1][cls][half][lane] = pnext;
+                rope[rs] = load_rope(rd + 1 + D);
+                __syncthreads();
             }
         }
-        // p <= 2^kSlack; exponents below -126 flush to 0, far below the step's largest p.
-        // Before the pair's first token the max is -inf and every p is 0.
-        const float mref = m_used == -INFINITY ? 0.f : m_used;
-        uint32_t pw[4];
-#pragma unroll
-        for (int v = 0; v < 4; v += 2) {
-            const float p0 = __builtin_amdgcn_exp2f(s[v] - mref), p1 = __builtin_amdgcn_exp2f(s[v + 1] - mref);
-            l_run += p0 + p1;
-            const uint32_t hi = pack_bf16x2(p0, p1);
-            pw[v / 2] = hi;
-            pw[2 + v / 2] = pack_bf16x2(p0 - __uint_as_float(hi << 16), p1 - __uint_as_float(hi & 0xffff0000u));
+        // (reference, sum) per class and head; wave 0 merges the classes and writes them
+        const float l_tot = rows4_sum(l_run);
+        if (half == 0 && q4 == 0) xm[cls][r16] = make_float2(m_ref, l_tot);
+        __syncthreads();  // xm complete
+        if (wave == 0 && q4 == 0 && h0 + r16 < a.H) {
+            const float2 v = xm[0][r16], o = xm[1][r16];
+            const float M = fmaxf(v.x, o.x);
+            const float f0 = v.x == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(v.x - M);
+            const float f1 = o.x == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(o.x - M);
+            a.ml[static_cast<int64_t>(split) * a.H + h0 + r16] = make_float2(M, v.y * f0 + o.y * f1);
         }
-        const bf16x8 pb = __builtin_bit_cast(bf16x8, make_uint4(pw[0], pw[1], pw[2], pw[3]));
-
-        // ---- ctx^T += rows^T . [P_hi; P_lo] over this wave's columns; all transposed
-        // reads are issued before the first product, so their latencies overlap
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-        const uint16_t *src = tsrc + slot * (kCopyBytes / 2);
+        __syncthreads();  // class 1's context staged
+    } else {
+        // ================= context waves
+        f32x4_t cacc[kColTiles];
 #pragma unroll
-        for (int n0 = 0; n0 < kHalfCols / 16; n0 += kTrBatch) {
-            s4_t t4[kTrBatch];
+        for (int n = 0; n < kColTiles; ++n) cacc[n] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+        __syncthreads();  // rounds 0 and 1 staged
+        __syncthreads();  // partials of round 0 published
+        for (int r0 = 0; r0 < nloop; r0 += D) {
 #pragma unroll
-            for (int n = 0; n < kTrBatch; ++n)
-                t4[n] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4)(src + (n0 + n) * 16));
-            __builtin_amdgcn_sched_barrier(0);
+            for (int d = 0; d < D; ++d) {
+                const int rd = r0 + d;
+                store_round(stg[(d + 2) % D], rd + 2);
+                load_round(stg[(d + 2) % D], rd + 2 + D);
+                if (rd >= 1) {
+                    // P and factors of round rd - 1 (published in the previous iteration)
+                    const int pr = (rd - 1) & 1;
+                    const bf16x8 pb = __builtin_bit_cast(bf16x8, xp[pr][cls][lane]);
+                    const float fj = xf[pr][cls][r16];
+                    if (__any(fj != 1.f)) {
 #pragma unroll
-            for (int n = 0; n < kTrBatch; ++n) {
-                const bf16x8 ra = __builtin_bit_cast(bf16x8, __builtin_shufflevector(t4[n], t4[n], 0, 1, 2, 3, 0, 1, 2, 3));
-                cacc[n0 + n] = mfma_bf16(ra, pb, cacc[n0 + n]);
+                        for (int n = 0; n < kColTiles; ++n) cacc[n] *= fj;
+                    }
+                    const char *tsrc = slot(rd - 1) + cls * kTileLds + (q4 * 4 + (r16 >> 2)) * kLatStride +
+                                       (half * (kR / 2) + (r16 & 3) * 4) * 2;
+                    constexpr int kTrAhead = 8;  // transposed reads in flight ahead of the products
+                    s4_t t4[kTrAhead];
+#pragma unroll
+                    for (int n = 0; n < kTrAhead; ++n)
+                        t4[n] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4)(tsrc + n * 32));
+#pragma unroll
+                    for (int n = 0; n < kColTiles; ++n) {
+                        const s4_t cur = t4[n % kTrAhead];
+                        if (n + kTrAhead < kColTiles)
+                            t4[n % kTrAhead] =
+                                __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4)(tsrc + (n + kTrAhead) * 32));
+                        const bf16x8 ra =
+                            __builtin_bit_cast(bf16x8, __builtin_shufflevector(cur, cur, 0, 1, 2, 3, 0, 1, 2, 3));
+                        cacc[n] = mfma_bf16(ra, pb, cacc[n]);
+                        __builtin_amdgcn_sched_barrier(0);
+                    }
+                }
+                __syncthreads();
             }
         }
-    };
-    // The max used by the exponentials (per head) is set by the first step of a pass and
-    // only moves when a score exceeds it by more than kSlack (log2 units).  Then the block
-    // restarts the pass from its first step, the triggering pair with its larger max, so the
-    // accumulators are never rescaled inside the loop.  A restarted pass does not trigger
-    // again on the steps before the trigger, so a block makes at most nsteps + 1 passes.
-    // The trip loop runs whole trips of RING steps (steps past the split are all masked)
-    // and has no other exit, so the waits at its top see the ring in steady-state order.
-    for (;;) {
-        // in buffer order (the trip loop waits for buffer r behind the loads of the others)
+        __syncthreads();  // xm complete; every wave is done with the staged tiles
+        const float mc = xm[cls][r16].x, mo = xm[1 - cls][r16].x;
+        const float M = fmaxf(mc, mo);  // -inf only if neither class saw a token
+        const float fc = mc == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mc - M);
+        float *crow = cs + r16 * kR + half * (kR / 2) + 4 * q4;
+        if (cls == 1) {
 #pragma unroll
-        for (int r = 0; r < RING; ++r) {
-            load(buf[r], r);
-            __builtin_amdgcn_sched_barrier(0);
+            for (int n = 0; n < kColTiles; ++n) *reinterpret_cast<f32x4_t *>(crow + 16 * n) = cacc[n] * fc;
         }
-        again = false;
-        mine = front(buf[0], 0);
-        for (int st = 0; st < nsteps; st += RING) {
+        __syncthreads();  // class 1's context staged
+        if (cls == 0 && h0 + r16 < a.H) {
+            float *rec = a.part + (static_cast<int64_t>(split) * a.H + h0 + r16) * kR + half * (kR / 2) + 4 * q4;
 #pragma unroll
-            for (int r = 0; r < RING; ++r) {
-                const f32x4_t next = front(buf[(r + 1) % RING], st + r + 1);
-                back(st + r);
-                mine = next;
-            }
+            for (int n = 0; n < kColTiles; ++n)
+                *reinterpret_cast<f32x4_t *>(rec + 16 * n) =
+                    cacc[n] * fc + *reinterpret_cast<const f32x4_t *>(crow + 16 * n);
         }
-        __syncthreads();  // publishes a request made in the last step
-        if (max(req[0], req[1]) <= pass) break;  // block-uniform
-        ++pass;
-#pragma unroll
-        for (int n = 0; n < kHalfCols / 16; ++n) cacc[n] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-        l_run = 0.f;
-    }
-
-    // ---- in-block merge of the P streams: common max, then a fixed pairwise tree
-    const float l_tot = rows4_sum(l_run);
-    if (j == 0 && q4 == 0) {
-        m_s[pr][r16] = m_used;
-        l_s[pr][r16] = l_tot;
-    }
-    __syncthreads();  // every stream is done with its LDS copies
-    float M = -INFINITY;
-#pragma unroll
-    for (int v = 0; v < P; ++v) M = fmaxf(M, m_s[v][r16]);  // finite: the split has a token
-    const float f = m_used == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m_used - M);
-#pragma unroll
-    for (int n = 0; n < kHalfCols / 16; ++n) cacc[n] *= f;
-    float4 *xb = reinterpret_cast<float4 *>(smem);  // [P / 2][2][16][64] float4
-#pragma unroll
-    for (int half = P / 2; half >= 1; half /= 2) {
-        if (pr >= half && pr < 2 * half) {
-#pragma unroll
-            for (int n = 0; n < kHalfCols / 16; ++n)
-                xb[(((pr - half) * 2 + j) * 16 + n) * 64 + lane] = make_float4(cacc[n][0], cacc[n][1], cacc[n][2], cacc[n][3]);
-        }
-        __syncthreads();
-        if (pr < half) {
-#pragma unroll
-            for (int n = 0; n < kHalfCols / 16; ++n) {
-                const float4 o = xb[((pr * 2 + j) * 16 + n) * 64 + lane];
-                cacc[n] += f32x4_t{o.x, o.y, o.z, o.w};
-            }
-        }
-        __syncthreads();
-    }
-    // ---- the merged context goes out through LDS, so that each store of a wave writes
-    // 1 KB of one record row (the merge buffers are free after the last barrier)
-    float *cs = reinterpret_cast<float *>(smem);  // [16][kCsRow]
-    if (pr == 0) {
-#pragma unroll
-        for (int n = 0; n < kHalfCols / 16; ++n)
-            *reinterpret_cast<float4 *>(cs + r16 * kCsRow + j * kHalfCols + n * 16 + q4 * 4) =
-                make_float4(cacc[n][0], cacc[n][1], cacc[n][2], cacc[n][3]);
-        if (j == 0 && q4 == 0 && h0 + r16 < a.H) {
-            float L = 0.f;
-#pragma unroll
-            for (int v = 0; v < P; ++v) {
-                const float mv = m_s[v][r16];
-                L += mv == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mv - M) * l_s[v][r16];
-            }
-            a.ml[static_cast<int64_t>(split) * a.H + h0 + r16] = make_float2(M, L);
-        }
-    }
-    __syncthreads();
-    float *rec = a.part + (static_cast<int64_t>(split) * a.H + h0) * kR;
-    for (int f = tid; f < kHG * kR / 4; f += 128 * P) {
-        const int row = f / (kR / 4), c4 = f % (kR / 4);
-        if (h0 + row < a.H)
-            *reinterpret_cast<float4 *>(rec + row * kR + c4 * 4) = *reinterpret_cast<const float4 *>(cs + row * kCsRow + c4 * 4);
     }
 }
 
@@ -645,16 +646,18 @@ __global__ __launch_bounds__(256) void mla_out_kernel(OutArgs a) {
 }
 
 // ------------------------------------------------------------------ host side
-constexpr int kPairs = 2;  // streams (wave pairs) per attention block: one wave per SIMD
-constexpr int kRing = 2;   // register buffers per wave (deeper rings measured no faster)
+#ifndef K3_MLA_D
+#define K3_MLA_D 2
+#endif
+constexpr int kD = K3_MLA_D;  // staged rounds in flight
 
 // One attention block per CU: about 256 blocks of (head group, split); a split is a
-// multiple of 16 kPairs tokens, so every step of every stream lies inside it.
+// multiple of one round of tiles.
 void mla_splits(int64_t H, int64_t T, int *Ts, int *NS) {
     const int64_t hgn = cdiv(H, kHG);
     const int64_t want = std::max<int64_t>(1, 256 / hgn);
     int64_t ts = cdiv(T, want);
-    ts = cdiv(ts, kStepT * kPairs) * kStepT * kPairs;
+    ts = cdiv(ts, kStepT * kRoundTiles) * kStepT * kRoundTiles;
     *Ts = static_cast<int>(ts);
     *NS = static_cast<int>(cdiv(T, ts));
 }
@@ -768,14 +771,14 @@ int k3::mla_decode_core(const void *q_nope, const void *q_rot, int64_t ld_q, int
     aa.scale_log2 = scale * 1.4426950408889634f;
     const int blocks = NS * static_cast<int>(cdiv(H, kHG));
     aa.swizzle = blocks % 8 == 0;
-    constexpr auto attn = &mla_attn_kernel<kPairs, kRing>;
-    constexpr size_t lds = attn_lds_bytes<kPairs>();
+    constexpr auto attn = &mla_attn_kernel<kD>;
+    constexpr size_t lds = kAttnLds;
     static const hipError_t lds_rc = hipFuncSetAttribute(reinterpret_cast<const void *>(attn),
                                                          hipFuncAttributeMaxDynamicSharedMemorySize,
                                                          static_cast<int>(lds));  // may exceed the 64 KB default
     rc = check_hip(lds_rc, "mla decode: attention LDS size");
     if (rc) return rc;
-    attn<<<dim3(static_cast<unsigned>(blocks)), 128 * kPairs, lds, st>>>(aa);
+    attn<<<dim3(static_cast<unsigned>(blocks)), 512, lds, st>>>(aa);
     rc = check_hip(hipGetLastError(), "mla decode: attention launch");
     if (rc) return rc;
 

@@ -101,11 +101,12 @@ def test_mla_decode_peaked_softmax():
     assert om.normwise_rel(got, want) <= TOL
 
 
-def test_mla_decode_rising_scores_restart_passes():
+def test_mla_decode_rising_scores_move_the_reference():
     """Scores that climb by 80..170 (log2 units) every 96 tokens, for half of the heads:
-    a later step of a split exceeds the max its pass started with by far more than the
-    kernel's headroom, so the split's pass restarts with the larger max (several times per
-    split); the other heads fall instead.  The rope column 0 carries the ramp."""
+    a later tile of a split exceeds the head's reference max by far more than the kernel's
+    headroom, so the reference moves and the accumulators are rescaled (several times per
+    split and tile class); the other heads fall instead.  The rope column 0 carries the
+    ramp."""
     H, T = 64, 20000
     q_nope, q_rot, w_uk, w_uv, lat, rot = make(11, H, T)
     q_rot[:, 0] = np.linspace(-2.0, 2.0, H).astype(np.float32)
