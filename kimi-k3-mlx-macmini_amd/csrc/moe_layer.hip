@@ -576,16 +576,20 @@ __global__ __launch_bounds__(256) void layer_l2(LayerArgs a) {
 // 4 * RW down rows (RW consecutive rows per wave).  A down row is cut into pieces of S
 // elements (S = 32: one group, 16 bytes; S = 16: half a group, 8 bytes); lane l takes pieces
 // l, l + 64, ... (NP of them), so each of the wave's loads is one contiguous run of the row,
-// and it holds the act values of those pieces in registers for all RW rows.  The row totals
-// go to yrow[j]; the last of the range's k blocks to finish combines them in slot order, so
-// the result does not depend on the order in which the blocks finish.
+// and it holds the act values of those pieces in registers for all RW rows.  The block reads
+// expert j's act vector from memory once and passes it to its waves through LDS in
+// chunk-major order ([chunk][piece], so the lanes of a wave read consecutive 16-byte slots)
+// rather than each wave reading it again.  The row totals go to yrow[j]; the last of the range's k blocks to finish combines them in slot
+// order, so the result does not depend on the order in which the blocks finish.
 template <int S, int NP, int RW>
 __global__ __launch_bounds__(256, 4) void layer_l3(LayerArgs a) {
     static_assert(S == 16 || S == 32, "a piece is half a group or one group");
     constexpr int ND = S / 8;   // packed dwords per piece
     constexpr int NC = S / 4;   // float4 act chunks per piece
     constexpr int RB = 4 * RW;  // rows per block
+    constexpr int NA = S * NP / 16;  // act float4 per thread: the block covers I <= S * NP * 64
     __shared__ uint32_t last_s;
+    __shared__ float4 act_s[NA * 256];  // expert j's act, [chunk q][piece]
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
     // slot-major order: consecutive blocks read different rows of one expert, so every XCD
     // streams from every selected expert
@@ -598,16 +602,14 @@ __global__ __launch_bounds__(256, 4) void layer_l3(LayerArgs a) {
     const auto rd = make_rsrc(uniform_ptr(t[4]), static_cast<uint32_t>(a.Hr) * rowB);
     const auto rds = make_rsrc(uniform_ptr(t[5]), static_cast<uint32_t>(a.Hr * GI));
     const auto ra = make_rsrc(a.ws.act + static_cast<int64_t>(j) * a.I, static_cast<uint32_t>(a.I) * 4u);
-    // 1. the act values of this lane's pieces (the block's four waves read the same bytes),
-    //    then the wave's down rows and their scale bytes
-    float4 av[NP][NC];
+    // 1. expert j's act vector (one read per block; float4 c is chunk (4c % S) / 4 of piece
+    //    4c / S), the wave's down rows and their scale bytes; the act goes to LDS once its
+    //    loads, issued first, have arrived
+    float4 ag[NA];
 #pragma unroll
-    for (int p = 0; p < NP; ++p) {
-        const int pc = p * 64 + lane;
-#pragma unroll
-        for (int q = 0; q < NC; ++q)
-            av[p][q] = __builtin_bit_cast(
-                float4, buf_load16(ra, pc < P ? static_cast<uint32_t>(pc) * (S * 4u) + q * 16u : kOobOffset));
+    for (int i = 0; i < NA; ++i) {
+        const int c = i * 256 + static_cast<int>(threadIdx.x);
+        ag[i] = __builtin_bit_cast(float4, buf_load16(ra, c < a.I / 4 ? c * 16u : kOobOffset));
     }
     uint32_t wd[RW][NP][ND];
     uint32_t sd[RW][NP];
@@ -628,6 +630,19 @@ __global__ __launch_bounds__(256, 4) void layer_l3(LayerArgs a) {
             sd[r][p] = __builtin_amdgcn_raw_buffer_load_b8(
                 rds, ok ? static_cast<uint32_t>(n * GI + pc * S / 32) : kOobOffset, 0, 0);
         }
+#pragma unroll
+    for (int i = 0; i < NA; ++i) {
+        const int c = i * 256 + static_cast<int>(threadIdx.x);
+        if (c < a.I / 4) act_s[(c % NC) * P + c / NC] = ag[i];
+    }
+    __syncthreads();
+    float4 av[NP][NC];
+#pragma unroll
+    for (int p = 0; p < NP; ++p) {
+        const int pc = p * 64 + lane;
+#pragma unroll
+        for (int q = 0; q < NC; ++q) av[p][q] = pc < P ? act_s[q * P + pc] : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
     // 2. row dots (out-of-range pieces hold zeros); wave totals to the workspace
 #pragma unroll
     for (int r = 0; r < RW; ++r) {
