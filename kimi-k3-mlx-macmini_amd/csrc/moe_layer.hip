@@ -589,7 +589,7 @@ __global__ __launch_bounds__(256, 4) void layer_l3(LayerArgs a) {
     constexpr int RB = 4 * RW;  // rows per block
     constexpr int NA = S * NP / 16;  // act float4 per thread: the block covers I <= S * NP * 64
     __shared__ uint32_t last_s;
-    __shared__ float4 act_s[NA * 256];  // expert j's act, [chunk q][piece]
+    __shared__ float4 act_s[NA * 256 + 1];  // expert j's act, [chunk q][piece]; the last slot is a sink
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
     // slot-major order: consecutive blocks read different rows of one expert, so every XCD
     // streams from every selected expert
@@ -630,10 +630,16 @@ __global__ __launch_bounds__(256, 4) void layer_l3(LayerArgs a) {
             sd[r][p] = __builtin_amdgcn_raw_buffer_load_b8(
                 rds, ok ? static_cast<uint32_t>(n * GI + pc * S / 32) : kOobOffset, 0, 0);
         }
+    __builtin_amdgcn_sched_barrier(0);  // every load in flight before the first wait
+    // Unconditional stores and reads: chunks past I store their zeros into the sink slot, and
+    // pieces past P read it (such pieces exist exactly when such chunks do) against zero
+    // weights.  A store or read under a branch lets the compiler move the act load behind the
+    // weight loads or wait for the weights before the first read, and then no row's dot
+    // overlaps the arrival of the later rows.
 #pragma unroll
     for (int i = 0; i < NA; ++i) {
         const int c = i * 256 + static_cast<int>(threadIdx.x);
-        if (c < a.I / 4) act_s[(c % NC) * P + c / NC] = ag[i];
+        act_s[c < a.I / 4 ? (c % NC) * P + c / NC : NA * 256] = ag[i];
     }
     __syncthreads();
     float4 av[NP][NC];
@@ -641,7 +647,7 @@ __global__ __launch_bounds__(256, 4) void layer_l3(LayerArgs a) {
     for (int p = 0; p < NP; ++p) {
         const int pc = p * 64 + lane;
 #pragma unroll
-        for (int q = 0; q < NC; ++q) av[p][q] = pc < P ? act_s[q * P + pc] : make_float4(0.f, 0.f, 0.f, 0.f);
+        for (int q = 0; q < NC; ++q) av[p][q] = act_s[pc < P ? q * P + pc : NA * 256];
     }
     // 2. row dots (out-of-range pieces hold zeros); wave totals to the workspace
 #pragma unroll
