@@ -127,10 +127,15 @@ def moe_layer(x, idx, weights, experts, shared=None, kind="silu", beta=1.0,
     idx = np.atleast_2d(idx)
     weights = np.atleast_2d(weights)
     y = np.zeros((x.shape[0], x.shape[1]), np.float64)
+    # expert ids that share one weight tuple (tests alias them) decode it once; the cache
+    # holds the tuple itself, so its id cannot be reused by another object meanwhile
+    dense = {}
     for e in sorted({int(v) for v in idx.reshape(-1)}):
         tok, slot = np.nonzero(idx == e)
-        out = expert_ffn(x[tok], *experts[e], kind=kind, beta=beta,
-                         linear_beta=linear_beta)[0]
+        ex = experts[e]
+        if id(ex) not in dense:
+            dense[id(ex)] = (ex, tuple(decode_mxfp4(*pair).astype(np.float64) for pair in ex))
+        out = dense_ffn(x[tok], *dense[id(ex)][1], kind=kind, beta=beta, linear_beta=linear_beta)[0]
         y[tok] += out * weights[tok, slot][:, None]
     if shared is not None:
         y += dense_ffn(x, *shared, kind=kind, beta=beta, linear_beta=linear_beta)[0]

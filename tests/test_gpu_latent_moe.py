@@ -104,6 +104,14 @@ def test_latent_moe_k3_shapes_decode():
                 num_experts_per_token=16), seed=50, T=1, distinct=4)
 
 
+def test_latent_moe_k3_shapes_grouped():
+    """The same K3 shapes with 16 tokens: more than DECODE_TOKENS, so the grouped path runs
+    (batched routing, latent down GEMM, k3_moe_grouped_ffn over 896 table rows aliasing
+    eight distinct weight sets, norm, up and shared GEMMs)."""
+    check(K3Cfg(hidden_size=7168, routed_expert_hidden_size=3584, moe_intermediate_size=3072, num_experts=896,
+                num_experts_per_token=16), seed=51, T=16, distinct=8)
+
+
 def test_latent_moe_rejects_wrong_projection_shapes():
     from k3hip.moe import LatentMoE
     cfg = K3Cfg(hidden_size=256, routed_expert_hidden_size=128, moe_intermediate_size=128, num_experts=8,

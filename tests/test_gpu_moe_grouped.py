@@ -97,11 +97,31 @@ def test_grouped_matches_oracle(T, H, I, E, k, D, routing, act):
     assert rel <= PATH_TOL, f"scaled-MFMA path above its expected error level: {rel:.3e}"
 
 
+def sampled_oracle(x32, idx, w, ex_np, sample, act="silu", beta=1.0, lbeta=None):
+    """fp64 routed outputs of the sampled tokens: each distinct weight set is decoded and
+    widened once and takes all the sampled (token, slot) pairs routed to it in one product."""
+    D = len(ex_np)
+    T, k = idx.shape
+    H = x32.shape[1]
+    want = np.zeros((len(sample), H))
+    pairs = [(r, j, int(idx[t, j]) % D) for r, t in enumerate(sample) for j in range(k)]
+    for d in sorted({p[2] for p in pairs}):
+        mine = [(r, j) for r, j, dd in pairs if dd == d]
+        xs = np.stack([x32[sample[r]] for r, _ in mine]).astype(np.float64)
+        wg, wu, wd = (om.decode_mxfp4(*pair).astype(np.float64) for pair in ex_np[d])
+        y = omoe.dense_ffn(xs, wg, wu, wd, act, beta, lbeta)[0]
+        for (r, j), yy in zip(mine, y):
+            want[r] += w[sample[r], j] * yy
+    return want
+
+
 def test_grouped_full_shape_sampled_tokens_and_determinism():
-    """2048 tokens x top-8 over 384 experts (4 distinct weight sets aliased), Zipf(1.1)
-    load, hidden 7168, intermediate 2048: a sample of tokens against the oracle, and two
-    runs bit-identical."""
-    T, H, I, E, k, D = 2048, 7168, 2048, 384, 8, 4
+    """2048 tokens x top-8 over 384 experts (16 distinct weight sets aliased), Zipf(1.1)
+    load, hidden 7168, intermediate 2048: 60 tokens against the oracle -- every 64-token tile
+    boundary of the hottest expert (first and last token of each of its tiles, in the grouped
+    order, which is token order), tokens routed to the coldest experts (single partly filled
+    tiles), the first and last tokens and a random draw -- and two runs bit-identical."""
+    T, H, I, E, k, D = 2048, 7168, 2048, 384, 8, 16
     rng = np.random.default_rng(1004)
     ex_np, ex_dev = make_experts(rng, D, H, I)
     idx, w = zipf_routing(rng, T, E, k)
@@ -111,16 +131,20 @@ def test_grouped_full_shape_sampled_tokens_and_determinism():
     got = run(x32, idx, w, ex_dev, E, I)
     again = run(x32, idx, w, ex_dev, E, I)
     assert np.array_equal(got, again)
-    sample = np.array([0, 1, 777, 1500, 2046, 2047])
-    dense = [tuple(om.decode_mxfp4(*pair) for pair in ex) for ex in ex_np]   # decode each set once
-    want = np.zeros((len(sample), H))
-    for r, t in enumerate(sample):
-        for j in range(k):
-            wg, wu, wd = dense[idx[t, j] % D]
-            want[r] += w[t, j] * omoe.dense_ffn(x32[t:t + 1], wg, wu, wd)[0][0]
+    hot = int(np.argmax(counts))
+    hot_tokens = np.nonzero((idx == hot).any(axis=1))[0]        # grouped rows of the hot expert, in order
+    edges = sorted({int(hot_tokens[m]) for m0 in range(0, len(hot_tokens), 64)
+                    for m in (m0, min(m0 + 63, len(hot_tokens) - 1))})
+    cold = [e for e in np.argsort(counts) if counts[e] > 0][:8]
+    cold_tokens = [int(np.nonzero((idx == e).any(axis=1))[0][0]) for e in cold]
+    sample = sorted(set(edges[:40] + cold_tokens + [0, 1, T - 2, T - 1]
+                        + [int(t) for t in rng.choice(T, 8, replace=False)]))
+    want = sampled_oracle(x32, idx, w, ex_np, sample)
     rel = om.normwise_rel(got[sample], want)
-    print(f"full shape sampled rel={rel:.3e}")
+    print(f"full shape: {len(sample)} sampled tokens, rel={rel:.3e}")
+    assert len(sample) >= 50
     assert rel <= TOL
+    assert rel <= PATH_TOL
 
 
 def test_grouped_bf16_output_and_errors():

@@ -100,6 +100,47 @@ def test_layer_matches_oracle(H, I, E, k, Is, distinct, router, act, xdt):
     assert om.normwise_rel(y.cpu().numpy(), y_want) < 2e-5
 
 
+def test_layer_full_shape_every_expert_distinct():
+    """The 384-expert top-8 layer at full size with every expert distinct (9 GB of weights
+    drawn on the device; only the selected experts are copied to the host for the oracle),
+    a bf16 shared expert, three tokens in a row through one module."""
+    from k3hip.moe import MoEConfig, RoutedMoE
+    H, I, E, k, Is = 7168, 2048, 384, 8, 2048
+    g = torch.Generator(device=DEV)
+    g.manual_seed(384)
+
+    def mx(n, kk):
+        return (torch.randint(0, 256, (n, kk // 2), dtype=torch.uint8, device=DEV, generator=g),
+                torch.randint(118, 131, (n, kk // 32), dtype=torch.uint8, device=DEV, generator=g))
+
+    experts = [(mx(I, H), mx(I, H), mx(H, I)) for _ in range(E)]
+    rng = np.random.default_rng(385)
+    router_w = om.bf16_round((rng.standard_normal((E, H)) * 0.02).astype(np.float32))
+    shared = tuple(om.bf16_round((rng.standard_normal(sh) * 0.02).astype(np.float32))
+                   for sh in ((Is, H), (Is, H), (H, Is)))
+    w = {"gate.weight": torch.from_numpy(router_w).to(DEV).to(torch.bfloat16)}
+    for name, a in zip(("gate", "up", "down"), shared):
+        w[f"shared_experts.{name}_proj.weight"] = torch.from_numpy(a).to(DEV).to(torch.bfloat16)
+    cfg = MoEConfig(hidden_size=H, moe_intermediate_size=I, num_experts=E, num_experts_per_token=k,
+                    shared_intermediate_size=Is, router="softmax", activation="silu")
+    which = {"w1": 0, "w3": 1, "w2": 2}
+    moe = RoutedMoE(cfg, 1, w, lambda layer, e, wh: experts[e][which[wh]])
+    seen = set()
+    for t in range(3):
+        x32 = om.bf16_round(rng.standard_normal((1, H)).astype(np.float32))
+        idx, wts, raw, _ = omoe.route_softmax(x32, router_w, k, True, 1.0)
+        assert topk_margin(raw, k) > 1e-5, "seed gives a near-tie at the top-k boundary"
+        sel = {int(e): tuple(tuple(a.cpu().numpy() for a in pair) for pair in experts[int(e)]) for e in idx[0]}
+        y_want = omoe.moe_layer(x32, idx, wts, sel, shared)
+        y, r = moe(torch.from_numpy(x32).to(DEV).to(torch.bfloat16), return_router=True)
+        assert np.array_equal(np.sort(r.expert_indices.cpu().numpy(), -1), np.sort(idx, -1))
+        rel = om.normwise_rel(y.cpu().numpy(), y_want)
+        print(f"token {t}: experts {sorted(sel)} rel={rel:.3e}")
+        assert rel < 2e-5
+        seen.update(sel)
+    assert len(seen) > 16  # distinct weights behind distinct experts, not a few aliased sets
+
+
 def test_route_only_matches_layer_record_and_invariants():
     """The invariants of tests/test_k3ref_layers.py:113-127 on the sigmoid+bias router:
     k distinct experts, weights renormalise to the scaling factor, selection follows the

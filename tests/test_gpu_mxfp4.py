@@ -136,6 +136,30 @@ def test_matvec_every_launch_shape(N, K, xdt):
     assert om.normwise_rel(got, om.matvec_f64(x32, packed, scales)) < 2e-6
 
 
+@pytest.mark.parametrize("n,k", [(2048, 7168), (7168, 2048)])
+@pytest.mark.parametrize("xdt", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("band", ["low", "high", "mixed"])
+def test_matvec_scale_bytes_at_the_legal_edges(n, k, xdt, band):
+    """Scale bytes at both ends of the accepted range 2..252 (mxfp4.py:58-65): 2..20 (block
+    scales down to 2^-125, products down to 2^-126, the smallest normal fp32 / bf16 value),
+    240..252 (up to 2^125, products up to 1.5 x 2^127) with x scaled by 2^-24 so the sums
+    stay finite, and rows mixing both ends group by group."""
+    from k3hip.mxfp4_matvec import mxfp4_matvec_fused
+    rng = np.random.default_rng(n + 3 * k + {"low": 0, "high": 1, "mixed": 2}[band])
+    packed = rng.integers(0, 256, size=(n, k // 2), dtype=np.uint8)
+    lo_s = rng.integers(2, 21, size=(n, k // 32), dtype=np.uint8)
+    hi_s = rng.integers(240, 253, size=(n, k // 32), dtype=np.uint8)
+    scales = {"low": lo_s, "high": hi_s, "mixed": np.where(rng.random((n, k // 32)) < 0.5, lo_s, hi_s)}[band]
+    x32 = rng.standard_normal((1, k)).astype(np.float32) * np.float32(2.0 ** (-24 if band != "low" else 0))
+    if xdt == torch.bfloat16:
+        x32 = om.bf16_round(x32)
+    x = torch.from_numpy(x32).to(DEV).to(xdt)
+    got = mxfp4_matvec_fused(x, _t(packed), _t(scales)).cpu().numpy()
+    want = om.matvec_f64(x32, packed, scales)
+    assert np.isfinite(got).all() and np.isfinite(want).all()
+    assert om.normwise_rel(got, want) < 2e-6
+
+
 def test_matvec_bf16_output_is_rne_of_fp32():
     from k3hip.mxfp4_matvec import mxfp4_matvec_fused
     packed, scales, x32 = _case(1001, 2048, 7168, 1)
