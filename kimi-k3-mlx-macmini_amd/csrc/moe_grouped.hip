@@ -335,23 +335,32 @@ __global__ __launch_bounds__(kThreads, 1) void mx_gemm_kernel(MxArgs a) {
         }
     };
 
-    // ---- B staging: thread (column c = tid & 15, piece p = tid >> 4) copies piece p of the
-    // four tile rows c, 16 + c, 32 + c, 48 + c, every term; (c, block pair g = (tid >> 4) & 3,
-    // tile tid >> 6) copies one scale pair per term.  Two register sets: loads run two
-    // super-steps ahead of their LDS stores.
+    // ---- B staging.  Gate/up (x terms, gathered from memory): thread (column c = tid >> 4,
+    // piece p = tid & 15) copies piece p of tile row c of every 16-column tile and term, so
+    // one wave instruction reads four whole rows' 256-byte super-step runs (whole 128-byte
+    // lines; the loads of 16 rows x 64 bytes they replace measured 5% slower), and the LDS
+    // tile keeps [piece][column] order for the operand reads with the column XOR-ed by the
+    // piece, so neither the stores nor the reads meet bank conflicts.  Down (act terms, just
+    // written and in cache): thread (c = tid & 15, p = tid >> 4), plain order (the line-wise
+    // form measured 3-7% slower there).  (c = tid & 15, block pair g = (tid >> 4) & 3, tile
+    // tid >> 6) copies one scale pair per term.  Two register sets: loads run two super-steps
+    // ahead of their LDS stores.
+    constexpr bool kLines = !DOWN;
     const auto rb = make_rsrc(a.b8, a.b_term * TERMS);
     const auto rbs = make_rsrc(a.bs, a.bs_term * TERMS);
-    const int sc_c = tid & 15, sp = tid >> 4;
-    const int sp_bb = 4 * ((sp >> 2) & 1) + 2 * ((sp & 3) >> 1) + (sp >> 3);  // block of piece sp
+    const int dc = kLines ? tid >> 4 : tid & 15, dp = kLines ? tid & 15 : tid >> 4;
+    // LDS unit (16 bytes) of piece pc of column c within one tile and term
+    auto bunit = [](int pc, int c) { return pc * 16 + (kLines ? c ^ pc : c); };
+    const int dp_bb = 4 * ((dp >> 2) & 1) + 2 * ((dp & 3) >> 1) + (dp >> 3);  // block of piece dp
     uint32_t boff[4];
 #pragma unroll
     for (int ct = 0; ct < 4; ++ct) {
-        const int rr = ct * 16 + sc_c;
+        const int rr = ct * 16 + dc;
         int brow = -1;
         if (rr < rows) brow = DOWN ? pos0 + rr : a.perm[pos0 + rr] / a.top_k;
-        boff[ct] = brow >= 0 ? static_cast<uint32_t>(brow) * a.Kpad + sp * 16u : kOobOffset;
+        boff[ct] = brow >= 0 ? static_cast<uint32_t>(brow) * a.Kpad + dp * 16u : kOobOffset;
     }
-    const int sg = sp & 3, sct = tid >> 6;
+    const int sc_c = tid & 15, sg = (tid >> 4) & 3, sct = tid >> 6;
     uint32_t bsoff;
     {
         const int rr = sct * 16 + sc_c;
@@ -366,7 +375,7 @@ __global__ __launch_bounds__(kThreads, 1) void mx_gemm_kernel(MxArgs a) {
     uint4 XR[XD][4][TERMS];
     uint16_t XS[XD][TERMS];
     auto load_x = [&](int S, int xs) {
-        const uint32_t poob = S >= 0 && S * 8 + sp_bb < KB ? 0u : kOobOffset;
+        const uint32_t poob = S >= 0 && S * 8 + dp_bb < KB ? 0u : kOobOffset;
         const uint32_t soob = S >= 0 && S * 8 + 2 * sg < KB ? 0u : kOobOffset;
 #pragma unroll
         for (int ct = 0; ct < 4; ++ct)
@@ -383,7 +392,7 @@ __global__ __launch_bounds__(kThreads, 1) void mx_gemm_kernel(MxArgs a) {
 #pragma unroll
         for (int ct = 0; ct < 4; ++ct)
 #pragma unroll
-            for (int t = 0; t < TERMS; ++t) xt[((ct * TERMS + t) * 16 + sp) * 16 + sc_c] = XR[xs][ct][t];
+            for (int t = 0; t < TERMS; ++t) xt[(ct * TERMS + t) * 256 + bunit(dp, dc)] = XR[xs][ct][t];
 #pragma unroll
         for (int t = 0; t < TERMS; ++t) st[((sct * TERMS + t) * 16 + sc_c) * 4 + sg] = XS[xs][t];
     };
@@ -408,8 +417,8 @@ __global__ __launch_bounds__(kThreads, 1) void mx_gemm_kernel(MxArgs a) {
                 for (int t = 0; t < TERMS; ++t) {
                     const uint4 *xb = xt + (ct * TERMS + t) * 256;
                     const uint32_t sb = st[((ct * TERMS + t) * 16 + r16) * 4 + q];
-                    const uint4 b00 = xb[0 * 64 + lane], b01 = xb[1 * 64 + lane];
-                    const uint4 b10 = xb[2 * 64 + lane], b11 = xb[3 * 64 + lane];
+                    const uint4 b00 = xb[bunit(q, r16)], b01 = xb[bunit(4 + q, r16)];
+                    const uint4 b10 = xb[bunit(8 + q, r16)], b11 = xb[bunit(12 + q, r16)];
 #pragma unroll
                     for (int j = 0; j < 4; ++j)
                         acc[j][ct] = mfma_fp4_fp8<0>(A[slot][j][0], b00, b01, acc[j][ct], SA[slot][j], sb);
