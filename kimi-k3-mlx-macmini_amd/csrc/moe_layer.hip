@@ -165,10 +165,11 @@ __device__ __forceinline__ const void *uniform_ptr(uint64_t p) {
 // weights: optional renormalisation by (sum + 1e-20), then * scaling   (moe.py:65-76)
 // Top-k is exact and deterministic with ties to the lower expert index: the order is the
 // strict total order on (selection score, -index), with NaN scores ranked as -inf, as one
-// 64-bit key per expert.  Two levels of parallel ranking (no sequential selection rounds):
-// every expert ranks itself inside its 64-expert group (64 broadcast LDS compares), the
-// group's best k become candidates, and every candidate ranks itself among all candidates.
-// The global top-k is inside the union of the per-group top-k.
+// 64-bit key per expert.  No sequential selection rounds over the experts: a lower bound on
+// the k-th largest key from a small sample picks out a few candidates, and the candidates
+// are ranked in parallel (each lane of a wave counts the larger keys among the wave's 64,
+// each key broadcast from its lane through v_readlane), in a merge tree of 64-wide groups
+// whose best k go on, until one group remains.
 // 64-bit order key of (selection score, expert): larger key = ranks first.  High word: the
 // float's bits mapped monotonically to unsigned (NaN mapped as -inf); low word: the
 // complement of the expert index, so ties go to the lower index.  Every live expert's key
@@ -181,39 +182,132 @@ __device__ __forceinline__ uint64_t order_key(float v, int e) {
 }
 __device__ __forceinline__ int key_expert(uint64_t k) { return static_cast<int>(0xffffffffu - static_cast<uint32_t>(k)); }
 
-__device__ __forceinline__ float block_reduce(float v, float *red, bool is_max) {
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
-    v = is_max ? wave_max_all(v) : wave_sum_all(v);
-    if (lane == 0) red[wave] = v;
-    __syncthreads();
-    float r = red[0];
-    for (int i = 1; i < nw; ++i) r = is_max ? fmaxf(r, red[i]) : r + red[i];
-    __syncthreads();
-    return r;
+// Lane l's 64-bit key, broadcast (SGPR pair); l is wave-uniform.
+__device__ __forceinline__ uint64_t readlane_key(uint64_t v, int l) {
+    return (static_cast<uint64_t>(static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(v >> 32), l))) << 32) |
+           static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(static_cast<uint32_t>(v)), l));
 }
-
-constexpr int kMaxCand = kMaxExperts / 64 * kMaxTopK;
+template <int CTRL>
+__device__ __forceinline__ uint64_t dpp_key(uint64_t v) {
+    const uint32_t lo = __builtin_amdgcn_update_dpp(0, static_cast<int>(static_cast<uint32_t>(v)), CTRL, 0xf, 0xf, false);
+    const uint32_t hi = __builtin_amdgcn_update_dpp(0, static_cast<int>(v >> 32), CTRL, 0xf, 0xf, false);
+    return (static_cast<uint64_t>(hi) << 32) | lo;
+}
+__device__ __forceinline__ uint64_t max_key(uint64_t a, uint64_t b) { return a > b ? a : b; }
+// Largest key of the wave, in every lane: DPP inside each 16-lane row (as wave_max_all),
+// then the four row maxima.
+__device__ __forceinline__ uint64_t wave_max_key(uint64_t v) {
+    v = max_key(v, dpp_key<0xb1>(v));
+    v = max_key(v, dpp_key<0x4e>(v));
+    v = max_key(v, dpp_key<0x141>(v));
+    v = max_key(v, dpp_key<0x140>(v));
+    return max_key(max_key(readlane_key(v, 0), readlane_key(v, 16)), max_key(readlane_key(v, 32), readlane_key(v, 48)));
+}
+// Number of lanes j < n (n wave-uniform, at most 64) whose key is larger than this lane's.
+__device__ __forceinline__ int wave_rank_n(uint64_t key, int n) {
+    int rank = 0;
+    for (int j = 0; j < n; ++j) rank += readlane_key(key, j) > key;
+    return rank;
+}
+// The same over all 64 lanes; the reads go in batches of 16 ahead of their compares, so no
+// compare waits on the SGPR write of the read just before it.
+__device__ __forceinline__ int wave_rank(uint64_t key) {
+    const int hi = static_cast<int>(key >> 32), lo = static_cast<int>(key);
+    int rank = 0;
+#pragma unroll
+    for (int j0 = 0; j0 < 64; j0 += 16) {
+        uint32_t h[16], w[16];
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+            h[j] = __builtin_amdgcn_readlane(hi, j0 + j);
+            w[j] = __builtin_amdgcn_readlane(lo, j0 + j);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int j = 0; j < 16; ++j) rank += ((static_cast<uint64_t>(h[j]) << 32) | w[j]) > key;
+    }
+    return rank;
+}
+// The same for a wave whose lane j holds expert e0 + j: the low word of
+// lane j's key is known without a read (order_key), so only the high word is broadcast.  A
+// lane past the last expert holds high word 0, below every live key.
+__device__ __forceinline__ int wave_rank_experts(uint64_t key, int e0) {
+    const int hi = static_cast<int>(key >> 32);
+    int rank = 0;
+#pragma unroll
+    for (int j0 = 0; j0 < 64; j0 += 16) {
+        uint32_t h[16];
+#pragma unroll
+        for (int j = 0; j < 16; ++j) h[j] = __builtin_amdgcn_readlane(hi, j0 + j);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int j = 0; j < 16; ++j)
+            rank += ((static_cast<uint64_t>(h[j]) << 32) | (0xffffffffu - static_cast<uint32_t>(e0 + j0 + j))) > key;
+    }
+    return rank;
+}
+// A wave's best k entries to out_k/out_v[0, k): the live lane of rank r < k writes slot r
+// (live keys are distinct, so their ranks are 0 .. n_live - 1) and slots from n_live to k
+// get key 0, which ranks below every live key.
+__device__ __forceinline__ void emit_best(uint64_t key, float v, int rank, bool live, int k, uint64_t *out_k,
+                                          float *out_v) {
+    const int lane = threadIdx.x & 63;
+    const int n_live = __builtin_popcountll(__builtin_amdgcn_ballot_w64(live));
+    if (live && rank < k) {
+        out_k[rank] = key;
+        out_v[rank] = v;
+    }
+    if (lane >= n_live && lane < k) out_k[lane] = 0;
+}
 
 // Called by all 256 threads of the last router block; logits are read with agent-coherent
 // loads (written by other blocks, possibly on other XCDs, in this launch).
+//
+// Selection values: sigmoid(logit) + bias for sigmoid_bias; for softmax the logit itself,
+// since the probability is a strictly increasing function of it (the fp64 probabilities
+// order exactly as the logits; fp32 ones may round distinct logits to one value).  A NaN
+// logit makes every softmax probability NaN; then all scores tie and the k lowest indices
+// are selected, as for any all-NaN score row.
+//
+// Steps (each thread holds experts t + 256 m):
+//   1. keys; per-wave softmax partials (max, sum of exp); a sample of two keys per 64-expert
+//      group (the group's two largest, by DPP wave maxima), when two per group reach k;
+//   2. theta = the k-th largest sample: the samples are keys, so at least k keys are at
+//      least theta and every key of the top k is; those keys (the survivors, typically
+//      10 to 30) are collected in LDS;
+//   3. the survivors, or without a sample every key, go through the ranking merge tree
+//      until one group of at most 64 is left, whose ranks are the selection order.
+// Nothing is stored to memory before the pointer copies at the end: vmcnt counts stores as
+// well as loads, so a store issued before the wait for the table loads would hold that wait
+// for a store round trip.
 __device__ void route_block(const LayerArgs &a) {
     constexpr int kPer = kMaxExperts / 256;  // experts per thread: e = t + 256 * m
-    __shared__ uint64_t key_s[kMaxExperts];
-    __shared__ uint64_t cand_k[kMaxCand];
-    __shared__ float cand_s[kMaxCand];
-    __shared__ float red[8];
-    __shared__ int32_t idx_s[kMaxTopK];
-    __shared__ float w_s[kMaxTopK];
-    const int t = threadIdx.x, lane = t & 63;
-    float l[kPer], s[kPer], sel[kPer];
-    uint64_t key[kPer];
+    constexpr int kMaxCand = kMaxExperts / 64 * kMaxTopK;
+    __shared__ uint64_t cand_k[2][kMaxCand];
+    __shared__ float cand_v[2][kMaxCand];
+    __shared__ uint64_t samp_s[2 * (kMaxExperts / 64)];
+    __shared__ float stat_s[2][4];
+    __shared__ uint32_t nsurv_s;
+    __shared__ uint8_t slot_s[kMaxExperts];  // selection slot of expert e; 0xff: not selected
+    const int t = threadIdx.x, lane = t & 63, wave = __builtin_amdgcn_readfirstlane(t >> 6);
+    const bool soft = a.route_kind == K3_ROUTE_SOFTMAX;
+    const bool biased = a.route_kind == K3_ROUTE_SIGMOID_BIAS && a.router_bias;
+    float l[kPer], bias[kPer];
 #pragma unroll
     for (int m = 0; m < kPer; ++m) {
         const int e = t + 256 * m;
         l[m] = e < a.E ? __hip_atomic_load(a.ws.logits + e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : -INFINITY;
     }
-    // every thread also loads the 6 table pointers of its experts now, alongside the logits,
-    // so that writing the selected experts' pointers needs no dependent load at the end
+    // the bias and the 6 table pointers of this thread's experts are loaded alongside the
+    // logits, so no dependent load waits later
+    {
+        const auto rb = make_rsrc(a.router_bias, biased ? static_cast<uint32_t>(a.E) * 4u : 0u);
+#pragma unroll
+        for (int m = 0; m < kPer; ++m) {
+            const int e = t + 256 * m;
+            bias[m] = __uint_as_float(buf_load4(rb, e < a.E ? static_cast<uint32_t>(e) * 4u : kOobOffset));
+        }
+    }
     uint4 tab[kPer][3];
     {
         const auto rt = make_rsrc(a.table, a.table ? static_cast<uint32_t>(a.E) * 48u : 0u);
@@ -224,102 +318,169 @@ __device__ void route_block(const LayerArgs &a) {
             for (int q = 0; q < 3; ++q) tab[m][q] = buf_load16(rt, e < a.E ? static_cast<uint32_t>(e) * 48u + q * 16u : kOobOffset);
         }
     }
-    if (a.route_kind == K3_ROUTE_SOFTMAX) {
+    // 1. keys (v: the value a candidate carries, the logit for softmax, else the score)
+    uint64_t key[kPer];
+    float v[kPer], sel[kPer];
+#pragma unroll
+    for (int m = 0; m < kPer; ++m) {
+        const int e = t + 256 * m;
+        if (soft) {
+            v[m] = sel[m] = l[m];
+        } else {
+            v[m] = 1.0f / (1.0f + expf(-l[m]));
+            sel[m] = biased ? v[m] + bias[m] : v[m];
+        }
+        key[m] = e < a.E ? order_key(sel[m], e) : 0;
+        slot_s[e] = 0xff;
+    }
+    if (t == 0) nsurv_s = 0;
+    if (soft) {  // per-wave max and sum of exp(logit - max); a NaN logit makes the sum NaN
         float mx = -INFINITY;
 #pragma unroll
         for (int m = 0; m < kPer; ++m) mx = fmaxf(mx, l[m]);
-        mx = block_reduce(mx, red, true);
+        mx = wave_max_all(mx);
         float sum = 0.f;
 #pragma unroll
+        for (int m = 0; m < kPer; ++m)
+            if (t + 256 * m < a.E) sum += l[m] != l[m] ? l[m] : (mx == -INFINITY ? 0.f : expf(l[m] - mx));
+        sum = wave_sum_all(sum);
+        if (lane == 0) {
+            stat_s[0][wave] = mx;
+            stat_s[1][wave] = sum;
+        }
+    }
+    const int g1 = (a.E + 63) / 64;  // 64-expert groups
+    const bool sampled = 2 * g1 >= a.k;
+    if (sampled) {
+#pragma unroll
         for (int m = 0; m < kPer; ++m) {
-            s[m] = t + 256 * m < a.E ? expf(l[m] - mx) : 0.f;
-            sum += s[m];
-        }
-        sum = block_reduce(sum, red, false);
-#pragma unroll
-        for (int m = 0; m < kPer; ++m) s[m] /= sum;
-    } else {
-#pragma unroll
-        for (int m = 0; m < kPer; ++m) s[m] = 1.0f / (1.0f + expf(-l[m]));
-    }
-    for (int c = t; c < kMaxCand; c += 256) cand_k[c] = 0;  // ranks below every expert
-#pragma unroll
-    for (int m = 0; m < kPer; ++m) {
-        const int e = t + 256 * m;
-        const bool live = e < a.E;
-        sel[m] = (a.route_kind == K3_ROUTE_SIGMOID_BIAS && a.router_bias && live) ? s[m] + a.router_bias[e] : s[m];
-        if (live) {
-            a.ws.scores[e] = s[m];
-            a.ws.corrected[e] = sel[m];
-        }
-        key[m] = live ? order_key(sel[m], e) : 0;
-        key_s[e] = key[m];
-    }
-    __syncthreads();
-    // level 1: rank inside the 64-expert group (all lanes of a wave share the group, so
-    // every LDS read is a broadcast); one 64-bit compare per pair
-#pragma unroll
-    for (int m = 0; m < kPer; ++m) {
-        const int e = t + 256 * m;
-        if (256 * m >= a.E) break;  // uniform: no expert of this or later rounds is live
-        const uint64_t *g = key_s + (e & ~63);
-        int rank = 0;
-#pragma unroll
-        for (int j = 0; j < 64; ++j) rank += g[j] > key[m];
-        if (e < a.E && rank < a.k) {
-            const int c = (e >> 6) * a.k + rank;
-            cand_k[c] = key[m];
-            cand_s[c] = s[m];
-        }
-    }
-    __syncthreads();
-    // level 2: every candidate ranks itself among all candidates
-    const int nc = (a.E + 63) / 64 * a.k;
-    if (nc <= 64) {
-        if (t < 64) {  // one candidate per lane of wave 0, 64 broadcast compares
-            const uint64_t kc = cand_k[lane];
-            int rank = 0;
-#pragma unroll
-            for (int d = 0; d < 64; ++d) rank += cand_k[d] > kc;
-            if (kc != 0 && rank < a.k) {
-                idx_s[rank] = key_expert(kc);
-                w_s[rank] = cand_s[lane];
-            }
-        }
-    } else {
-        for (int c = t; c < nc; c += 256) {
-            const uint64_t kc = cand_k[c];
-            if (kc == 0) continue;
-            int rank = 0;
-            for (int d = 0; d < nc; ++d) rank += cand_k[d] > kc;
-            if (rank < a.k) {
-                idx_s[rank] = key_expert(kc);
-                w_s[rank] = cand_s[c];
+            const int g = 4 * m + wave;
+            if (g < g1) {  // uniform per wave
+                uint64_t kk = key[m];
+                const uint64_t m1 = wave_max_key(kk);
+                if (kk == m1) kk = 0;
+                const uint64_t m2 = wave_max_key(kk);
+                if (lane == 0) {
+                    samp_s[2 * g] = m1;
+                    samp_s[2 * g + 1] = m2;
+                }
             }
         }
     }
     __syncthreads();
-    if (t < 64) {
-        float wsum = lane < a.k ? w_s[lane] : 0.f;
-        wsum = wave_sum_all(wsum);
+    // softmax statistics from the per-wave partials; every probability uses the same max
+    float M = 0.f, S = 1.f;
+    if (soft) {
+        M = fmaxf(fmaxf(stat_s[0][0], stat_s[0][1]), fmaxf(stat_s[0][2], stat_s[0][3]));
+        S = 0.f;
+#pragma unroll
+        for (int w = 0; w < 4; ++w) S += stat_s[1][w] == 0.f ? 0.f : stat_s[1][w] * expf(stat_s[0][w] - M);
+    }
+    const bool nan_route = soft && !(S > 0.f);  // a NaN or infinite logit: every probability NaN
+    int n = 0, buf = 0;
+    if (sampled) {
+        // 2. theta and the survivors
+        const int ns = 2 * g1;
+        const uint64_t ks = lane < ns ? samp_s[lane] : 0;
+        const int rs = wave_rank_n(ks, ns);
+        const uint64_t hit = __builtin_amdgcn_ballot_w64(lane < ns && rs == a.k - 1);
+        const uint64_t theta = hit ? readlane_key(ks, __builtin_ctzll(hit)) : 0;
+#pragma unroll
+        for (int m = 0; m < kPer; ++m) {
+            if (256 * m >= a.E) break;  // uniform
+            const bool sv = key[m] != 0 && key[m] >= theta;
+            const uint64_t mask = __builtin_amdgcn_ballot_w64(sv);
+            if (mask) {  // uniform
+                uint32_t base = 0;
+                if (lane == 0) base = atomicAdd(&nsurv_s, static_cast<uint32_t>(__builtin_popcountll(mask)));
+                base = __builtin_amdgcn_readfirstlane(base);
+                const uint32_t pos =
+                    base + __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(mask >> 32),
+                                                     __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(mask), 0u));
+                if (sv && pos < kMaxCand) {
+                    cand_k[0][pos] = key[m];
+                    cand_v[0][pos] = v[m];
+                }
+            }
+        }
+        __syncthreads();
+        n = static_cast<int>(nsurv_s);
+    }
+    if (!sampled || n > kMaxCand) {
+        // 3'. every key: each wave ranks its 64 experts of round m (experts 256 m + 64 wave + lane)
+#pragma unroll
+        for (int m = 0; m < kPer; ++m) {
+            const int g = 4 * m + wave;
+            if (g < g1) {  // uniform per wave
+                const int rank = wave_rank_experts(key[m], 64 * g);
+                emit_best(key[m], v[m], rank, key[m] != 0, a.k, cand_k[0] + g * a.k, cand_v[0] + g * a.k);
+            }
+        }
+        n = g1 * a.k;
+        __syncthreads();
+    }
+    // 3. ranking levels while more than one group of 64 candidates is left
+    while (n > 64) {
+        const int ng = (n + 63) / 64;
+        for (int g = wave; g < ng; g += 4) {
+            const int c = g * 64 + lane;
+            const uint64_t kc = c < n ? cand_k[buf][c] : 0;
+            const float vc = c < n ? cand_v[buf][c] : 0.f;
+            emit_best(kc, vc, wave_rank(kc), kc != 0, a.k, cand_k[buf ^ 1] + g * a.k, cand_v[buf ^ 1] + g * a.k);
+        }
+        buf ^= 1;
+        n = ng * a.k;
+        __syncthreads();
+    }
+    // the last group (wave 0): the lane of rank r < k holds the r-th selected expert
+    bool chosen = false;
+    int rank = 0, esel = 0;
+    float wsel = 0.f;
+    if (wave == 0) {
+        const uint64_t kc = lane < n ? cand_k[buf][lane] : 0;
+        const float vc = lane < n ? cand_v[buf][lane] : 0.f;
+        float sc;
+        if (nan_route) {
+            rank = esel = lane;
+            chosen = lane < a.k;
+            sc = __int_as_float(0x7fc00000);
+        } else {
+            rank = wave_rank_n(kc, n);
+            chosen = kc != 0 && rank < a.k;
+            esel = key_expert(kc);
+            sc = soft ? expf(vc - M) / S : vc;
+        }
+        const float wsum = wave_sum_all(chosen ? sc : 0.f);
         const float norm = (a.renorm && a.k > 1) ? 1.0f / (wsum + 1e-20f) : 1.0f;
-        if (lane < a.k) {
-            a.ws.topk_idx[lane] = idx_s[lane];
-            a.ws.topk_w[lane] = w_s[lane] * norm * a.scaling;
-        }
+        wsel = sc * norm * a.scaling;
+        if (chosen) slot_s[esel] = static_cast<uint8_t>(rank);
     }
     if (a.table) {  // the owner of each selected expert writes its pointers
+        __syncthreads();
 #pragma unroll
         for (int m = 0; m < kPer; ++m) {
             const int e = t + 256 * m;
-            for (int r = 0; r < a.k; ++r) {
-                if (idx_s[r] == e) {
-                    uint4 *dst = reinterpret_cast<uint4 *>(a.ws.sel_ptrs + r * 6);
-                    dst[0] = tab[m][0];
-                    dst[1] = tab[m][1];
-                    dst[2] = tab[m][2];
-                }
+            if (256 * m >= a.E) break;  // uniform: no expert of this or later rounds
+            const int r = slot_s[e];
+            if (r != 0xff) {
+                uint4 *dst = reinterpret_cast<uint4 *>(a.ws.sel_ptrs + r * 6);
+                dst[0] = tab[m][0];
+                dst[1] = tab[m][1];
+                dst[2] = tab[m][2];
             }
+        }
+    }
+    if (chosen) {
+        a.ws.topk_idx[rank] = esel;
+        a.ws.topk_w[rank] = wsel;
+    }
+#pragma unroll
+    for (int m = 0; m < kPer; ++m) {
+        const int e = t + 256 * m;
+        if (e < a.E) {
+            const float sc = soft ? expf(l[m] - M) / S : v[m];
+            a.ws.scores[e] = sc;
+            a.ws.corrected[e] = soft ? sc : sel[m];
         }
     }
 }

@@ -111,6 +111,54 @@ def test_topk_ties_go_to_lower_index_and_empty_batch():
               T.stream(z))
 
 
+@pytest.mark.parametrize("case", ["ties_across_groups", "clustered", "all_equal", "random_1024", "softmax_nan"])
+def test_topk_every_selection_path(case):
+    """Rows built to reach each path of the selection: a few candidates at or above the
+    bound sampled from each 64-expert group (random rows), more than 64 of them (a ranking
+    level before the last: 100 hot experts in the first two groups), more than 256 (every
+    key ranked: all logits equal), ties across groups and waves, and a NaN logit under
+    softmax (every probability NaN: the k lowest indices, NaN weights and scores)."""
+    from k3hip import _lib
+    rng = np.random.default_rng(sum(map(ord, case)))
+    bias = None
+    kind, code = "softmax", _lib.K3_ROUTE_SOFTMAX
+    if case == "ties_across_groups":
+        E, k = 384, 8
+        logits = np.zeros((3, E), np.float32)
+        logits[0, [5, 100, 300, 301]] = 3.0
+        logits[0, [200, 7]] = 2.5
+        logits[1, [383, 64, 128, 0]] = 1.0          # ties in four groups, three waves
+        logits[2] = np.repeat(np.arange(6, dtype=np.float32), 64)[::-1].copy()  # group-constant
+    elif case == "clustered":
+        E, k = 896, 16
+        kind, code = "sigmoid_bias", _lib.K3_ROUTE_SIGMOID_BIAS
+        logits = rng.standard_normal((4, E)).astype(np.float32)
+        logits[:, :100] += 4.0
+        bias = (rng.standard_normal(E) * 0.05).astype(np.float32)
+    elif case == "all_equal":
+        E, k = 1024, 16
+        logits = np.zeros((2, E), np.float32)
+        logits[1, [1000, 999]] = 1.0
+    elif case == "random_1024":
+        E, k = 1024, 16
+        logits = (rng.standard_normal((8, E)) * 2).astype(np.float32)
+    else:
+        E, k = 384, 8
+        logits = (rng.standard_normal((2, E)) * 2).astype(np.float32)
+        logits[1, 200] = np.nan
+    idx, w, sc, co = _topk_run(logits, bias, code, k, scaling=1.5)
+    widx, ww, wraw, wcorr = _oracle_select(logits, bias, kind, k, scaling=1.5)
+    assert np.array_equal(idx, widx)
+    if case == "softmax_nan":
+        assert np.allclose(w[0], ww[0], rtol=2e-6, atol=1e-9)
+        assert idx[1].tolist() == list(range(k))
+        assert np.isnan(w[1]).all() and np.isnan(sc[1]).all() and np.isnan(co[1]).all()
+        return
+    assert np.allclose(w, ww, rtol=2e-6, atol=1e-9)
+    assert np.allclose(sc, wraw, rtol=2e-6, atol=1e-12)
+    assert np.allclose(co, wcorr, rtol=2e-6, atol=1e-7)
+
+
 def test_topk_rejects_bad_arguments():
     from k3hip import _lib
     from k3hip import _torch as T
