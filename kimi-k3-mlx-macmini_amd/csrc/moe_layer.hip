@@ -194,28 +194,22 @@ __device__ __forceinline__ uint64_t dpp_key(uint64_t v) {
     return (static_cast<uint64_t>(hi) << 32) | lo;
 }
 __device__ __forceinline__ uint64_t max_key(uint64_t a, uint64_t b) { return a > b ? a : b; }
-// Largest key of the wave, in every lane: DPP inside each 16-lane row (as wave_max_all),
-// then the four row maxima.
-__device__ __forceinline__ uint64_t wave_max_key(uint64_t v) {
+// Largest key of each 16-lane row, in every lane of the row (DPP only, as wave_max_all).
+__device__ __forceinline__ uint64_t row_max_key(uint64_t v) {
     v = max_key(v, dpp_key<0xb1>(v));
     v = max_key(v, dpp_key<0x4e>(v));
     v = max_key(v, dpp_key<0x141>(v));
-    v = max_key(v, dpp_key<0x140>(v));
-    return max_key(max_key(readlane_key(v, 0), readlane_key(v, 16)), max_key(readlane_key(v, 32), readlane_key(v, 48)));
+    return max_key(v, dpp_key<0x140>(v));
 }
-// Number of lanes j < n (n wave-uniform, at most 64) whose key is larger than this lane's.
-__device__ __forceinline__ int wave_rank_n(uint64_t key, int n) {
-    int rank = 0;
-    for (int j = 0; j < n; ++j) rank += readlane_key(key, j) > key;
-    return rank;
-}
-// The same over all 64 lanes; the reads go in batches of 16 ahead of their compares, so no
-// compare waits on the SGPR write of the read just before it.
-__device__ __forceinline__ int wave_rank(uint64_t key) {
+// Number of lanes j < n (n wave-uniform, at most 64) whose key is larger than this lane's,
+// in batches of 16 lanes (the reads of a batch ahead of its compares); lanes from n up to the
+// end of the last batch must hold keys no larger than any counted lane's (0 for an empty slot).
+__device__ __forceinline__ int wave_rank_upto(uint64_t key, int n) {
     const int hi = static_cast<int>(key >> 32), lo = static_cast<int>(key);
     int rank = 0;
 #pragma unroll
     for (int j0 = 0; j0 < 64; j0 += 16) {
+        if (j0 >= n) break;  // uniform
         uint32_t h[16], w[16];
 #pragma unroll
         for (int j = 0; j < 16; ++j) {
@@ -271,21 +265,21 @@ __device__ __forceinline__ void emit_best(uint64_t key, float v, int rank, bool 
 //
 // Steps (each thread holds experts t + 256 m):
 //   1. keys; per-wave softmax partials (max, sum of exp); a sample of two keys per 64-expert
-//      group (the group's two largest, by DPP wave maxima), when two per group reach k;
+//      group: the largest key of each of its four 16-lane rows (DPP row maxima), when the
+//      samples number at least k;
 //   2. theta = the k-th largest sample: the samples are keys, so at least k keys are at
 //      least theta and every key of the top k is; those keys (the survivors, typically
 //      10 to 30) are collected in LDS;
 //   3. the survivors, or without a sample every key, go through the ranking merge tree
 //      until one group of at most 64 is left, whose ranks are the selection order.
-// Nothing is stored to memory before the pointer copies at the end: vmcnt counts stores as
-// well as loads, so a store issued before the wait for the table loads would hold that wait
-// for a store round trip.
+// No wave stores to memory before it has waited for its table loads: vmcnt counts stores as
+// well as loads, so a store issued before that wait would hold it for a store round trip.
 __device__ void route_block(const LayerArgs &a) {
     constexpr int kPer = kMaxExperts / 256;  // experts per thread: e = t + 256 * m
     constexpr int kMaxCand = kMaxExperts / 64 * kMaxTopK;
     __shared__ uint64_t cand_k[2][kMaxCand];
     __shared__ float cand_v[2][kMaxCand];
-    __shared__ uint64_t samp_s[2 * (kMaxExperts / 64)];
+    __shared__ uint64_t samp_s[4 * (kMaxExperts / 64)];
     __shared__ float stat_s[2][4];
     __shared__ uint32_t nsurv_s;
     __shared__ uint8_t slot_s[kMaxExperts];  // selection slot of expert e; 0xff: not selected
@@ -350,20 +344,15 @@ __device__ void route_block(const LayerArgs &a) {
         }
     }
     const int g1 = (a.E + 63) / 64;  // 64-expert groups
-    const bool sampled = 2 * g1 >= a.k;
+    const int ns = 4 * g1;           // samples: the largest key of each 16-lane row of a group
+    const bool sampled = ns >= a.k;
     if (sampled) {
 #pragma unroll
         for (int m = 0; m < kPer; ++m) {
             const int g = 4 * m + wave;
             if (g < g1) {  // uniform per wave
-                uint64_t kk = key[m];
-                const uint64_t m1 = wave_max_key(kk);
-                if (kk == m1) kk = 0;
-                const uint64_t m2 = wave_max_key(kk);
-                if (lane == 0) {
-                    samp_s[2 * g] = m1;
-                    samp_s[2 * g + 1] = m2;
-                }
+                const uint64_t rm = row_max_key(key[m]);
+                if ((lane & 15) == 0) samp_s[4 * g + (lane >> 4)] = rm;
             }
         }
     }
@@ -379,29 +368,34 @@ __device__ void route_block(const LayerArgs &a) {
     const bool nan_route = soft && !(S > 0.f);  // a NaN or infinite logit: every probability NaN
     int n = 0, buf = 0;
     if (sampled) {
-        // 2. theta and the survivors
-        const int ns = 2 * g1;
+        // 2. theta (every wave computes it) and the survivors, one LDS atomic per wave
         const uint64_t ks = lane < ns ? samp_s[lane] : 0;
-        const int rs = wave_rank_n(ks, ns);
+        const int rs = wave_rank_upto(ks, ns);
         const uint64_t hit = __builtin_amdgcn_ballot_w64(lane < ns && rs == a.k - 1);
         const uint64_t theta = hit ? readlane_key(ks, __builtin_ctzll(hit)) : 0;
+        bool sv[kPer];
+        uint64_t mask[kPer];
+        uint32_t cnt = 0;
 #pragma unroll
         for (int m = 0; m < kPer; ++m) {
-            if (256 * m >= a.E) break;  // uniform
-            const bool sv = key[m] != 0 && key[m] >= theta;
-            const uint64_t mask = __builtin_amdgcn_ballot_w64(sv);
-            if (mask) {  // uniform
-                uint32_t base = 0;
-                if (lane == 0) base = atomicAdd(&nsurv_s, static_cast<uint32_t>(__builtin_popcountll(mask)));
-                base = __builtin_amdgcn_readfirstlane(base);
-                const uint32_t pos =
-                    base + __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(mask >> 32),
-                                                     __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(mask), 0u));
-                if (sv && pos < kMaxCand) {
-                    cand_k[0][pos] = key[m];
-                    cand_v[0][pos] = v[m];
-                }
+            sv[m] = key[m] != 0 && key[m] >= theta;
+            mask[m] = __builtin_amdgcn_ballot_w64(sv[m]);
+            cnt += static_cast<uint32_t>(__builtin_popcountll(mask[m]));
+        }
+        uint32_t base = 0;
+        if (cnt) {  // uniform
+            if (lane == 0) base = atomicAdd(&nsurv_s, cnt);
+            base = __builtin_amdgcn_readfirstlane(base);
+        }
+#pragma unroll
+        for (int m = 0; m < kPer; ++m) {
+            const uint32_t pos = base + __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(mask[m] >> 32),
+                                                                  __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(mask[m]), 0u));
+            if (sv[m] && pos < kMaxCand) {
+                cand_k[0][pos] = key[m];
+                cand_v[0][pos] = v[m];
             }
+            base += static_cast<uint32_t>(__builtin_popcountll(mask[m]));
         }
         __syncthreads();
         n = static_cast<int>(nsurv_s);
@@ -426,13 +420,30 @@ __device__ void route_block(const LayerArgs &a) {
             const int c = g * 64 + lane;
             const uint64_t kc = c < n ? cand_k[buf][c] : 0;
             const float vc = c < n ? cand_v[buf][c] : 0.f;
-            emit_best(kc, vc, wave_rank(kc), kc != 0, a.k, cand_k[buf ^ 1] + g * a.k, cand_v[buf ^ 1] + g * a.k);
+            emit_best(kc, vc, wave_rank_upto(kc, 64), kc != 0, a.k, cand_k[buf ^ 1] + g * a.k, cand_v[buf ^ 1] + g * a.k);
         }
         buf ^= 1;
         n = ng * a.k;
         __syncthreads();
     }
-    // the last group (wave 0): the lane of rank r < k holds the r-th selected expert
+    // the router records of this thread's experts, after the wave's wait for its table loads
+    auto store_records = [&]() {
+#pragma unroll
+        for (int m = 0; m < kPer; ++m)
+#pragma unroll
+            for (int q = 0; q < 3; ++q) asm volatile("" ::"v"(tab[m][q].x), "v"(tab[m][q].w));
+#pragma unroll
+        for (int m = 0; m < kPer; ++m) {
+            const int e = t + 256 * m;
+            if (e < a.E) {
+                const float sc = soft ? expf(l[m] - M) / S : v[m];
+                a.ws.scores[e] = sc;
+                a.ws.corrected[e] = soft ? sc : sel[m];
+            }
+        }
+    };
+    // the last group (wave 0): the lane of rank r < k holds the r-th selected expert; waves
+    // 1-3 store their records meanwhile
     bool chosen = false;
     int rank = 0, esel = 0;
     float wsel = 0.f;
@@ -445,7 +456,7 @@ __device__ void route_block(const LayerArgs &a) {
             chosen = lane < a.k;
             sc = __int_as_float(0x7fc00000);
         } else {
-            rank = wave_rank_n(kc, n);
+            rank = wave_rank_upto(kc, n);
             chosen = kc != 0 && rank < a.k;
             esel = key_expert(kc);
             sc = soft ? expf(vc - M) / S : vc;
@@ -454,6 +465,8 @@ __device__ void route_block(const LayerArgs &a) {
         const float norm = (a.renorm && a.k > 1) ? 1.0f / (wsum + 1e-20f) : 1.0f;
         wsel = sc * norm * a.scaling;
         if (chosen) slot_s[esel] = static_cast<uint8_t>(rank);
+    } else {
+        store_records();
     }
     if (a.table) {  // the owner of each selected expert writes its pointers
         __syncthreads();
@@ -474,15 +487,7 @@ __device__ void route_block(const LayerArgs &a) {
         a.ws.topk_idx[rank] = esel;
         a.ws.topk_w[rank] = wsel;
     }
-#pragma unroll
-    for (int m = 0; m < kPer; ++m) {
-        const int e = t + 256 * m;
-        if (e < a.E) {
-            const float sc = soft ? expf(l[m] - M) / S : v[m];
-            a.ws.scores[e] = sc;
-            a.ws.corrected[e] = soft ? sc : sel[m];
-        }
-    }
+    if (wave == 0) store_records();
 }
 
 // ------------------------------------------------------------------ batched selection
@@ -501,8 +506,10 @@ __global__ __launch_bounds__(256) void topk_kernel(LayerArgs a, int64_t ld_logit
 }
 
 // ------------------------------------------------------------------ L1
-// CHH: bf16 chunks (8 elements) per lane over H.
-template <typename XT, int CHH>
+// CHH: bf16 chunks (8 elements) per lane over H.  UP_DELAY: the shared blocks issue their up
+// rows' loads ~1.6 us after their gate rows' (a template parameter: a runtime branch between
+// the two load orders measured as slow as no delay at all).
+template <typename XT, int CHH, bool UP_DELAY>
 __global__ __launch_bounds__(256) void layer_l1(LayerArgs a) {
     extern __shared__ uint4 smem[];
     __shared__ uint32_t last_s;
@@ -599,12 +606,33 @@ __global__ __launch_bounds__(256) void layer_l1(LayerArgs a) {
         const auto rg = make_rsrc(a.sh_gate, static_cast<uint32_t>(a.Is) * row_bytes);
         const auto ru = make_rsrc(a.sh_up, static_cast<uint32_t>(a.Is) * row_bytes);
         uint4 wg[CHH], wu[CHH];
+        if constexpr (UP_DELAY) {
+            // The whole grid is resident at once, so router blocks share their CUs with these
+            // blocks, and a CU delivers about 10 bytes per clock to all its blocks together:
+            // with the up rows' loads held back the router rows get a larger share of their
+            // CU, the last router block finishes earlier and the routing runs under this
+            // stream (the gate rows keep every CU busy meanwhile).
 #pragma unroll
-        for (int u = 0; u < CHH; ++u) {
-            const int c = u * 64 + lane;
-            const uint32_t off = (v && c < nch) ? static_cast<uint32_t>(i) * row_bytes + c * 16u : kOobOffset;
-            wg[u] = buf_load16(rg, off);
-            wu[u] = buf_load16(ru, off);
+            for (int u = 0; u < CHH; ++u) {
+                const int c = u * 64 + lane;
+                wg[u] = buf_load16(rg, (v && c < nch) ? static_cast<uint32_t>(i) * row_bytes + c * 16u : kOobOffset);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+            __builtin_amdgcn_s_sleep(60);
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int u = 0; u < CHH; ++u) {
+                const int c = u * 64 + lane;
+                wu[u] = buf_load16(ru, (v && c < nch) ? static_cast<uint32_t>(i) * row_bytes + c * 16u : kOobOffset);
+            }
+        } else {
+#pragma unroll
+            for (int u = 0; u < CHH; ++u) {
+                const int c = u * 64 + lane;
+                const uint32_t off = (v && c < nch) ? static_cast<uint32_t>(i) * row_bytes + c * 16u : kOobOffset;
+                wg[u] = buf_load16(rg, off);
+                wu[u] = buf_load16(ru, off);
+            }
         }
         x_store<XT, XREG, false>(smem, xr);
         __syncthreads();
@@ -899,6 +927,24 @@ static LayerWsLayout layer_ws_layout(int64_t H, int64_t I, int64_t Is, int64_t E
     return L;
 }
 
+// Whether a grid of `blocks` blocks of layer_l1<XT, C> is resident all at once on the current
+// device (CUs x blocks per CU at the kernel's occupancy), computed once per device.
+constexpr int kMaxDevices = 64;
+template <typename XT, int C, bool D>
+static bool l1_one_round(int blocks, size_t lds) {
+    static int resident[kMaxDevices] = {};  // blocks held at once + 1; 0: not computed yet
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return false;
+    if (!resident[dev]) {
+        int per_cu = 0, cus = 0;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, layer_l1<XT, C, D>, 256, lds) != hipSuccess ||
+            hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+            return false;
+        resident[dev] = per_cu * cus + 1;
+    }
+    return blocks < resident[dev];
+}
+
 template <typename XT>
 static int launch_l1(LayerArgs &a, bool with_shared, hipStream_t st) {
     const int chh = static_cast<int>(cdiv(a.H / 8, 64));
@@ -908,7 +954,10 @@ static int launch_l1(LayerArgs &a, bool with_shared, hipStream_t st) {
     const size_t lds = static_cast<size_t>(256) * x_regs<XT>() * 16;
 #define K3_L1(C) \
     if (chh <= C) { \
-        layer_l1<XT, C><<<dim3(blocks), 256, lds, st>>>(a); \
+        if (!a.lat_down && with_shared && l1_one_round<XT, C, true>(blocks, lds)) \
+            layer_l1<XT, C, true><<<dim3(blocks), 256, lds, st>>>(a); \
+        else \
+            layer_l1<XT, C, false><<<dim3(blocks), 256, lds, st>>>(a); \
         return check_hip(hipGetLastError(), "moe layer L1"); \
     }
     K3_L1(4) K3_L1(8) K3_L1(12) K3_L1(16)

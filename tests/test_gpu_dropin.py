@@ -111,12 +111,14 @@ def test_topk_ties_go_to_lower_index_and_empty_batch():
               T.stream(z))
 
 
-@pytest.mark.parametrize("case", ["ties_across_groups", "clustered", "all_equal", "random_1024", "softmax_nan"])
+@pytest.mark.parametrize("case", ["ties_across_groups", "clustered", "all_equal", "random_1024", "unsampled",
+                                  "softmax_nan"])
 def test_topk_every_selection_path(case):
     """Rows built to reach each path of the selection: a few candidates at or above the
-    bound sampled from each 64-expert group (random rows), more than 64 of them (a ranking
-    level before the last: 100 hot experts in the first two groups), more than 256 (every
-    key ranked: all logits equal), ties across groups and waves, and a NaN logit under
+    bound sampled from the experts (the largest key of every 16 experts; random rows), more
+    than 64 of them (a ranking level before the last: 100 hot experts in the first two
+    groups of 64, or all logits equal: 241 candidates), fewer samples than k (every key
+    ranked: 100 experts, top-12), ties across groups and waves, and a NaN logit under
     softmax (every probability NaN: the k lowest indices, NaN weights and scores)."""
     from k3hip import _lib
     rng = np.random.default_rng(sum(map(ord, case)))
@@ -139,6 +141,10 @@ def test_topk_every_selection_path(case):
         E, k = 1024, 16
         logits = np.zeros((2, E), np.float32)
         logits[1, [1000, 999]] = 1.0
+    elif case == "unsampled":
+        E, k = 100, 12
+        logits = (rng.standard_normal((4, E)) * 2).astype(np.float32)
+        logits[3, ::7] = 5.0
     elif case == "random_1024":
         E, k = 1024, 16
         logits = (rng.standard_normal((8, E)) * 2).astype(np.float32)
