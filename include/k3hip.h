@@ -41,7 +41,8 @@ extern "C" {
 #define K3_ACT_SITU  1   /* b*tanh(g/b)*sigmoid(g) * bl*tanh(u/bl) (air_llm/models/kimi_k3/ops.py:17-28) */
 
 /* ---- router enums ------------------------------------------------------------------ */
-#define K3_ROUTE_SOFTMAX      0  /* softmax(logits), top-k on probabilities                 */
+#define K3_ROUTE_SOFTMAX      0  /* softmax(logits); top-k in probability order (selected on the
+                                    logits, which order exactly as the probabilities do)  */
 #define K3_ROUTE_SIGMOID_BIAS 1  /* sigmoid(logits); select on +bias; weights from raw (moe.py:65-76) */
 
 const char *k3_last_error(void);
@@ -119,15 +120,18 @@ int k3_moe_layer_workspace_offsets(int64_t H, int64_t I, int64_t shared_I, int64
  * k3ref/layers.py:214-224): router_w bf16 [E, H]; route_kind K3_ROUTE_SOFTMAX or
  * K3_ROUTE_SIGMOID_BIAS (router_bias f32 [E] added for selection only); weights gathered
  * from the raw scores, divided by (sum + 1e-20) when renormalize and top_k > 1, times
- * scaling.  Ties go to the lower expert index.  Results land in the workspace records. */
+ * scaling.  Ties go to the lower expert index; softmax selects on the logits (the
+ * probabilities' order without fp32 rounding ties), and a NaN or infinite logit makes every
+ * probability NaN and selects the k lowest indices.  Results land in the workspace records. */
 int k3_moe_route(const void *x, int x_dtype, const void *router_w, const void *router_bias,
                  int route_kind, int renormalize, float scaling, int64_t H, int64_t n_experts,
                  int64_t top_k, void *workspace, int64_t workspace_bytes, void *stream);
 
 /* Selection half of the router for T tokens at once, from router logits computed by the
  * caller (fp32 [T, E], row stride ld_logits; the prefill path takes them from one GEMM over
- * all tokens): per token, scores = softmax or sigmoid of the logits, selection on scores
- * (+ router_bias for K3_ROUTE_SIGMOID_BIAS), exact top-k with ties to the lower expert index,
+ * all tokens): per token, scores = softmax or sigmoid of the logits, selection on the logits
+ * for softmax (the probabilities' order) and on scores + router_bias for
+ * K3_ROUTE_SIGMOID_BIAS, exact top-k with ties to the lower expert index,
  * weights gathered from the raw scores, divided by (sum + 1e-20) when renormalize and
  * top_k > 1, times scaling.  Outputs: expert_idx int32 [T, top_k] (largest first),
  * expert_w f32 [T, top_k], scores and corrected f32 [T, E].  One block per token.
