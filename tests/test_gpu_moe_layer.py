@@ -73,6 +73,9 @@ CASES = [
     (7168, 2048, 384, 8, 2048, 12, "softmax", "silu", torch.bfloat16),
     (3584, 3072, 96, 8, 0, 6, "sigmoid_bias", "situ", torch.bfloat16),
     (2048, 4096, 32, 16, 0, 8, "sigmoid_bias", "situ", torch.bfloat16),
+    # a shared expert wide enough that L1's grid takes more than one round of blocks (the
+    # launch without the up-row delay)
+    (2048, 512, 64, 4, 6144, 8, "softmax", "silu", torch.bfloat16),
 ]
 
 
