@@ -264,12 +264,13 @@ __device__ __forceinline__ void emit_best(uint64_t key, float v, int rank, bool 
 // are selected, as for any all-NaN score row.
 //
 // Steps (each thread holds experts t + 256 m):
-//   1. keys; per-wave softmax partials (max, sum of exp); a sample of two keys per 64-expert
-//      group: the largest key of each of its four 16-lane rows (DPP row maxima), when the
-//      samples number at least k;
+//   1. keys; per-wave softmax partials (max, sum of exp); a sample of four keys per
+//      64-expert group: the largest key of each of its 16-lane rows (DPP row maxima), when
+//      the samples number at least k;
 //   2. theta = the k-th largest sample: the samples are keys, so at least k keys are at
-//      least theta and every key of the top k is; those keys (the survivors, typically
-//      10 to 30) are collected in LDS;
+//      least theta and every key of the top k is; only the k rows whose maximum reaches
+//      theta hold such keys, so these survivors number at most 16 k (typically 9 to 20);
+//      they are collected in LDS;
 //   3. the survivors, or without a sample every key, go through the ranking merge tree
 //      until one group of at most 64 is left, whose ranks are the selection order.
 // No wave stores to memory before it has waited for its table loads: vmcnt counts stores as
