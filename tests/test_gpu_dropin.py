@@ -165,6 +165,21 @@ def test_topk_every_selection_path(case):
     assert np.allclose(co, wcorr, rtol=2e-6, atol=1e-7)
 
 
+@pytest.mark.parametrize("E,k", [(384, 8), (896, 16), (1024, 16), (100, 12)])
+def test_topk_many_rows_with_ties(E, k):
+    """512 softmax rows whose logits lie on a half-integer grid, so most rows hold exact ties
+    across 64-expert groups and across the sampled bound: the selection (order included)
+    must be the oracle's, ties to the lower index."""
+    from k3hip import _lib
+    rng = np.random.default_rng(E * 31 + k)
+    logits = (np.round(rng.standard_normal((512, E)) * 3.0) / 2.0).astype(np.float32)
+    idx, w, sc, _ = _topk_run(logits, None, _lib.K3_ROUTE_SOFTMAX, k, scaling=1.0)
+    widx, ww, wraw, _ = _oracle_select(logits, None, "softmax", k)
+    assert np.array_equal(idx, widx)
+    assert np.allclose(w, ww, rtol=2e-6, atol=1e-9)
+    assert np.allclose(sc, wraw, rtol=2e-6, atol=1e-12)
+
+
 def test_topk_rejects_bad_arguments():
     from k3hip import _lib
     from k3hip import _torch as T
