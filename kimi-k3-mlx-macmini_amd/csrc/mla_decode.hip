@@ -275,6 +275,33 @@ __global__ __launch_bounds__(512, 1) void mla_attn_kernel(AttnArgs a) {
     uint4 stg[D][kPerWave];
     load_round(stg[0], 0);
     load_round(stg[1], 1);
+    // score waves: qa operands (head h0 + r16, this half's columns; heads past H load zeros)
+    // and the first rounds' rope rows, issued together with the first rounds' latent rows so
+    // their latencies overlap (context waves issue none of them)
+    bf16x8 qhi[kHalfKb + 1], qlo[kHalfKb + 1];
+    const auto rr = make_rsrc(a.rot, a.rot_bytes);
+    auto load_rope = [&](int rd) -> uint4 {
+        const int tile = rd * kRoundTiles + cls;
+        const int t = t_begin + tile * kStepT + r16;
+        const bool ok = tile < nsteps && t < t_end;
+        return buf_load16(rr, ok ? static_cast<uint32_t>(t) * a.rot_row_bytes + (half * 32 + q4 * 8) * 2u
+                                 : kOobOffset);
+    };
+    uint4 rope[D], rope0;
+    if (!ctx_role) {
+        const uint32_t qbytes = static_cast<uint32_t>(a.H) * kQaLd * 2;
+        const auto rqh = make_rsrc(a.qa_hi, qbytes), rql = make_rsrc(a.qa_lo, qbytes);
+        const uint32_t qrow = h0 + r16 < a.H ? static_cast<uint32_t>((h0 + r16) * kQaLd) * 2u : kOobOffset;
+#pragma unroll
+        for (int k = 0; k <= kHalfKb; ++k) {
+            const int col = k < kHalfKb ? (half * kHalfKb + k) * 32 + q4 * 8 : kR + half * 32 + q4 * 8;
+            qhi[k] = __builtin_bit_cast(bf16x8, buf_load16(rqh, qrow + static_cast<uint32_t>(col) * 2u));
+            qlo[k] = __builtin_bit_cast(bf16x8, buf_load16(rql, qrow + static_cast<uint32_t>(col) * 2u));
+        }
+#pragma unroll
+        for (int d = 1; d <= D; ++d) rope[d % D] = load_rope(d);
+        rope0 = load_rope(0);
+    }
     store_round(stg[0], 0);
     store_round(stg[1], 1);
 #pragma unroll
@@ -285,36 +312,6 @@ __global__ __launch_bounds__(512, 1) void mla_attn_kernel(AttnArgs a) {
 
     if (!ctx_role) {
         // ================= score waves
-        // qa operands of head h0 + r16 over this half's columns (heads past H load zeros):
-        // latent k-blocks 8 half .. +8 and rope k-block half
-        bf16x8 qhi[kHalfKb + 1], qlo[kHalfKb + 1];
-        {
-            const uint32_t qbytes = static_cast<uint32_t>(a.H) * kQaLd * 2;
-            const auto rqh = make_rsrc(a.qa_hi, qbytes), rql = make_rsrc(a.qa_lo, qbytes);
-            const uint32_t qrow = h0 + r16 < a.H ? static_cast<uint32_t>((h0 + r16) * kQaLd) * 2u : kOobOffset;
-#pragma unroll
-            for (int k = 0; k <= kHalfKb; ++k) {
-                const int col = k < kHalfKb ? (half * kHalfKb + k) * 32 + q4 * 8 : kR + half * 32 + q4 * 8;
-                qhi[k] = __builtin_bit_cast(bf16x8, buf_load16(rqh, qrow + static_cast<uint32_t>(col) * 2u));
-                qlo[k] = __builtin_bit_cast(bf16x8, buf_load16(rql, qrow + static_cast<uint32_t>(col) * 2u));
-            }
-        }
-        // rope operand of a round's tile, loaded straight into operand layout (lane (token
-        // r16, q4): 16 bytes of the row at rope column 32 half + 8 q4), D rounds ahead
-        const auto rr = make_rsrc(a.rot, a.rot_bytes);
-        auto load_rope = [&](int rd) -> uint4 {
-            const int tile = rd * kRoundTiles + cls;
-            const int t = t_begin + tile * kStepT + r16;
-            const bool ok = tile < nsteps && t < t_end;
-            return buf_load16(rr, ok ? static_cast<uint32_t>(t) * a.rot_row_bytes + (half * 32 + q4 * 8) * 2u
-                                     : kOobOffset);
-        };
-        // ring of D: slot s holds the round r with r % D == s; round 0 separately
-        uint4 rope[D];
-#pragma unroll
-        for (int d = 1; d <= D; ++d) rope[d % D] = load_rope(d);
-        const uint4 rope0 = load_rope(0);
-
         float m_ref = -INFINITY, l_run = 0.f;  // head h0 + r16, class cls (both halves alike)
         // partial scores of round rd over this half's columns
         auto partial = [&](int rd, const uint4 &rp) -> f32x4_t {
