@@ -11,6 +11,8 @@
 // rows of more than 4096 values, so one staged vector serves more rows).
 #pragma once
 
+#include <algorithm>
+
 #include "k3_common.h"
 
 namespace k3 {
@@ -193,6 +195,100 @@ __global__ __launch_bounds__(64 * NW) void step_rows_kernel(RowsArgs a) {
     }
 }
 
+// Persistent form for wide rows: about one block per CU walks the row groups
+// g = blockIdx.x, blockIdx.x + gridDim.x, ... of the concatenated row sets (NW rows per group,
+// one per wave, a.blocks[s] groups in set s).  The input vector is staged once per block and
+// every wave keeps the next group's row in flight while it reduces the current one, so no
+// block restages the vector and the CUs share the rows evenly.  No cache append.
+template <int MODE, int CH, int NW>
+__global__ __launch_bounds__(64 * NW) void step_rows_loop_kernel(RowsArgs a) {
+    extern __shared__ float vs[];
+    __shared__ float red[NW];
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+    const int K = a.K, nch = K >> 3;
+    const uint32_t rowb = static_cast<uint32_t>(K) * 2u;
+    int total = 0;
+#pragma unroll
+    for (int s = 0; s < kRowSets; ++s) total += a.blocks[s];
+    const int G = static_cast<int>(gridDim.x);
+    // this wave's row of group g: set s, row n (none when g >= total or n >= N[s]; such rows
+    // load zeros through out-of-range offsets and store nothing)
+    auto locate = [&](int g, int &s, int &n) {
+        int b = g;
+        s = 0;
+        while (s < kRowSets - 1 && b >= a.blocks[s]) b -= a.blocks[s++];
+        n = b * NW + wave;
+    };
+    auto load_row = [&](uint4 (&wr)[CH], int g) {
+        int s, n;
+        locate(g, s, n);
+        const bool ok = g < total && n < a.N[s];
+        const auto rw = make_rsrc(a.w[s], static_cast<uint32_t>(a.N[s]) * rowb);
+#pragma unroll
+        for (int u = 0; u < CH; ++u) {
+            const int c = u * 64 + lane;
+            wr[u] = buf_load16(rw, (ok && c < nch) ? static_cast<uint32_t>(n) * rowb + c * 16u : kOobOffset);
+        }
+    };
+    auto reduce_row = [&](const uint4 (&wr)[CH], int g) {
+        int s, n;
+        locate(g, s, n);
+        const float4 *v4 = reinterpret_cast<const float4 *>(vs);
+        float acc0 = 0.f, acc1 = 0.f;
+#pragma unroll
+        for (int u = 0; u < CH; ++u) {
+            const int c = u * 64 + lane;
+            if (c < nch) {
+                if (u & 1)
+                    acc1 = dot8_bf16_f32(wr[u], v4[2 * c], v4[2 * c + 1], acc1);
+                else
+                    acc0 = dot8_bf16_f32(wr[u], v4[2 * c], v4[2 * c + 1], acc0);
+            }
+        }
+        const float t = wave_sum_to_lane63(acc0 + acc1);
+        if (lane == 63 && g < total && n < a.N[s]) {
+            if (a.out) {
+                const float t2 = a.add ? t + a.add[n] : t;
+                if (a.out_bf16)
+                    static_cast<uint16_t *>(a.out)[n] = f32_to_bf16(t2);
+                else
+                    static_cast<float *>(a.out)[n] = t2;
+            } else {
+                a.y[s][n] = t;
+            }
+        }
+    };
+    uint4 wa[CH], wb[CH];
+    int g = static_cast<int>(blockIdx.x);
+    load_row(wa, g);
+    stage_vector<MODE, NW>(a, vs, red);
+    for (; g < total; g += 2 * G) {
+        load_row(wb, g + G);
+        reduce_row(wa, g);
+        if (g + G >= total) break;
+        load_row(wa, g + 2 * G);
+        reduce_row(wb, g + G);
+    }
+}
+
+// Resident blocks of the persistent form per device (occupancy x CUs), cached.
+template <int MODE, int CH, int NW>
+int rows_loop_blocks(size_t lds) {
+    constexpr int kDevs = 64;
+    static int cached[kDevs] = {};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kDevs) return 0;
+    if (!cached[dev]) {
+        int per_cu = 0, cus = 0;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, step_rows_loop_kernel<MODE, CH, NW>, 64 * NW, lds) !=
+                hipSuccess ||
+            hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+            return 0;
+        cached[dev] = std::max(1, per_cu) * cus;
+    }
+    return cached[dev];
+}
+
 template <int MODE, int CH>
 int launch_rows_ch(RowsArgs &a, hipStream_t st) {
     // rows of 4097..8192 values: eight waves of one row, so one staged vector serves 8 rows;
@@ -220,6 +316,29 @@ int launch_rows(RowsArgs &a, hipStream_t st) {
     if (ch <= 16) return launch_rows_ch<MODE, 16>(a, st);
     if (ch <= 24) return launch_rows_ch<MODE, 24>(a, st);
     return set_error(K3_ERR_SHAPE, "dense rows: input width %d above %d", a.K, kMaxWidth);
+}
+
+// Row sets of 4097..12288 values through the persistent form (eight waves, one row each);
+// other widths, and the normalising launch with the cache append, take launch_rows.
+template <int MODE>
+int launch_rows_loop(RowsArgs &a, hipStream_t st) {
+    const int ch = static_cast<int>(cdiv(a.K / 8, 64));
+    if (ch <= 8 || ch > 24 || (MODE == kModeNorm && a.append)) return launch_rows<MODE>(a, st);
+    constexpr int NW = 8;
+    int total = 0;
+    for (int s = 0; s < kRowSets; ++s) {
+        a.blocks[s] = a.w[s] ? static_cast<int>(cdiv(a.N[s], NW)) : 0;
+        total += a.blocks[s];
+    }
+    const size_t lds = static_cast<size_t>(a.K) * 4;
+    auto go = [&](auto kern, int resident) {
+        if (resident <= 0) return set_error(K3_ERR_HIP, "dense rows (persistent): occupancy query failed");
+        const int grid = std::max(1, std::min(total, resident));
+        kern<<<dim3(static_cast<unsigned>(grid)), 64 * NW, lds, st>>>(a);
+        return check_hip(hipGetLastError(), "dense rows (persistent) launch");
+    };
+    if (ch <= 16) return go(step_rows_loop_kernel<MODE, 16, NW>, rows_loop_blocks<MODE, 16, NW>(lds));
+    return go(step_rows_loop_kernel<MODE, 24, NW>, rows_loop_blocks<MODE, 24, NW>(lds));
 }
 
 }  // namespace

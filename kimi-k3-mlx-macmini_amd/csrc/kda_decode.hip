@@ -417,10 +417,12 @@ extern "C" int k3_kda_step_decode(const void *x, int x_dtype, const void *q_proj
     kda_step_kernel<<<dim3(static_cast<unsigned>(heads * (kKdaK / kKdaVS))), 256, 0, st>>>(k);
     rc = check_hip(hipGetLastError(), "kda step: recurrence launch");
     if (rc) return rc;
-    // K4: rows of o_proj against the gated heads scaled by their RMS norms
+    // K4: rows of o_proj against the gated heads scaled by their RMS norms, in the persistent
+    // row form (one block per CU stages the 48 KB vector once): measured faster for this
+    // launch, while K1 measured slower in that form
     RowsArgs a4{};
     a4.o = wo, a4.gl = whss, a4.nw = o_norm, a4.eps = eps, a4.K = static_cast<int>(P);
     a4.w[0] = static_cast<const uint16_t *>(o_proj), a4.N[0] = static_cast<int>(hidden);
     a4.out = out, a4.out_bf16 = out_dtype == K3_BF16;
-    return launch_rows<kModeHeadNorm>(a4, st);
+    return launch_rows_loop<kModeHeadNorm>(a4, st);
 }
