@@ -293,8 +293,9 @@ template <int MODE, int CH>
 int launch_rows_ch(RowsArgs &a, hipStream_t st) {
     // rows of 4097..8192 values: eight waves of one row, so one staged vector serves 8 rows;
     // rows of 8193..12288 values: eight waves of two rows (16 rows per staged 48 KB vector).
-    // Measured faster than four-wave blocks for both.
-    constexpr int R = CH >= 24 ? 2 : (CH >= 16 ? 1 : (CH >= 8 ? 2 : (CH >= 4 ? 4 : 8)));
+    // Measured faster than four-wave blocks for both.  Rows of 1025..2048 values take two
+    // rows per wave (measured faster than four: twice the blocks over the same rows).
+    constexpr int R = CH >= 24 ? 2 : (CH >= 16 ? 1 : (CH >= 8 ? 2 : (CH >= 4 ? 2 : 8)));
     constexpr int NW = CH >= 16 ? 8 : 4;
     int total = 0;
     for (int s = 0; s < kRowSets; ++s) {
