@@ -8,7 +8,7 @@
 //                  given as four partial sums in gl (o already carries its gate)
 // Every block issues its weight rows first, then stages the vector, then reduces: a lane
 // takes 16-byte chunks (8 bf16) l, l + 64, ... of a row; R rows per wave, 4 waves (8 for
-// rows of more than 4096 values, so one staged vector serves more rows).
+// rows of more than 2048 values, so one staged vector serves more rows).
 #pragma once
 
 #include <algorithm>
@@ -291,12 +291,13 @@ int rows_loop_blocks(size_t lds) {
 
 template <int MODE, int CH>
 int launch_rows_ch(RowsArgs &a, hipStream_t st) {
+    // rows of 2049..4096 values: eight waves of two rows (16 rows per staged vector);
     // rows of 4097..8192 values: eight waves of one row, so one staged vector serves 8 rows;
     // rows of 8193..12288 values: eight waves of two rows (16 rows per staged 48 KB vector).
-    // Measured faster than four-wave blocks for both.  Rows of 1025..2048 values take two
-    // rows per wave (measured faster than four: twice the blocks over the same rows).
+    // Measured faster than four-wave blocks for all three.  Rows of 1025..2048 values take
+    // two rows per wave in four-wave blocks (measured faster than four rows per wave).
     constexpr int R = CH >= 24 ? 2 : (CH >= 16 ? 1 : (CH >= 8 ? 2 : (CH >= 4 ? 2 : 8)));
-    constexpr int NW = CH >= 16 ? 8 : 4;
+    constexpr int NW = CH >= 8 ? 8 : 4;
     int total = 0;
     for (int s = 0; s < kRowSets; ++s) {
         a.blocks[s] = a.w[s] ? static_cast<int>(cdiv(a.N[s], NW * R)) : 0;
