@@ -125,6 +125,22 @@ def test_kda_layer_k3_shapes_one_token():
     assert r_out <= 2e-5 and r_S <= 2e-5
 
 
+def test_kda_layer_persistent_o_proj_odd_shapes():
+    """67 heads (o_proj input 8576 wide: 17 of the lane's 24 chunk slots hold data) and hidden
+    4104 (513 row groups of 8 over the persistent o_proj launch's blocks, so blocks take two
+    or three groups and the last pass ends half way), one token on a random state."""
+    cfg, w, attn, rng = _layer(25, 4104, 67)
+    x = om.bf16_round(rng.standard_normal((1, 1, 4104)).astype(np.float32))
+    S0 = (rng.standard_normal((1, 67, 128, 128)) * 0.1).astype(np.float32)
+    cv0 = tuple((rng.standard_normal((1, 3, 67 * 128)) * 0.5).astype(np.float32) for _ in range(3))
+    out, S, _ = attn(torch.from_numpy(x).to(DEV).to(torch.bfloat16), state=torch.from_numpy(S0).to(DEV),
+                     conv=tuple(torch.from_numpy(c).to(DEV) for c in cv0))
+    want, S_want, _ = okda.kda_layer(cfg, w, x, S0, cv0)
+    r_out, r_S = om.normwise_rel(out.cpu().numpy(), want), om.normwise_rel(S.cpu().numpy(), S_want)
+    print(f"kda layer 67 heads, hidden 4104: out {r_out:.2e} state {r_S:.2e}")
+    assert r_out <= 2e-5 and r_S <= 2e-5
+
+
 def test_kda_layer_batch_of_two_sequences():
     """Two sequences share the weights and keep their own recurrent and convolution states."""
     cfg, w, attn, rng = _layer(23, 256, 2, scale=0.05)
