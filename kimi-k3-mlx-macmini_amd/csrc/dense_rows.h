@@ -12,6 +12,7 @@
 #pragma once
 
 #include <algorithm>
+#include <atomic>
 
 #include "k3_common.h"
 
@@ -275,18 +276,20 @@ __global__ __launch_bounds__(64 * NW) void step_rows_loop_kernel(RowsArgs a) {
 template <int MODE, int CH, int NW>
 int rows_loop_blocks(size_t lds) {
     constexpr int kDevs = 64;
-    static int cached[kDevs] = {};
+    static std::atomic<int> cached[kDevs] = {};  // 0: not computed yet (racing threads store one value)
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kDevs) return 0;
-    if (!cached[dev]) {
+    int r = cached[dev].load(std::memory_order_relaxed);
+    if (!r) {
         int per_cu = 0, cus = 0;
         if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, step_rows_loop_kernel<MODE, CH, NW>, 64 * NW, lds) !=
                 hipSuccess ||
             hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
             return 0;
-        cached[dev] = std::max(1, per_cu) * cus;
+        r = std::max(1, per_cu) * cus;
+        cached[dev].store(r, std::memory_order_relaxed);
     }
-    return cached[dev];
+    return r;
 }
 
 template <int MODE, int CH>

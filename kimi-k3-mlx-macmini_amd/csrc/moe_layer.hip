@@ -30,6 +30,7 @@
 // anything into LDS or registers it consumes, and stages with unconditional stores, so the
 // in-order vmcnt waits never hold the staging behind the weight stream.
 #include <algorithm>
+#include <atomic>
 
 #include "dense_rows.h"
 #include "moe_common.h"
@@ -933,17 +934,20 @@ static LayerWsLayout layer_ws_layout(int64_t H, int64_t I, int64_t Is, int64_t E
 constexpr int kMaxDevices = 64;
 template <typename XT, int C, bool D>
 static bool l1_one_round(int blocks, size_t lds) {
-    static int resident[kMaxDevices] = {};  // blocks held at once + 1; 0: not computed yet
+    // blocks held at once + 1; 0: not computed yet (threads that race here store one value)
+    static std::atomic<int> resident[kMaxDevices] = {};
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return false;
-    if (!resident[dev]) {
+    int r = resident[dev].load(std::memory_order_relaxed);
+    if (!r) {
         int per_cu = 0, cus = 0;
         if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, layer_l1<XT, C, D>, 256, lds) != hipSuccess ||
             hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
             return false;
-        resident[dev] = per_cu * cus + 1;
+        r = per_cu * cus + 1;
+        resident[dev].store(r, std::memory_order_relaxed);
     }
-    return blocks < resident[dev];
+    return blocks < r;
 }
 
 template <typename XT>
