@@ -307,6 +307,7 @@ int launch_rows_ch(RowsArgs &a, hipStream_t st) {
         total += a.blocks[s];
     }
     if (MODE == kModeNorm && a.append) ++total;
+    if (total == 0) return K3_OK;  // no rows and no cache append: nothing to launch
     step_rows_kernel<MODE, CH, R, NW><<<dim3(static_cast<unsigned>(total)), 64 * NW, static_cast<size_t>(a.K) * 4, st>>>(a);
     return check_hip(hipGetLastError(), "dense rows launch");
 }
@@ -335,6 +336,7 @@ int launch_rows_loop(RowsArgs &a, hipStream_t st) {
         a.blocks[s] = a.w[s] ? static_cast<int>(cdiv(a.N[s], NW)) : 0;
         total += a.blocks[s];
     }
+    if (total == 0) return K3_OK;
     const size_t lds = static_cast<size_t>(a.K) * 4;
     auto go = [&](auto kern, int resident) {
         if (resident <= 0) return set_error(K3_ERR_HIP, "dense rows (persistent): occupancy query failed");
