@@ -87,3 +87,43 @@ def test_threads_on_their_own_streams_match_one_thread():
             assert torch.equal(ffn, want_ffn[t]) and torch.equal(mv, want_mv[t])
     # every rejected call raised, with the message of its own call
     assert len(bad_msgs) == rounds and all(f"K={K} " in m for K, m in bad_msgs), bad_msgs[:3]
+
+
+def test_moe_layer_from_threads_matches_one_thread():
+    """Three threads decode tokens through one RoutedMoE on their own streams: each stream
+    gets its own workspace (arrival counters included), so the launches of different
+    threads never meet, and every output equals the same token's output on one thread."""
+    from k3hip.moe import RoutedMoE
+    from test_gpu_moe_layer import make_layer
+    cfg, w, source, *_ = make_layer(5, 1024, 256, 64, 8, 512)
+    moe = RoutedMoE(cfg, 0, w, source)
+    rng = np.random.default_rng(6)
+    xs = [torch.from_numpy(om.bf16_round(rng.standard_normal((1, 1024)).astype(np.float32))).to(DEV).to(torch.bfloat16)
+          for _ in range(3)]
+    want = [moe(x).clone() for x in xs]
+    torch.cuda.synchronize()
+    rounds = 40
+    results: dict[int, list] = {}
+    errors: list[str] = []
+    start = threading.Barrier(3)
+
+    def worker(t):
+        try:
+            s = torch.cuda.Stream()
+            start.wait()
+            with torch.cuda.stream(s):
+                outs = [moe(xs[t]) for _ in range(rounds)]
+            s.synchronize()
+            results[t] = outs
+        except Exception as e:  # reported below with the thread's index
+            errors.append(f"thread {t}: {e!r}")
+
+    threads = [threading.Thread(target=worker, args=(t,)) for t in range(3)]
+    for th in threads:
+        th.start()
+    for th in threads:
+        th.join(timeout=120)
+    assert not any(th.is_alive() for th in threads), "a thread did not finish"
+    assert not errors, errors
+    for t in range(3):
+        assert len(results[t]) == rounds and all(torch.equal(y, want[t]) for y in results[t])
