@@ -265,6 +265,34 @@ def bench_layer(torch, steps, warmup, dev):
     return sec, len(touched), stats
 
 
+MULTI_T = 4                     # decode tokens per step of the multi-token layer workload
+
+
+def bench_layer_multi(torch, steps, warmup, dev, T=MULTI_T):
+    """The 384-expert layer for T decode tokens per step (RoutedMoE.__call__: router GEMM and
+    top-k, k3_moe_routed_decode over the union of the routed experts, shared expert on the
+    BLAS library).  Returns seconds for `steps` steps and the mean union size / bytes per
+    step, the algorithmic bytes when every union expert, the router and the shared expert
+    are read once."""
+    import numpy as np
+    moe, _ = build_layer(torch, dev)
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(8)
+    n = steps + warmup + 3
+    xs = torch.randn(n * T, H, device=dev, generator=gen).to(torch.bfloat16)
+
+    def step(i):
+        moe(xs[i * T:(i + 1) * T])
+
+    sec, _ = graph_time(torch, step, steps, warmup)
+    stats = None if EAGER else step_stats(torch, step, min(64, steps))
+    unions = [len(set(moe.route(xs[i * T:(i + 1) * T]).expert_indices.view(-1).tolist())) for i in range(steps)]
+    del moe
+    u = float(np.mean(unions))
+    nbytes = E_LAYER * H * 2 + u * EXPERT_BYTES + 3 * H * I * 2
+    return sec, u, nbytes, stats
+
+
 K3_H, K3_L, K3_I, K3_E, K3_K, K3_IS = 7168, 3584, 3072, 896, 16, 6144
 K3_LAYER_BYTES = (K3_E * K3_H * 2 + 2 * K3_L * K3_H * 2 + K3_K * 3 * proj_bytes(K3_I, K3_L)
                   + 3 * K3_IS * K3_H * 2)                                 # 660,602,880
@@ -421,19 +449,22 @@ def bench_prefill(torch, steps, warmup, dev):
 
 
 MLA_H, MLA_T = 64, 32768
-MLA_BYTES = MLA_T * (512 + 64) * 2 + 2 * MLA_H * 128 * 512 * 2 + MLA_H * 192 * 2 + MLA_H * 128 * 4  # 54,575,104
+MLA_BYTES = MLA_T * (512 + 64) * 2 + 2 * MLA_H * 128 * 512 * 2 + MLA_H * 192 * 2 + MLA_H * 128 * 4  # 54,583,296
+MLA_F32_BYTES = MLA_BYTES + MLA_T * (512 + 64) * 2                                                  # 92,332,032
 
 
-def bench_mla(torch, steps, warmup, dev):
-    """Latent-MLA absorbed decode: 64 heads over a 32768-token bf16 latent cache
-    (kv_lora_rank 512 + rope 64), W_UK / W_UV [64, 128, 512] bf16, scale 1/sqrt(192).
-    16 distinct caches and 8 weight sets rotate (737 MB) so the MALL cannot hold them."""
+def bench_mla(torch, steps, warmup, dev, cache_dtype=None):
+    """Latent-MLA absorbed decode: 64 heads over a 32768-token latent cache (kv_lora_rank
+    512 + rope 64; bf16, or fp32 as the reference's default cache), W_UK / W_UV
+    [64, 128, 512] bf16, scale 1/sqrt(192).  16 distinct caches and 8 weight sets rotate
+    (737 MB in bf16) so the MALL cannot hold them."""
     from k3hip.mla import mla_decode_absorbed
     gen = torch.Generator(device=dev)
     gen.manual_seed(1005)
     bf = torch.bfloat16
-    caches = [(torch.randn(MLA_T, 512, device=dev, generator=gen).to(bf),
-               torch.randn(MLA_T, 64, device=dev, generator=gen).to(bf)) for _ in range(16)]
+    cdt = cache_dtype or bf
+    caches = [(torch.randn(MLA_T, 512, device=dev, generator=gen).to(cdt),
+               torch.randn(MLA_T, 64, device=dev, generator=gen).to(cdt)) for _ in range(16)]
     weights = [((torch.randn(MLA_H, 128, 512, device=dev, generator=gen) * 0.02).to(bf),
                 (torch.randn(MLA_H, 128, 512, device=dev, generator=gen) * 0.02).to(bf)) for _ in range(8)]
     q_nope = torch.randn(MLA_H, 128, device=dev, generator=gen).to(bf)
@@ -690,7 +721,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--workloads",
-                    default="expert,sustained,layer,k3layer,ingest,prefill,gemv,mla,mlastep,kda,kdastep,ceiling")
+                    default="expert,sustained,layer,layer4,k3layer,ingest,prefill,gemv,mla,mlaf32,mlastep,kda,"
+                            "kdastep,ceiling")
     ap.add_argument("--eager", action="store_true",
                     help="launch steps one by one instead of replaying a HIP graph (profiler counter runs)")
     args = ap.parse_args()
@@ -757,6 +789,21 @@ def main():
                              "shared_expert": "bf16", "distinct_experts_routed_first32": touched,
                              "launches_per_layer": 3, "step_us": lstats,
                              **counter_fields(cnt.get("moe_layer_b1"))}
+    if "layer4" in work:
+        ms4 = min(K, 128)
+        msec4, union4, bytes4, mstats4 = bench_layer_multi(torch, ms4, min(W, 16), dev)
+        mus4 = msec4 / ms4 * 1e6
+        line["moe_layer_t4"] = {
+            "us_per_step": round(mus4, 2), "tokens_per_step": MULTI_T, "us_per_token": round(mus4 / MULTI_T, 2),
+            "union_experts_mean": round(union4, 2), "bytes_per_step_mean": int(bytes4),
+            "GB/s": round(bytes4 / (mus4 * 1e-6) / 1e9, 1),
+            "pct_hbm_peak": round(100 * bytes4 / (mus4 * 1e-6) / 1e9 / HBM_PEAK_GBS, 1),
+            "bytes_if_per_token": MULTI_T * LAYER_BYTES,
+            "what": "RoutedMoE on 4 tokens: router GEMM + k3_moe_topk, k3_moe_routed_decode over the union "
+                    "of the routed experts (each read once), shared expert on the BLAS library",
+            "step_us": mstats4, **counter_fields(cnt.get("moe_layer_t4"))}
+        if "moe_layer" in line:
+            line["moe_layer_t4"]["vs_4_single_token_layers"] = round(4 * line["moe_layer"]["us_per_layer"] / mus4, 3)
     if "k3layer" in work:
         ks = min(K, 256)
         ksec, ktouched, kstats, kpre = bench_k3_layer(torch, ks, min(W, 32), dev)
@@ -797,6 +844,16 @@ def main():
                               "heads": MLA_H, "tokens": MLA_T, "kv_lora_rank": 512, "rope": 64,
                               "cache": "bf16", "launches": 4, "step_us": mstats,
                               **counter_fields(cnt.get("mla_decode_h64_t32768"))}
+    if "mlaf32" in work:
+        ms = min(K, 128)
+        fsec, fstats = bench_mla(torch, ms, min(W, 16), dev, cache_dtype=torch.float32)
+        fus = fsec / ms * 1e6
+        fgbs = MLA_F32_BYTES / (fus * 1e-6) / 1e9
+        line["mla_decode_f32_cache"] = {
+            "us": round(fus, 2), "GB/s": round(fgbs, 1), "pct_hbm_peak": round(100 * fgbs / HBM_PEAK_GBS, 1),
+            "bytes": MLA_F32_BYTES, "heads": MLA_H, "tokens": MLA_T, "cache": "fp32 (the reference's default)",
+            "what": "k3_mla_decode_absorbed_f32: fp32 rows split into hi/lo bf16 planes as staged",
+            "launches": 4, "step_us": fstats}
     if "mlastep" in work:
         ms_ = min(K, 128)
         ssec, sstats = bench_mla_step(torch, ms_, min(W, 16), dev)

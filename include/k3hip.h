@@ -122,7 +122,9 @@ int k3_moe_layer_workspace_offsets(int64_t H, int64_t I, int64_t shared_I, int64
  * from the raw scores, divided by (sum + 1e-20) when renormalize and top_k > 1, times
  * scaling.  Ties go to the lower expert index; softmax selects on the logits (the
  * probabilities' order without fp32 rounding ties), and a NaN or infinite logit makes every
- * probability NaN and selects the k lowest indices.  Results land in the workspace records. */
+ * probability NaN and selects the k lowest indices.  Results land in the workspace records.
+ * Resets the router's arrival counter itself (one small launch before the router rows), so
+ * it routes correctly whatever the workspace's counter bytes hold. */
 int k3_moe_route(const void *x, int x_dtype, const void *router_w, const void *router_bias,
                  int route_kind, int renormalize, float scaling, int64_t H, int64_t n_experts,
                  int64_t top_k, void *workspace, int64_t workspace_bytes, void *stream);
@@ -184,6 +186,61 @@ int k3_moe_grouped_ffn(const void *x, int x_dtype, const int32_t *expert_idx, co
                        int64_t I, int64_t n_experts, int64_t top_k, int act_kind, float beta,
                        float linear_beta, void *workspace, int64_t workspace_bytes, void *stream);
 
+/* ---- routed experts for a few decode tokens, each selected expert read once ---------------- */
+
+/* Workspace bytes k3_moe_routed_decode needs for T tokens (the union records, arrival
+ * counters, fp32 act and down-row totals per (token, slot) pair).  No initialisation: every
+ * call rewrites it, counters included. */
+int64_t k3_moe_routed_workspace_size(int64_t T, int64_t H, int64_t I, int64_t n_experts, int64_t top_k);
+
+/* y[t] = sum_j w[t, j] * expert_{idx[t, j]}(x[t]) for T <= 8 decode tokens, with each expert
+ * any token selects read from HBM once for all the tokens routed to it:
+ *   x [T, H] bf16 or fp32 (x_dtype); expert_idx int32 [T, top_k]; expert_w f32 [T, top_k];
+ *   expert_table as in k3_moe_layer_decode; out [T, H] f32 or bf16.
+ * A token is gathered once per expert, with the weight of its first slot holding it; ids
+ * outside 0..n_experts-1 contribute nothing.  Three stream-ordered launches (the union of the
+ * routed experts on the device, the gate/up rows of every union expert against its tokens,
+ * its down rows with a fixed-order combine), no host synchronisation, fp32 accumulation,
+ * deterministic.  H and I multiples of 128, H <= 8192, I <= 4096, top_k <= 16,
+ * n_experts <= 1024.
+ * Replaces the per-expert dispatch loop of LatentMoE.__call__ (air_llm/models/kimi_k3/moe.py:
+ * 119-127, h[ti] gathered per expert; k3ref/layers.py:241-261) at decode batch sizes, whose
+ * kernel takes the M tokens of an expert in one launch (mxfp4_matvec.py:89-95). */
+int k3_moe_routed_decode(const void *x, int x_dtype, const int32_t *expert_idx, const float *expert_w,
+                         const void *expert_table, void *out, int out_dtype, int64_t T, int64_t H,
+                         int64_t I, int64_t n_experts, int64_t top_k, int act_kind, float beta,
+                         float linear_beta, void *workspace, int64_t workspace_bytes, void *stream);
+
+/* Workspace bytes for k3_moe_layer_decode_multi (the k3_moe_routed_decode records plus the
+ * router records and the shared expert's act and output for T tokens).  No initialisation. */
+int64_t k3_moe_layer_multi_workspace_size(int64_t T, int64_t H, int64_t I, int64_t shared_I,
+                                          int64_t n_experts, int64_t top_k);
+
+/* Byte offsets of k3_moe_layer_decode_multi's router records: [0] logits f32 [T, E], [1] scores
+ * f32 [T, E] (softmax probabilities or raw sigmoid scores), [2] corrected scores f32 [T, E],
+ * [3] top-k expert ids int32 [T, k], [4] top-k weights f32 [T, k] (the RouterResult of
+ * LatentMoE.route, air_llm/models/kimi_k3/moe.py:32-37, for the T tokens). */
+int k3_moe_layer_multi_workspace_offsets(int64_t T, int64_t H, int64_t I, int64_t shared_I,
+                                         int64_t n_experts, int64_t top_k, int64_t *offsets);
+
+/* k3_moe_layer_decode for T <= 8 decode tokens at once, x [T, H] and out [T, H]: the router
+ * rows and the shared gate/up rows against all T tokens in one launch (bf16 rows, exact
+ * products, fp32 accumulation), the batched top-k (as k3_moe_topk), the routed experts as in
+ * k3_moe_routed_decode (every expert any token selects read once for all the tokens routed to
+ * it), the shared down rows, and the fixed-order combine with the shared output: six
+ * stream-ordered launches, no host synchronisation.  Arguments as k3_moe_layer_decode, plus T;
+ * shared_I a multiple of 128, <= 8192.
+ * Replaces LatentMoE.__call__ (air_llm/models/kimi_k3/moe.py:110-132, without the latent
+ * wrapper) for a decode batch of T tokens, whose dispatch loop gathers every token routed to
+ * an expert (h[ti], moe.py:120-124) and whose kernel takes M tokens per launch
+ * (mxfp4_matvec.py:89-95). */
+int k3_moe_layer_decode_multi(const void *x, int x_dtype, const void *router_w, const void *router_bias,
+                              int route_kind, int renormalize, float scaling, const void *expert_table,
+                              const void *shared_gate, const void *shared_up, const void *shared_down,
+                              void *out, int out_dtype, int64_t T, int64_t H, int64_t I, int64_t shared_I,
+                              int64_t n_experts, int64_t top_k, int act_kind, float beta, float linear_beta,
+                              void *workspace, int64_t workspace_bytes, void *stream);
+
 /* Workspace bytes for k3_moe_latent_layer_decode: the k3_moe_layer_decode records plus the
  * bf16 latent state and the fp32 routed sum.  Same counter rule as k3_moe_layer_workspace_size
  * (first 4096 bytes zero before the first call; every call returns them to zero). */
@@ -236,6 +293,21 @@ int k3_mla_decode_absorbed(const void *q_nope, const void *q_rot, int64_t ld_q, 
                            int64_t kv_lora_rank, int64_t rope_dim, int64_t nope_dim, int64_t v_dim,
                            float scale, void *out, int out_dtype, int64_t ld_out, void *workspace,
                            int64_t workspace_bytes, void *stream);
+
+/* k3_mla_decode_absorbed over an fp32 latent cache (the reference's default cache dtype,
+ * MLACache with mx.float32, attention_mla.py:164; its view, :83-87): lat [T, r] and rot
+ * [T, rope] fp32 rows ld_lat / ld_rot elements apart (multiples of 4).  Every other argument,
+ * the workspace size included, as k3_mla_decode_absorbed.  The rows are read once, each split
+ * on the device into two bf16 planes (hi = rne(v), lo = rne(v - hi)) whose four products with
+ * the hi/lo query terms are all kept, so the fp32 cache enters to ~2^-16 relative.
+ * Replaces the absorbed core of MLAAttention.__call__ (attention_mla.py:193-212) for T == 1
+ * with the reference's fp32 cache. */
+int k3_mla_decode_absorbed_f32(const void *q_nope, const void *q_rot, int64_t ld_q, int64_t ld_q_rot,
+                               int q_dtype, const void *w_uk, const void *w_uv, const void *lat, int64_t ld_lat,
+                               const void *rot, int64_t ld_rot, int64_t T, int64_t H,
+                               int64_t kv_lora_rank, int64_t rope_dim, int64_t nope_dim, int64_t v_dim,
+                               float scale, void *out, int out_dtype, int64_t ld_out, void *workspace,
+                               int64_t workspace_bytes, void *stream);
 
 /* ---- one decode token through a whole MLA layer (batch 1) ------------------------------ */
 

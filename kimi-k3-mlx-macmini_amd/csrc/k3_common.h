@@ -21,13 +21,14 @@ int check_hip(hipError_t e, const char *what);
 
 inline bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
-// The absorbed MLA decode core behind k3_mla_decode_absorbed, with an optional output gate:
-// gate [H, v_dim] fp32 logits (null: none) multiply o by sigmoid(gate) as it is written.
+// The absorbed MLA decode core behind k3_mla_decode_absorbed(_f32), with an optional output
+// gate: gate [H, v_dim] fp32 logits (null: none) multiply o by sigmoid(gate) as it is
+// written.  cache_dtype: K3_BF16 or K3_F32 rows of lat and rot.
 int mla_decode_core(const void *q_nope, const void *q_rot, int64_t ld_q, int64_t ld_q_rot, int q_dtype,
                     const void *w_uk, const void *w_uv, const void *lat, int64_t ld_lat, const void *rot,
                     int64_t ld_rot, int64_t T, int64_t H, int64_t kv_lora_rank, int64_t rope_dim, int64_t nope_dim,
                     int64_t v_dim, float scale, void *out, int out_dtype, int64_t ld_out, const float *gate,
-                    void *workspace, int64_t workspace_bytes, void *stream);
+                    void *workspace, int64_t workspace_bytes, void *stream, int cache_dtype = K3_BF16);
 
 // ---------------------------------------------------------------- bf16 <-> f32
 __device__ __forceinline__ float bf16_to_f32(uint16_t b) {

@@ -220,9 +220,18 @@ constexpr float kSlack = 64.f;                      // log2 headroom before a re
 constexpr size_t kAttnLds = static_cast<size_t>(kSlots) * kRoundLds;  // 135168 B
 static_assert(static_cast<size_t>(kHG) * kR * 4 <= kAttnLds, "class merge staging fits");
 
-template <int D>
+// F32: the cache holds fp32 rows (the reference's default cache dtype).  A round is then one
+// 16-token tile staged as two bf16 planes, hi = rne(v) and lo = rne(v - hi), and the tile
+// classes become the planes: class 0 works on the hi plane, class 1 on the lo plane of the
+// same tokens.  The score waves' partials of both planes add into one score (so both classes
+// run the same softmax, with identical references and sums), and each class's context waves
+// take plane^T . [P_hi; P_lo]; the two contexts add at the end.  Every product of
+// (hi + lo) x (hi + lo) is kept, so the fp32 rows enter to ~2^-16 relative.
+template <int D, bool F32>
 __global__ __launch_bounds__(512, 1) void mla_attn_kernel(AttnArgs a) {
     static_assert(D >= 2, "rounds 0 and 1 are staged from two register slots");
+    constexpr int kRoundTok = F32 ? kStepT : kStepT * kRoundTiles;  // tokens per round
+    constexpr int RP = F32 ? 2 : 1;                                 // 16-byte rope loads per lane
     extern __shared__ uint4 smem[];
     __shared__ f32x4_t xs[2][kRoundTiles][2][64];   // partial scores [parity][class][half][lane]
     __shared__ uint4 xp[2][kRoundTiles][64];        // P hi/lo [parity][class][lane]
@@ -245,7 +254,9 @@ __global__ __launch_bounds__(512, 1) void mla_attn_kernel(AttnArgs a) {
     const int t_begin = split * a.Ts;
     const int t_end = min(a.T, t_begin + a.Ts);
     const int nsteps = (t_end - t_begin + kStepT - 1) / kStepT;   // tiles of the split
-    const int nrounds = (nsteps + kRoundTiles - 1) / kRoundTiles;
+    const int nrounds = F32 ? nsteps : (nsteps + kRoundTiles - 1) / kRoundTiles;
+    // the 16-token tile that class c works on in round rd
+    auto tile_of = [&](int rd, int c) { return F32 ? rd : rd * kRoundTiles + c; };
     const int nloop = (nrounds + 1 + D - 1) / D * D;              // one more for the context waves
     auto slot = [&](int rd) { return lds + (rd % kSlots) * kRoundLds; };
 
@@ -253,14 +264,18 @@ __global__ __launch_bounds__(512, 1) void mla_attn_kernel(AttnArgs a) {
     // q % 16); tiles and rows past the split load zeros (out-of-range offsets), so every
     // round issues the same loads
     const auto rl = make_rsrc(a.lat, a.lat_bytes);
+    // bf16: load q is row q % 16 of tile 2 rd + q / 16, whole (1 KB);  fp32: load q is half
+    // q % 2 (1 KB, 256 values) of row q / 2 of tile rd
     auto load_round = [&](uint4 (&g)[kPerWave], int rd) {
 #pragma unroll
         for (int i = 0; i < kPerWave; ++i) {
             const int q = wave + 8 * i;
-            const int tile = rd * kRoundTiles + q / kStepT;
-            const int t = t_begin + tile * kStepT + q % kStepT;
+            const int tile = F32 ? rd : rd * kRoundTiles + q / kStepT;
+            const int row = F32 ? q / 2 : q % kStepT;
+            const int t = t_begin + tile * kStepT + row;
             const bool ok = q < kChunks && tile < nsteps && t < t_end;
-            g[i] = buf_load16(rl, ok ? static_cast<uint32_t>(t) * a.lat_row_bytes + lane * 16u : kOobOffset);
+            const uint32_t col = F32 ? (q % 2) * 1024u + lane * 16u : lane * 16u;
+            g[i] = buf_load16(rl, ok ? static_cast<uint32_t>(t) * a.lat_row_bytes + col : kOobOffset);
         }
     };
     auto store_round = [&](const uint4 (&g)[kPerWave], int rd) {
@@ -268,8 +283,22 @@ __global__ __launch_bounds__(512, 1) void mla_attn_kernel(AttnArgs a) {
 #pragma unroll
         for (int i = 0; i < kPerWave; ++i) {
             const int q = wave + 8 * i;
-            if (q < kChunks)
-                *reinterpret_cast<uint4 *>(base + (q / kStepT) * kTileLds + (q % kStepT) * kLatStride + lane * 16) = g[i];
+            if (q < kChunks) {
+                if constexpr (F32) {
+                    // four fp32 values -> their hi bf16 (plane 0) and lo bf16 (plane 1)
+                    const float v0 = __uint_as_float(g[i].x), v1 = __uint_as_float(g[i].y);
+                    const float v2 = __uint_as_float(g[i].z), v3 = __uint_as_float(g[i].w);
+                    const uint32_t h01 = pack_bf16x2(v0, v1), h23 = pack_bf16x2(v2, v3);
+                    const uint32_t l01 = pack_bf16x2(v0 - __uint_as_float(h01 << 16), v1 - __uint_as_float(h01 & 0xffff0000u));
+                    const uint32_t l23 = pack_bf16x2(v2 - __uint_as_float(h23 << 16), v3 - __uint_as_float(h23 & 0xffff0000u));
+                    char *row = base + (q / 2) * kLatStride + ((q % 2) * 256 + lane * 4) * 2;
+                    *reinterpret_cast<uint2 *>(row) = make_uint2(h01, h23);
+                    *reinterpret_cast<uint2 *>(row + kTileLds) = make_uint2(l01, l23);
+                } else {
+                    *reinterpret_cast<uint4 *>(base + (q / kStepT) * kTileLds + (q % kStepT) * kLatStride + lane * 16) =
+                        g[i];
+                }
+            }
         }
     };
     uint4 stg[D][kPerWave];
@@ -280,14 +309,18 @@ __global__ __launch_bounds__(512, 1) void mla_attn_kernel(AttnArgs a) {
     // their latencies overlap (context waves issue none of them)
     bf16x8 qhi[kHalfKb + 1], qlo[kHalfKb + 1];
     const auto rr = make_rsrc(a.rot, a.rot_bytes);
-    auto load_rope = [&](int rd) -> uint4 {
-        const int tile = rd * kRoundTiles + cls;
+    // the 8 rope values (columns 32 half + 8 q4 ..) of token r16 of the class's tile: one
+    // 16-byte load of bf16 rows, two of fp32 rows (split into the class's plane at use)
+    typedef uint4 RopeRaw[RP];
+    auto load_rope = [&](RopeRaw &o, int rd) {
+        const int tile = tile_of(rd, cls);
         const int t = t_begin + tile * kStepT + r16;
         const bool ok = tile < nsteps && t < t_end;
-        return buf_load16(rr, ok ? static_cast<uint32_t>(t) * a.rot_row_bytes + (half * 32 + q4 * 8) * 2u
-                                 : kOobOffset);
+        const uint32_t off = static_cast<uint32_t>(t) * a.rot_row_bytes + (half * 32 + q4 * 8) * (F32 ? 4u : 2u);
+#pragma unroll
+        for (int j = 0; j < RP; ++j) o[j] = buf_load16(rr, ok ? off + 16u * j : kOobOffset);
     };
-    uint4 rope[D], rope0;
+    RopeRaw rope[D], rope0;
     if (!ctx_role) {
         const uint32_t qbytes = static_cast<uint32_t>(a.H) * kQaLd * 2;
         const auto rqh = make_rsrc(a.qa_hi, qbytes), rql = make_rsrc(a.qa_lo, qbytes);
@@ -299,8 +332,8 @@ __global__ __launch_bounds__(512, 1) void mla_attn_kernel(AttnArgs a) {
             qlo[k] = __builtin_bit_cast(bf16x8, buf_load16(rql, qrow + static_cast<uint32_t>(col) * 2u));
         }
 #pragma unroll
-        for (int d = 1; d <= D; ++d) rope[d % D] = load_rope(d);
-        rope0 = load_rope(0);
+        for (int d = 1; d <= D; ++d) load_rope(rope[d % D], d);
+        load_rope(rope0, 0);
     }
     store_round(stg[0], 0);
     store_round(stg[1], 1);
@@ -314,7 +347,7 @@ __global__ __launch_bounds__(512, 1) void mla_attn_kernel(AttnArgs a) {
         // ================= score waves
         float m_ref = -INFINITY, l_run = 0.f;  // head h0 + r16, class cls (both halves alike)
         // partial scores of round rd over this half's columns
-        auto partial = [&](int rd, const uint4 &rp) -> f32x4_t {
+        auto partial = [&](int rd, const RopeRaw &rp) -> f32x4_t {
             const char *arow = slot(rd) + cls * kTileLds + r16 * kLatStride + half * 512 + q4 * 16;
             auto rdk = [&](int k) { return __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4 *>(arow + k * 64)); };
             f32x4_t s0 = {0.f, 0.f, 0.f, 0.f}, s1 = s0, s2 = s0, s3 = s0;
@@ -333,15 +366,33 @@ __global__ __launch_bounds__(512, 1) void mla_attn_kernel(AttnArgs a) {
                 s3 = mfma_bf16(c[k + 1], qlo[k + 1], s3);
                 __builtin_amdgcn_sched_barrier(0);
             }
-            const bf16x8 rk = __builtin_bit_cast(bf16x8, rp);
+            bf16x8 rk;
+            if constexpr (F32) {
+                // the class's plane of the 8 fp32 rope values: hi for class 0, lo for class 1
+                const uint32_t v[8] = {rp[0].x, rp[0].y, rp[0].z, rp[0].w, rp[1].x, rp[1].y, rp[1].z, rp[1].w};
+                uint32_t pk[4];
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const float f0 = __uint_as_float(v[2 * j]), f1 = __uint_as_float(v[2 * j + 1]);
+                    const uint32_t hi = pack_bf16x2(f0, f1);
+                    pk[j] = cls == 0 ? hi
+                                     : pack_bf16x2(f0 - __uint_as_float(hi << 16), f1 - __uint_as_float(hi & 0xffff0000u));
+                }
+                rk = __builtin_bit_cast(bf16x8, make_uint4(pk[0], pk[1], pk[2], pk[3]));
+            } else {
+                rk = __builtin_bit_cast(bf16x8, rp[0]);
+            }
             s0 = mfma_bf16(rk, qhi[kHalfKb], s0);
             s1 = mfma_bf16(rk, qlo[kHalfKb], s1);
             return (s0 + s2) + (s1 + s3);
         };
         // softmax of round rd from the two halves' partials; half 0 publishes P and factors
         auto softmax = [&](int rd) {
-            const f32x4_t sc = xs[rd & 1][cls][0][lane] + xs[rd & 1][cls][1][lane];
-            const int tbeg = t_begin + (rd * kRoundTiles + cls) * kStepT + q4 * 4;
+            // fp32 rows: the hi and lo planes' partials, in one order for both classes
+            const f32x4_t sc = F32 ? (xs[rd & 1][0][0][lane] + xs[rd & 1][0][1][lane]) +
+                                         (xs[rd & 1][1][0][lane] + xs[rd & 1][1][1][lane])
+                                   : xs[rd & 1][cls][0][lane] + xs[rd & 1][cls][1][lane];
+            const int tbeg = t_begin + tile_of(rd, cls) * kStepT + q4 * 4;
             float sv[4];
             float mt = -INFINITY;
 #pragma unroll
@@ -390,7 +441,7 @@ __global__ __launch_bounds__(512, 1) void mla_attn_kernel(AttnArgs a) {
                 const f32x4_t pnext = partial(rd + 1, rope[rs]);
                 softmax(rd);
                 xs[(rd + 1) & 1][cls][half][lane] = pnext;
-                rope[rs] = load_rope(rd + 1 + D);
+                load_rope(rope[rs], rd + 1 + D);
                 __syncthreads();
             }
         }
@@ -403,7 +454,8 @@ __global__ __launch_bounds__(512, 1) void mla_attn_kernel(AttnArgs a) {
             const float M = fmaxf(v.x, o.x);
             const float f0 = v.x == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(v.x - M);
             const float f1 = o.x == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(o.x - M);
-            a.ml[static_cast<int64_t>(split) * a.H + h0 + r16] = make_float2(M, v.y * f0 + o.y * f1);
+            // fp32 rows: both classes summed the same tokens' probabilities (identically)
+            a.ml[static_cast<int64_t>(split) * a.H + h0 + r16] = make_float2(M, F32 ? v.y : v.y * f0 + o.y * f1);
         }
         __syncthreads();  // class 1's context staged
     } else {
@@ -698,19 +750,34 @@ extern "C" int k3_mla_decode_absorbed(const void *q_nope, const void *q_rot, int
                                       void *stream) {
     return k3::mla_decode_core(q_nope, q_rot, ld_q, ld_q_rot, q_dtype, w_uk, w_uv, lat, ld_lat, rot, ld_rot, T, H,
                                kv_lora_rank, rope_dim, nope_dim, v_dim, scale, out, out_dtype, ld_out, nullptr,
-                               workspace, workspace_bytes, stream);
+                               workspace, workspace_bytes, stream, K3_BF16);
+}
+
+extern "C" int k3_mla_decode_absorbed_f32(const void *q_nope, const void *q_rot, int64_t ld_q, int64_t ld_q_rot,
+                                          int q_dtype, const void *w_uk, const void *w_uv, const void *lat,
+                                          int64_t ld_lat, const void *rot, int64_t ld_rot, int64_t T, int64_t H,
+                                          int64_t kv_lora_rank, int64_t rope_dim, int64_t nope_dim, int64_t v_dim,
+                                          float scale, void *out, int out_dtype, int64_t ld_out, void *workspace,
+                                          int64_t workspace_bytes, void *stream) {
+    return k3::mla_decode_core(q_nope, q_rot, ld_q, ld_q_rot, q_dtype, w_uk, w_uv, lat, ld_lat, rot, ld_rot, T, H,
+                               kv_lora_rank, rope_dim, nope_dim, v_dim, scale, out, out_dtype, ld_out, nullptr,
+                               workspace, workspace_bytes, stream, K3_F32);
 }
 
 int k3::mla_decode_core(const void *q_nope, const void *q_rot, int64_t ld_q, int64_t ld_q_rot, int q_dtype,
                         const void *w_uk, const void *w_uv, const void *lat, int64_t ld_lat, const void *rot,
                         int64_t ld_rot, int64_t T, int64_t H, int64_t kv_lora_rank, int64_t rope_dim,
                         int64_t nope_dim, int64_t v_dim, float scale, void *out, int out_dtype, int64_t ld_out,
-                        const float *gate, void *workspace, int64_t workspace_bytes, void *stream) {
+                        const float *gate, void *workspace, int64_t workspace_bytes, void *stream, int cache_dtype) {
     if (!q_nope || !q_rot || !w_uk || !w_uv || !lat || !rot || !out || !workspace)
         return set_error(K3_ERR_NULL, "mla decode: null pointer");
     if (q_dtype != K3_F32 && q_dtype != K3_BF16) return set_error(K3_ERR_DTYPE, "mla decode: q_dtype %d", q_dtype);
     if (out_dtype != K3_F32 && out_dtype != K3_BF16)
         return set_error(K3_ERR_DTYPE, "mla decode: out_dtype %d", out_dtype);
+    if (cache_dtype != K3_F32 && cache_dtype != K3_BF16)
+        return set_error(K3_ERR_DTYPE, "mla decode: cache dtype %d", cache_dtype);
+    const bool f32c = cache_dtype == K3_F32;
+    const int64_t esz = f32c ? 4 : 2, align_el = 16 / esz;  // cache element bytes; elements per 16 bytes
     if (kv_lora_rank != kR || rope_dim != kRope)
         return set_error(K3_ERR_SHAPE, "mla decode: kv_lora_rank=%lld rope=%lld; the kernels take 512 and 64",
                          (long long)kv_lora_rank, (long long)rope_dim);
@@ -719,12 +786,12 @@ int k3::mla_decode_core(const void *q_nope, const void *q_rot, int64_t ld_q, int
         return set_error(K3_ERR_SHAPE, "mla decode: nope=%lld must be in 1..256 and v=%lld in 1..1024",
                          (long long)nope_dim, (long long)v_dim);
     if (T <= 0) return set_error(K3_ERR_SHAPE, "mla decode: empty cache (T=%lld)", (long long)T);
-    if (ld_q < nope_dim || ld_q_rot < rope_dim || ld_lat < kR || ld_rot < kRope || ld_out < v_dim || ld_lat % 8 ||
-        ld_rot % 8)
-        return set_error(K3_ERR_SHAPE, "mla decode: row strides too small, or cache strides not multiples of 8");
+    if (ld_q < nope_dim || ld_q_rot < rope_dim || ld_lat < kR || ld_rot < kRope || ld_out < v_dim ||
+        ld_lat % align_el || ld_rot % align_el)
+        return set_error(K3_ERR_SHAPE, "mla decode: row strides too small, or cache rows not 16-byte multiples");
     if (!aligned16(lat) || !aligned16(rot) || !aligned16(w_uk) || !aligned16(w_uv) || !aligned16(workspace))
         return set_error(K3_ERR_ALIGN, "mla decode: cache, weights and workspace must be 16-byte aligned");
-    const int64_t lat_bytes = ((T - 1) * ld_lat + kR) * 2, rot_bytes = ((T - 1) * ld_rot + kRope) * 2;
+    const int64_t lat_bytes = ((T - 1) * ld_lat + kR) * esz, rot_bytes = ((T - 1) * ld_rot + kRope) * esz;
     if (lat_bytes >= (1ll << 31) || rot_bytes >= (1ll << 31))
         return set_error(K3_ERR_SHAPE, "mla decode: cache views above 2 GiB are not supported");
     const MlaWs L = mla_ws_layout(H, T);
@@ -757,8 +824,8 @@ int k3::mla_decode_core(const void *q_nope, const void *q_rot, int64_t ld_q, int
     aa.rot = rot;
     aa.lat_bytes = static_cast<uint32_t>(lat_bytes);
     aa.rot_bytes = static_cast<uint32_t>(rot_bytes);
-    aa.lat_row_bytes = static_cast<uint32_t>(ld_lat * 2);
-    aa.rot_row_bytes = static_cast<uint32_t>(ld_rot * 2);
+    aa.lat_row_bytes = static_cast<uint32_t>(ld_lat * esz);
+    aa.rot_row_bytes = static_cast<uint32_t>(ld_rot * esz);
     aa.part = part;
     aa.ml = ml;
     aa.H = static_cast<int>(H);
@@ -768,14 +835,22 @@ int k3::mla_decode_core(const void *q_nope, const void *q_rot, int64_t ld_q, int
     aa.scale_log2 = scale * 1.4426950408889634f;
     const int blocks = NS * static_cast<int>(cdiv(H, kHG));
     aa.swizzle = blocks % 8 == 0;
-    constexpr auto attn = &mla_attn_kernel<kD>;
+    constexpr auto attn_bf16 = &mla_attn_kernel<kD, false>;
+    constexpr auto attn_f32 = &mla_attn_kernel<kD, true>;
     constexpr size_t lds = kAttnLds;
-    static const hipError_t lds_rc = hipFuncSetAttribute(reinterpret_cast<const void *>(attn),
-                                                         hipFuncAttributeMaxDynamicSharedMemorySize,
-                                                         static_cast<int>(lds));  // may exceed the 64 KB default
-    rc = check_hip(lds_rc, "mla decode: attention LDS size");
+    // may exceed the 64 KB default; set once per process for each form
+    static const hipError_t lds_rc =
+        hipFuncSetAttribute(reinterpret_cast<const void *>(attn_bf16), hipFuncAttributeMaxDynamicSharedMemorySize,
+                            static_cast<int>(lds));
+    static const hipError_t lds_rc32 =
+        hipFuncSetAttribute(reinterpret_cast<const void *>(attn_f32), hipFuncAttributeMaxDynamicSharedMemorySize,
+                            static_cast<int>(lds));
+    rc = check_hip(f32c ? lds_rc32 : lds_rc, "mla decode: attention LDS size");
     if (rc) return rc;
-    attn<<<dim3(static_cast<unsigned>(blocks)), 512, lds, st>>>(aa);
+    if (f32c)
+        attn_f32<<<dim3(static_cast<unsigned>(blocks)), 512, lds, st>>>(aa);
+    else
+        attn_bf16<<<dim3(static_cast<unsigned>(blocks)), 512, lds, st>>>(aa);
     rc = check_hip(hipGetLastError(), "mla decode: attention launch");
     if (rc) return rc;
 

@@ -152,14 +152,6 @@ __device__ __forceinline__ void x_store(uint4 *xl, const uint4 (&xr)[XREG]) {
 template <typename XT>
 constexpr int x_regs() { return sizeof(XT) == 2 ? 4 : 8; }  // H <= 8192
 
-// A 64-bit pointer held in memory, made wave-uniform (SGPRs) so buffer resources built
-// from it need no waterfall loop.
-__device__ __forceinline__ const void *uniform_ptr(uint64_t p) {
-    const uint32_t lo = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(p));
-    const uint32_t hi = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(p >> 32));
-    return reinterpret_cast<const void *>((static_cast<uint64_t>(hi) << 32) | lo);
-}
-
 // ------------------------------------------------------------------ routing (one block)
 // softmax:       scores = softmax(logits), selection on scores
 // sigmoid_bias:  scores = sigmoid(logits), selection on scores + bias, weights from scores
@@ -899,6 +891,11 @@ __global__ __launch_bounds__(256, 4) void layer_l3(LayerArgs a) {
 }
 
 
+// The router arrival counter back to zero (the route-only call, which has no L2 to do it).
+__global__ void counter_zero_kernel(uint32_t *counter) {
+    if (threadIdx.x == 0) counter[0] = 0u;
+}
+
 // ------------------------------------------------------------------ host side
 struct LayerWsLayout {
     size_t logits, scores, corrected, idx, w, shared_act, act, yshared, ptrs, counter, h, ylat, yrow, total;
@@ -1120,8 +1117,14 @@ static int layer_impl(const void *x, int x_dtype, const void *router_w, const vo
     a.lbeta = linear_beta;
     a.out_bf16 = out_dtype == K3_BF16;
     auto st = static_cast<hipStream_t>(stream);
-    if (route_only_flag)
+    if (route_only_flag) {
+        // Only L1 runs, and no later launch of this call zeroes the router counter: zero it
+        // first, so a workspace whose counter bytes hold garbage still routes on this call.
+        counter_zero_kernel<<<1, 64, 0, st>>>(a.ws.counter);
+        const int rc = check_hip(hipGetLastError(), "moe route: counter reset");
+        if (rc) return rc;
         return x_dtype == K3_BF16 ? launch_l1<uint16_t>(a, false, st) : launch_l1<float>(a, false, st);
+    }
     return x_dtype == K3_BF16 ? launch_layer<uint16_t>(a, st) : launch_layer<float>(a, st);
 }
 

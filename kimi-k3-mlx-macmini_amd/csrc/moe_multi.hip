@@ -1,0 +1,752 @@
+// Routed experts for a few decode tokens (up to 8) in one pass: every expert any of the
+// tokens selects is read from HBM once, against all the tokens routed to it.
+//
+// Reference: the dispatch loop of LatentMoE.__call__ (air_llm/models/kimi_k3/moe.py:119-127;
+// k3ref/layers.py:241-261): for each distinct routed expert e, in ascending id, gather the
+// tokens whose top-k holds e (h[ti]), run expert_forward on them together (the Metal kernel
+// takes M tokens per launch, grid (N, M, 1), mxfp4_matvec.py:89-95), scale each token's
+// output by its gate weight for e and add it into y.  A token is gathered once per expert,
+// with the weight of its first slot holding e (list.index, moe.py:121-122).  Here, three
+// stream-ordered launches and no host synchronisation:
+//
+//   U   one block: the union of the routed experts (distinct valid ids, ascending), each
+//       union slot's (token, slot) pairs -- one per token, the token's first slot holding
+//       the expert -- in token order, the slots' six weight pointers, a live flag per pair;
+//       it zeroes D's arrival counters.
+//   G   block (union slot u, 8 intermediate rows): each wave holds two (gate row, up row)
+//       pairs of u's expert in registers and reduces them against every token of u, whose
+//       rows are staged in LDS (up to tb_x tokens at a time, in the swizzled group order of
+//       the batch-1 kernels) -> act[pair][i] = f(gate, up) in fp32.
+//   D   block (union slot u, 4 * RW output rows): the rows of u's down projection in
+//       registers, reduced against the act vector of each of u's pairs (staged in LDS, up to
+//       tb_act at a time, chunk-major as the layer's down launch stages one); the row totals
+//       per pair go to the workspace, and the last of a row range's blocks to finish combines
+//       y[t] = yadd[t] + sum over the token's live slots j, in slot order, of w[t, j] * down_{t, j}
+//       (yadd: the shared expert's output of the whole-layer entry point, or nothing).
+//
+// The whole layer for T tokens (k3_moe_layer_decode_multi) adds the dense bf16 parts on R, a
+// row kernel for T tokens (4 waves, one row or one (gate, up) row pair per wave, the T input
+// rows staged in LDS once per block): the router logits with the shared gate/up rows in one
+// launch, the batched top-k (k3_moe_topk), U, G, the shared down rows, and D.
+//
+// Every selected expert's gate, up and down bytes are read once per call, whatever the
+// number of tokens routed to it.  Deterministic: no float atomics, fixed orders.
+#include <algorithm>
+#include <type_traits>
+
+#include "moe_common.h"
+#include "mxfp4_dot.h"
+
+namespace k3 {
+namespace {
+
+constexpr int kMaxTokens = 8;
+constexpr int kMaxTopK = 16;
+constexpr int kMaxPairs = kMaxTokens * kMaxTopK;  // 128
+constexpr int kMaxExperts = 1024;
+constexpr size_t kCounterBytes = 4096;            // D's row-range arrival counters
+constexpr int kPairsPerWave = 2;                  // G: (gate, up) row pairs per wave
+constexpr int kGRows = 4 * kPairsPerWave;         // G: intermediate rows per block
+// LDS bytes per block for the staged token batches: small, so that LDS does not cap the
+// blocks per CU below what the registers allow (the launches are bandwidth-bound)
+constexpr int kLdsBudgetG = 16384;
+constexpr int kLdsBudgetD = 40960;
+
+struct MultiArgs {
+    const void *x;           // [T, Hr] rows, bf16 or fp32
+    const int32_t *idx;      // [T, k]
+    const float *wts;        // [T, k]
+    const uint64_t *table;   // [E][6] gate p/s, up p/s, down p/s
+    void *out;               // [T, Hr]
+    int T, Hr, I, E, k, P;
+    int act_kind;
+    float beta, lbeta;
+    int out_bf16;
+    int tb_x, tb_act;        // tokens per staged batch in G and D
+    int n_ranges;            // D row ranges (one arrival counter each)
+    // workspace records
+    uint32_t *counter;       // [n_ranges]
+    int32_t *nu;             // [1] union size
+    int32_t *u_count;        // [P] pairs of union slot u
+    int32_t *u_pairs;        // [P][T] pair ids t * k + j of slot u, tokens ascending
+    int32_t *live;           // [P] 1: pair contributes (valid id, the token's first slot holding it)
+    uint64_t *u_ptrs;        // [P][6] weight pointers of slot u's expert
+    float *act;              // [P][I] act of each live pair
+    float *yrow;             // [P][Hr] down totals of each live pair
+    const float *yadd;       // [T][Hr] added to each combined row (the shared expert) or null
+};
+
+// ------------------------------------------------------------------ U: the union
+__global__ __launch_bounds__(256) void multi_union_kernel(MultiArgs a) {
+    __shared__ int id_s[kMaxPairs];
+    __shared__ int ex_s[kMaxPairs];
+    __shared__ int first_s[kMaxPairs];
+    __shared__ int nu_s;
+    const int p = threadIdx.x;
+    if (p == 0) nu_s = 0;
+    const int v = p < a.P ? a.idx[p] : -1;  // every id loaded once, side by side
+    if (p < kMaxPairs) id_s[p] = v;
+    __syncthreads();
+    int e = -1;
+    if (p < a.P) {
+        e = (v >= 0 && v < a.E) ? v : -1;
+        const int t = p / a.k, j = p % a.k;
+        for (int jj = 0; jj < j; ++jj)
+            if (id_s[t * a.k + jj] == v) e = -1;  // an earlier slot of the token holds it
+    }
+    if (p < kMaxPairs) ex_s[p] = e;
+    __syncthreads();
+    bool fst = false;
+    int pos = 0, cnt = 0;
+    if (e >= 0) {
+        fst = true;
+        for (int q = 0; q < a.P; ++q) {
+            if (ex_s[q] == e) {
+                if (q < p) fst = false, ++pos;
+                ++cnt;
+            }
+        }
+    }
+    if (p < kMaxPairs) first_s[p] = fst;
+    __syncthreads();
+    if (e >= 0) {
+        int slot = 0;  // distinct experts below e
+        for (int q = 0; q < a.P; ++q) slot += first_s[q] && ex_s[q] < e;
+        a.u_pairs[slot * a.T + pos] = p;
+        if (fst) {
+            a.u_count[slot] = cnt;
+#pragma unroll
+            for (int c = 0; c < 6; ++c) a.u_ptrs[slot * 6 + c] = a.table[static_cast<int64_t>(e) * 6 + c];
+            atomicAdd(&nu_s, 1);
+        }
+    }
+    if (p < a.P) a.live[p] = e >= 0;
+    for (int c = p; c < a.n_ranges; c += 256) a.counter[c] = 0u;
+    __syncthreads();
+    if (p == 0) *a.nu = nu_s;
+}
+
+// ------------------------------------------------------------------ G: gate/up + act
+// GA: MXFP4 groups per lane over Hr (Hr <= 2048 * GA).
+template <typename XT, int GA>
+__global__ __launch_bounds__(256) void multi_gateup_kernel(MultiArgs a) {
+    extern __shared__ uint4 smem[];  // [tb_x][Hr / 8 (bf16) or Hr / 4 (fp32) chunks], swizzled
+    constexpr int CPGX = XTile<XT>::kChunks;
+    const int nrb = a.I / kGRows;
+    const int u = blockIdx.x / nrb, rb = blockIdx.x % nrb;
+    if (u >= *a.nu) return;  // uniform over the block
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+    const int GH = a.Hr >> 5, nch = GH * CPGX;
+    const uint32_t rowA = static_cast<uint32_t>(a.Hr >> 1);
+    const int cnt = a.u_count[u];
+    const uint64_t *t = a.u_ptrs + u * 6;
+    const auto rg = make_rsrc(uniform_ptr(t[0]), static_cast<uint32_t>(a.I) * rowA);
+    const auto rgs = make_rsrc(uniform_ptr(t[1]), static_cast<uint32_t>(a.I * GH));
+    const auto ru = make_rsrc(uniform_ptr(t[2]), static_cast<uint32_t>(a.I) * rowA);
+    const auto rus = make_rsrc(uniform_ptr(t[3]), static_cast<uint32_t>(a.I * GH));
+    // the wave's weight rows, issued before anything is staged
+    uint4 wg[kPairsPerWave][GA], wu[kPairsPerWave][GA];
+    uint32_t sg[kPairsPerWave][GA], su[kPairsPerWave][GA];
+#pragma unroll
+    for (int q = 0; q < kPairsPerWave; ++q) {
+        const int i = rb * kGRows + wave * kPairsPerWave + q;
+#pragma unroll
+        for (int v = 0; v < GA; ++v) {
+            const int g = v * 64 + lane;
+            const bool ok = g < GH;
+            const uint32_t off = ok ? static_cast<uint32_t>(i) * rowA + g * 16u : kOobOffset;
+            const uint32_t soff = ok ? static_cast<uint32_t>(i * GH + g) : kOobOffset;
+            wg[q][v] = buf_load16(rg, off);
+            wu[q][v] = buf_load16(ru, off);
+            sg[q][v] = __builtin_amdgcn_raw_buffer_load_b8(rgs, soff, 0, 0);
+            su[q][v] = __builtin_amdgcn_raw_buffer_load_b8(rus, soff, 0, 0);
+        }
+    }
+    const char *xb = static_cast<const char *>(a.x);
+#pragma unroll 1
+    for (int c0 = 0; c0 < cnt; c0 += a.tb_x) {
+        const int nb = min(a.tb_x, cnt - c0);
+        if (c0 > 0) __syncthreads();  // every wave is done with the previous batch
+        for (int c = 0; c < nb; ++c) {
+            const int tok = a.u_pairs[u * a.T + c0 + c] / a.k;
+            stage_x_tile<XT>(smem + c * nch, xb + static_cast<int64_t>(tok) * a.Hr * sizeof(XT), nch);
+        }
+        __syncthreads();
+#pragma unroll 1
+        for (int c = 0; c < nb; ++c) {
+            const uint4 *xs = smem + c * nch;
+            float accg[kPairsPerWave], accu[kPairsPerWave];
+#pragma unroll
+            for (int q = 0; q < kPairsPerWave; ++q) accg[q] = accu[q] = 0.f;
+#pragma unroll
+            for (int v = 0; v < GA; ++v) {
+                const int g = v * 64 + lane;
+                if (g < GH) {
+                    XChunk<XT> xc[CPGX];
+#pragma unroll
+                    for (int q = 0; q < CPGX; ++q) xc[q] = reinterpret_cast<const XChunk<XT> *>(xs)[XTile<XT>::slot(g, q)];
+#pragma unroll
+                    for (int q = 0; q < kPairsPerWave; ++q) {
+                        accg[q] = fmaf(group_dot(wg[q][v], xc), e8m0_to_f32(sg[q][v]), accg[q]);
+                        accu[q] = fmaf(group_dot(wu[q][v], xc), e8m0_to_f32(su[q][v]), accu[q]);
+                    }
+                }
+            }
+            const int pair = a.u_pairs[u * a.T + c0 + c];
+#pragma unroll
+            for (int q = 0; q < kPairsPerWave; ++q) {
+                const float gs = wave_sum_to_lane63(accg[q]);
+                const float us = wave_sum_to_lane63(accu[q]);
+                const int i = rb * kGRows + wave * kPairsPerWave + q;
+                if (lane == 63) a.act[static_cast<int64_t>(pair) * a.I + i] = act_fn(gs, us, a.act_kind, a.beta, a.lbeta);
+            }
+        }
+    }
+}
+
+// ------------------------------------------------------------------ D: down + combine
+// A down row is cut into pieces of S elements (S = 32: one group, 16 bytes; S = 16: half a
+// group); lane l takes pieces l, l + 64, ... (NP of them) of its wave's RW rows.  A pair's
+// act vector is staged chunk-major ([chunk q][piece], plus one zero sink slot), so the lanes
+// of a wave read consecutive 16-byte slots.
+template <int S, int NP, int RW>
+__global__ __launch_bounds__(256, 2) void multi_down_kernel(MultiArgs a) {
+    static_assert(S == 16 || S == 32, "a piece is half a group or one group");
+    constexpr int ND = S / 8;        // packed dwords per piece
+    constexpr int NC = S / 4;        // float4 act chunks per piece
+    constexpr int RB = 4 * RW;       // rows per block
+    constexpr int NA = S * NP / 16;  // act float4 per thread and pair (I <= S * NP * 64)
+    constexpr int AV = NA * 256 + 1; // staged float4 per pair (the last one is the sink)
+    extern __shared__ float4 act_s[];  // [tb_act][AV]
+    __shared__ uint32_t last_s;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+    const int nR = (a.Hr + RB - 1) / RB;
+    const int u = blockIdx.x / nR, rr = blockIdx.x % nR;
+    const int nu = *a.nu;
+    // with no live pair at all, the blocks of slot 0 still count in and write zeros
+    if (u >= max(nu, 1)) return;
+    const int cnt = u < nu ? a.u_count[u] : 0;
+    const int GI = a.I >> 5, P = a.I / S;
+    const uint32_t rowB = static_cast<uint32_t>(a.I >> 1);
+    const int n0 = rr * RB + wave * RW;
+    uint32_t wd[RW][NP][ND];
+    uint32_t sd[RW][NP];
+    if (cnt > 0) {
+        const uint64_t *t = a.u_ptrs + u * 6;
+        const auto rd = make_rsrc(uniform_ptr(t[4]), static_cast<uint32_t>(a.Hr) * rowB);
+        const auto rds = make_rsrc(uniform_ptr(t[5]), static_cast<uint32_t>(a.Hr * GI));
+#pragma unroll
+        for (int r = 0; r < RW; ++r)
+#pragma unroll
+            for (int p = 0; p < NP; ++p) {
+                const int n = n0 + r, pc = p * 64 + lane;
+                const bool ok = n < a.Hr && pc < P;
+                const uint32_t off = ok ? static_cast<uint32_t>(n) * rowB + pc * (S / 2u) : kOobOffset;
+                if constexpr (S == 32) {
+                    const uint4 v = buf_load16(rd, off);
+                    wd[r][p][0] = v.x, wd[r][p][1] = v.y, wd[r][p][2] = v.z, wd[r][p][3] = v.w;
+                } else {
+                    const auto v = __builtin_amdgcn_raw_buffer_load_b64(rd, off, 0, 0);
+                    wd[r][p][0] = v[0], wd[r][p][1] = v[1];
+                }
+                sd[r][p] = __builtin_amdgcn_raw_buffer_load_b8(
+                    rds, ok ? static_cast<uint32_t>(n * GI + pc * S / 32) : kOobOffset, 0, 0);
+            }
+    }
+#pragma unroll 1
+    for (int c0 = 0; c0 < cnt; c0 += a.tb_act) {
+        const int nb = min(a.tb_act, cnt - c0);
+        if (c0 > 0) __syncthreads();  // every wave is done with the previous batch
+        for (int c = 0; c < nb; ++c) {
+            const int pair = a.u_pairs[u * a.T + c0 + c];
+            const auto ra = make_rsrc(a.act + static_cast<int64_t>(pair) * a.I, static_cast<uint32_t>(a.I) * 4u);
+            float4 *dst = act_s + c * AV;
+#pragma unroll
+            for (int i = 0; i < NA; ++i) {
+                const int ch = i * 256 + static_cast<int>(threadIdx.x);
+                const float4 v = __builtin_bit_cast(float4, buf_load16(ra, ch < a.I / 4 ? ch * 16u : kOobOffset));
+                dst[ch < a.I / 4 ? (ch % NC) * P + ch / NC : NA * 256] = v;
+            }
+        }
+        __syncthreads();
+#pragma unroll 1
+        for (int c = 0; c < nb; ++c) {
+            const float4 *src = act_s + c * AV;
+            float4 av[NP][NC];
+#pragma unroll
+            for (int p = 0; p < NP; ++p) {
+                const int pc = p * 64 + lane;
+#pragma unroll
+                for (int q = 0; q < NC; ++q) av[p][q] = src[pc < P ? q * P + pc : NA * 256];
+            }
+            const int pair = a.u_pairs[u * a.T + c0 + c];
+            // The packed weights stay packed across the token loop: without this, the
+            // compiler hoists their fp4 -> fp32 conversion out of the loop (8 floats per
+            // dword) and spills.  An empty asm that claims to modify them keeps it inside.
+#pragma unroll
+            for (int r = 0; r < RW; ++r)
+#pragma unroll
+                for (int p = 0; p < NP; ++p)
+#pragma unroll
+                    for (int d = 0; d < ND; ++d) asm volatile("" : "+v"(wd[r][p][d]));
+#pragma unroll
+            for (int r = 0; r < RW; ++r) {
+                float acc = 0.f;
+#pragma unroll
+                for (int p = 0; p < NP; ++p) acc = fmaf(piece_dot<ND>(wd[r][p], av[p]), e8m0_to_f32(sd[r][p]), acc);
+                const float tot = wave_sum_to_lane63(acc);
+                const int n = n0 + r;
+                if (lane == 63 && n < a.Hr)
+                    __hip_atomic_store(a.yrow + static_cast<int64_t>(pair) * a.Hr + n, tot, __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_AGENT);
+            }
+        }
+    }
+    // The block counts itself done once its row stores (agent-scope atomic stores, written
+    // through to the coherence point) have completed; the last of the range's blocks runs an
+    // agent-scope acquire, resets the counter and combines.  U zeroed every counter.
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        uint32_t *ctr = a.counter + rr;
+        const uint32_t old = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        last_s = old + 1 == static_cast<uint32_t>(max(nu, 1));
+        if (last_s) {
+            __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+        }
+    }
+    __syncthreads();
+    if (!last_s) return;
+    for (int o = threadIdx.x; o < a.T * RB; o += 256) {
+        const int tk = o / RB, n = rr * RB + o % RB;
+        if (n >= a.Hr) continue;
+        float y = a.yadd ? a.yadd[static_cast<int64_t>(tk) * a.Hr + n] : 0.f;
+        for (int j = 0; j < a.k; ++j) {
+            const int pair = tk * a.k + j;
+            if (a.live[pair])
+                y = fmaf(a.wts[pair],
+                         __hip_atomic_load(a.yrow + static_cast<int64_t>(pair) * a.Hr + n, __ATOMIC_RELAXED,
+                                           __HIP_MEMORY_SCOPE_AGENT),
+                         y);
+        }
+        const int64_t oi = static_cast<int64_t>(tk) * a.Hr + n;
+        if (a.out_bf16)
+            static_cast<uint16_t *>(a.out)[oi] = f32_to_bf16(y);
+        else
+            static_cast<float *>(a.out)[oi] = y;
+    }
+}
+
+// ------------------------------------------------------------------ R: dense rows, T tokens
+// bf16 row sets [N, K] against T input rows [T, K] (bf16 or fp32) staged in LDS in plain
+// 16-byte chunk order, tb tokens at a time; 4 waves per block:
+//   section 0 (blocks [0, blocks0)): R rows per wave (1 for rows of more than 4096 values, up
+//                                    to 4 for rows of at most 2048), out0[t * ld0 + n] = W0[n] . in[t]
+//   section 1 (the next blocks):     one (gate, up) row pair per wave,
+//                                    act[t * ld1 + i] = f(G[i] . in[t], U[i] . in[t])
+// Products are exact (bf16 x bf16 in v_dot2, bf16 x fp32 as fp32 FMAs), accumulation fp32.
+struct MRowsArgs {
+    const void *in;          // [T, K] rows
+    int T, K, tb;
+    const uint16_t *w0;      // section 0 rows [N0, K]
+    int N0, blocks0;
+    float *out0;
+    int ld0;
+    const uint16_t *wg, *wu; // section 1 rows [N1, K] each
+    int N1;
+    float *act;
+    int ld1;
+    int act_kind;
+    float beta, lbeta;
+};
+constexpr int kRowWaves = 4;
+// small enough that LDS allows more blocks per CU than the registers do (three at 133 VGPRs)
+constexpr int kLdsBudgetR = 32768;
+
+// 8 bf16 weights . 8 bf16 inputs (exact products)
+__device__ __forceinline__ float rdot(uint4 w, const uint4 *x, int c, float acc) {
+    const uint4 v = x[c];
+    acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, w.x), __builtin_bit_cast(bf16x2, v.x), acc, false);
+    acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, w.y), __builtin_bit_cast(bf16x2, v.y), acc, false);
+    acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, w.z), __builtin_bit_cast(bf16x2, v.z), acc, false);
+    acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, w.w), __builtin_bit_cast(bf16x2, v.w), acc, false);
+    return acc;
+}
+// 8 bf16 weights . 8 fp32 inputs (the weights widened exactly, fp32 FMAs)
+__device__ __forceinline__ float rdot(uint4 w, const float4 *x, int c, float acc) {
+    const float4 a = x[2 * c], b = x[2 * c + 1];
+    acc = fmaf(__uint_as_float(w.x << 16), a.x, acc);
+    acc = fmaf(__uint_as_float(w.x & 0xffff0000u), a.y, acc);
+    acc = fmaf(__uint_as_float(w.y << 16), a.z, acc);
+    acc = fmaf(__uint_as_float(w.y & 0xffff0000u), a.w, acc);
+    acc = fmaf(__uint_as_float(w.z << 16), b.x, acc);
+    acc = fmaf(__uint_as_float(w.z & 0xffff0000u), b.y, acc);
+    acc = fmaf(__uint_as_float(w.w << 16), b.z, acc);
+    acc = fmaf(__uint_as_float(w.w & 0xffff0000u), b.w, acc);
+    return acc;
+}
+
+// IT: input element type (uint16_t = bf16, float); CH: 16-byte weight chunks per lane (K <= 512 CH);
+// R: section-0 rows per wave (narrow rows take several, so one staged batch serves more rows).
+template <typename IT, int CH, int R>
+__global__ __launch_bounds__(256) void multi_rows_kernel(MRowsArgs a) {
+    extern __shared__ uint4 xs[];  // [tb][K * sizeof(IT) / 16]
+    using XC = typename std::conditional<std::is_same<IT, float>::value, float4, uint4>::type;
+    constexpr int NR = R > 2 ? R : 2;  // weight rows held per wave (a pair needs two)
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+    const bool pair = static_cast<int>(blockIdx.x) >= a.blocks0;  // uniform
+    const int nrows = pair ? 2 : R;                                // rows this wave reduces
+    const int n0 = pair ? (static_cast<int>(blockIdx.x) - a.blocks0) * kRowWaves + wave
+                        : (static_cast<int>(blockIdx.x) * kRowWaves + wave) * R;
+    const int N = pair ? a.N1 : a.N0;
+    const int nch = a.K >> 3;
+    const uint32_t rowb = static_cast<uint32_t>(a.K) * 2u;
+    const auto rg = make_rsrc(pair ? a.wg : a.w0, static_cast<uint32_t>(N) * rowb);
+    const auto ru = make_rsrc(a.wu, pair ? static_cast<uint32_t>(N) * rowb : 0u);
+    uint4 w[NR][CH];
+#pragma unroll
+    for (int r = 0; r < NR; ++r) {
+        // plain: rows n0 + r (r < R); pair: gate row n0 (r = 0) and up row n0 (r = 1)
+        const int n = pair ? n0 : n0 + r;
+        const bool ok = (pair ? r < 2 : r < R) && n < N;
+#pragma unroll
+        for (int u = 0; u < CH; ++u) {
+            const int c = u * 64 + lane;
+            const uint32_t off = (ok && c < nch) ? static_cast<uint32_t>(n) * rowb + c * 16u : kOobOffset;
+            w[r][u] = buf_load16(pair && r == 1 ? ru : rg, off);
+        }
+    }
+    const int cpr = static_cast<int>(a.K * sizeof(IT) / 16);  // 16-byte chunks per input row
+    const uint4 *in4 = static_cast<const uint4 *>(a.in);
+#pragma unroll 1
+    for (int c0 = 0; c0 < a.T; c0 += a.tb) {
+        const int nb = min(a.tb, a.T - c0);
+        if (c0 > 0) __syncthreads();  // every wave is done with the previous batch
+        for (int i = threadIdx.x; i < nb * cpr; i += 64 * kRowWaves) xs[i] = in4[static_cast<int64_t>(c0) * cpr + i];
+        __syncthreads();
+#pragma unroll 1
+        for (int c = 0; c < nb; ++c) {
+            // keep the weights packed inside the token loop (no hoisted widening)
+#pragma unroll
+            for (int r = 0; r < NR; ++r)
+#pragma unroll
+                for (int u = 0; u < CH; ++u)
+                    asm volatile("" : "+v"(w[r][u].x), "+v"(w[r][u].y), "+v"(w[r][u].z), "+v"(w[r][u].w));
+            const XC *xr = reinterpret_cast<const XC *>(xs + c * cpr);
+            float acc[NR];
+#pragma unroll
+            for (int r = 0; r < NR; ++r) {
+                float a0 = 0.f, a1 = 0.f;
+                if (r < nrows) {
+#pragma unroll
+                    for (int u = 0; u < CH; ++u) {
+                        const int cc = u * 64 + lane;
+                        if (cc < nch) {
+                            if (u & 1)
+                                a1 = rdot(w[r][u], xr, cc, a1);
+                            else
+                                a0 = rdot(w[r][u], xr, cc, a0);
+                        }
+                    }
+                }
+                acc[r] = wave_sum_to_lane63(a0 + a1);
+            }
+            const int t = c0 + c;
+            if (lane == 63) {
+                if (pair) {
+                    if (n0 < N) a.act[static_cast<int64_t>(t) * a.ld1 + n0] = act_fn(acc[0], acc[1], a.act_kind, a.beta, a.lbeta);
+                } else {
+#pragma unroll
+                    for (int r = 0; r < R; ++r)
+                        if (n0 + r < N) a.out0[static_cast<int64_t>(t) * a.ld0 + n0 + r] = acc[r];
+                }
+            }
+        }
+    }
+}
+
+template <typename IT>
+int launch_rows_multi(MRowsArgs &r, hipStream_t st) {
+    const size_t row = static_cast<size_t>(r.K) * sizeof(IT);
+    r.tb = static_cast<int>(std::max<size_t>(1, std::min<size_t>(r.T, kLdsBudgetR / row)));
+    const int ch = static_cast<int>(cdiv(r.K / 8, 64));
+    const int R = ch <= 4 ? 4 : (ch <= 8 ? 2 : 1);
+    r.blocks0 = r.w0 ? static_cast<int>(cdiv(r.N0, kRowWaves * R)) : 0;
+    const int blocks1 = r.wg ? static_cast<int>(cdiv(r.N1, kRowWaves)) : 0;
+    const int blocks = r.blocks0 + blocks1;
+    if (blocks == 0) return K3_OK;
+    const size_t lds = static_cast<size_t>(r.tb) * row;
+    const dim3 g(static_cast<unsigned>(blocks));
+    if (ch <= 4)
+        multi_rows_kernel<IT, 4, 4><<<g, 64 * kRowWaves, lds, st>>>(r);
+    else if (ch <= 8)
+        multi_rows_kernel<IT, 8, 2><<<g, 64 * kRowWaves, lds, st>>>(r);
+    else if (ch <= 14)
+        multi_rows_kernel<IT, 14, 1><<<g, 64 * kRowWaves, lds, st>>>(r);
+    else if (ch <= 16)
+        multi_rows_kernel<IT, 16, 1><<<g, 64 * kRowWaves, lds, st>>>(r);
+    else
+        return set_error(K3_ERR_SHAPE, "moe layer (T tokens): row width %d above 8192", r.K);
+    return check_hip(hipGetLastError(), "moe layer (T tokens): dense rows launch");
+}
+
+// ------------------------------------------------------------------ host side
+struct MultiWs {
+    size_t counter, nu, u_count, u_pairs, live, u_ptrs, act, yrow, total;
+};
+
+size_t up256(size_t v) { return (v + 255) & ~size_t(255); }
+
+MultiWs multi_ws_layout(int64_t T, int64_t H, int64_t I, int64_t k) {
+    const int64_t P = T * k;
+    MultiWs L{};
+    size_t o = 0;
+    L.counter = o, o += kCounterBytes;
+    L.nu = o, o += 256;
+    L.u_count = o, o += up256(P * 4);
+    L.u_pairs = o, o += up256(P * T * 4);
+    L.live = o, o += up256(P * 4);
+    L.u_ptrs = o, o += up256(P * 6 * 8);
+    L.act = o, o += up256(P * I * 4);
+    L.yrow = o, o += up256(P * H * 4);
+    L.total = o;
+    return L;
+}
+
+// Rows per D block for the intermediate width's groups GI (as the layer's down launch).
+int down_rows(int GI) { return GI <= 64 ? 4 * 14 : (GI <= 96 ? 4 * 7 : 4 * 4); }
+
+template <typename XT>
+int launch_union_gateup(MultiArgs &a, int n_slots, hipStream_t st) {
+    multi_union_kernel<<<1, 256, 0, st>>>(a);
+    int rc = check_hip(hipGetLastError(), "moe routed decode: union launch");
+    if (rc) return rc;
+    const int GH = a.Hr / 32;
+    const size_t xrow = static_cast<size_t>(a.Hr) * sizeof(XT);
+    a.tb_x = static_cast<int>(std::max<size_t>(1, std::min<size_t>(a.T, kLdsBudgetG / xrow)));
+    const dim3 gg(static_cast<unsigned>(n_slots * (a.I / kGRows)));
+    const size_t lds_g = static_cast<size_t>(a.tb_x) * xrow;
+    if (GH <= 64)
+        multi_gateup_kernel<XT, 1><<<gg, 256, lds_g, st>>>(a);
+    else if (GH <= 128)
+        multi_gateup_kernel<XT, 2><<<gg, 256, lds_g, st>>>(a);
+    else
+        multi_gateup_kernel<XT, 4><<<gg, 256, lds_g, st>>>(a);
+    return check_hip(hipGetLastError(), "moe routed decode: gate/up launch");
+}
+
+int launch_down(MultiArgs &a, int n_slots, hipStream_t st) {
+    const int GI = a.I / 32;
+    const dim3 gd(static_cast<unsigned>(n_slots * a.n_ranges));
+    auto down = [&](auto kern, int na) {
+        const size_t per = (static_cast<size_t>(na) * 256 + 1) * 16;
+        a.tb_act = static_cast<int>(std::max<size_t>(1, std::min<size_t>(a.T, kLdsBudgetD / per)));
+        kern<<<gd, 256, static_cast<size_t>(a.tb_act) * per, st>>>(a);
+    };
+    if (GI <= 64)
+        down(multi_down_kernel<32, 1, 14>, 2);
+    else if (GI <= 96)
+        down(multi_down_kernel<16, 3, 7>, 3);
+    else
+        down(multi_down_kernel<32, 2, 4>, 4);
+    return check_hip(hipGetLastError(), "moe routed decode: down launch");
+}
+
+template <typename XT>
+int launch_multi(MultiArgs &a, int n_slots, hipStream_t st) {
+    const int rc = launch_union_gateup<XT>(a, n_slots, st);
+    return rc ? rc : launch_down(a, n_slots, st);
+}
+
+// Validation and the MultiArgs of the routed part; the workspace starts at w.
+int multi_args(MultiArgs &a, const void *x, int x_dtype, const int32_t *expert_idx, const float *expert_w,
+               const void *expert_table, void *out, int out_dtype, int64_t T, int64_t H, int64_t I,
+               int64_t n_experts, int64_t top_k, int act_kind, float beta, float linear_beta, char *w,
+               const char *what) {
+    if (x_dtype != K3_F32 && x_dtype != K3_BF16) return set_error(K3_ERR_DTYPE, "%s: x_dtype %d", what, x_dtype);
+    if (out_dtype != K3_F32 && out_dtype != K3_BF16)
+        return set_error(K3_ERR_DTYPE, "%s: out_dtype %d", what, out_dtype);
+    if (act_kind != K3_ACT_SILU && act_kind != K3_ACT_SITU)
+        return set_error(K3_ERR_SHAPE, "%s: act_kind %d", what, act_kind);
+    if (T < 1 || T > kMaxTokens)
+        return set_error(K3_ERR_SHAPE, "%s: T=%lld must be in 1..%d", what, (long long)T, kMaxTokens);
+    if (n_experts <= 0 || n_experts > kMaxExperts || top_k <= 0 || top_k > kMaxTopK || top_k > n_experts)
+        return set_error(K3_ERR_SHAPE, "%s: n_experts must be in 1..%d and top_k in 1..min(%d, n_experts)", what,
+                         kMaxExperts, kMaxTopK);
+    if (H <= 0 || H % 128 || H > 8192 || I <= 0 || I % 128 || I > 4096)
+        return set_error(K3_ERR_SHAPE, "%s: H=%lld (multiple of 128, <= 8192) and I=%lld (multiple of 128, <= 4096)",
+                         what, (long long)H, (long long)I);
+    if (!aligned16(x) || !aligned16(w))
+        return set_error(K3_ERR_ALIGN, "%s: x and workspace must be 16-byte aligned", what);
+    const MultiWs L = multi_ws_layout(T, H, I, top_k);
+    a = MultiArgs{};
+    a.x = x;
+    a.idx = expert_idx;
+    a.wts = expert_w;
+    a.table = static_cast<const uint64_t *>(expert_table);
+    a.out = out;
+    a.T = static_cast<int>(T);
+    a.Hr = static_cast<int>(H);
+    a.I = static_cast<int>(I);
+    a.E = static_cast<int>(n_experts);
+    a.k = static_cast<int>(top_k);
+    a.P = a.T * a.k;
+    a.act_kind = act_kind;
+    a.beta = beta;
+    a.lbeta = linear_beta;
+    a.out_bf16 = out_dtype == K3_BF16;
+    a.n_ranges = static_cast<int>(cdiv(H, down_rows(static_cast<int>(I / 32))));
+    a.counter = reinterpret_cast<uint32_t *>(w + L.counter);
+    a.nu = reinterpret_cast<int32_t *>(w + L.nu);
+    a.u_count = reinterpret_cast<int32_t *>(w + L.u_count);
+    a.u_pairs = reinterpret_cast<int32_t *>(w + L.u_pairs);
+    a.live = reinterpret_cast<int32_t *>(w + L.live);
+    a.u_ptrs = reinterpret_cast<uint64_t *>(w + L.u_ptrs);
+    a.act = reinterpret_cast<float *>(w + L.act);
+    a.yrow = reinterpret_cast<float *>(w + L.yrow);
+    return K3_OK;
+}
+
+// The whole layer for T tokens: router and shared records after the routed part's.
+struct LayerMultiWs {
+    size_t routed, logits, scores, corrected, idx, w, act_sh, ysh, total;
+};
+
+LayerMultiWs layer_multi_layout(int64_t T, int64_t H, int64_t I, int64_t Is, int64_t E, int64_t k) {
+    LayerMultiWs L{};
+    size_t o = multi_ws_layout(T, H, I, k).total;
+    L.routed = 0;
+    L.logits = o, o += up256(T * E * 4);
+    L.scores = o, o += up256(T * E * 4);
+    L.corrected = o, o += up256(T * E * 4);
+    L.idx = o, o += up256(T * k * 4);
+    L.w = o, o += up256(T * k * 4);
+    L.act_sh = o, o += up256(std::max<int64_t>(T * Is, 1) * 4);
+    L.ysh = o, o += up256(T * H * 4);
+    L.total = o;
+    return L;
+}
+
+}  // namespace
+}  // namespace k3
+
+using namespace k3;
+
+extern "C" int64_t k3_moe_routed_workspace_size(int64_t T, int64_t H, int64_t I, int64_t n_experts, int64_t top_k) {
+    (void)n_experts;
+    if (T <= 0 || H <= 0 || I <= 0 || top_k <= 0) return 0;
+    return static_cast<int64_t>(multi_ws_layout(T, H, I, top_k).total);
+}
+
+extern "C" int k3_moe_routed_decode(const void *x, int x_dtype, const int32_t *expert_idx, const float *expert_w,
+                                    const void *expert_table, void *out, int out_dtype, int64_t T, int64_t H,
+                                    int64_t I, int64_t n_experts, int64_t top_k, int act_kind, float beta,
+                                    float linear_beta, void *workspace, int64_t workspace_bytes, void *stream) {
+    if (!x || !expert_idx || !expert_w || !expert_table || !out || !workspace)
+        return set_error(K3_ERR_NULL, "moe routed decode: null pointer");
+    MultiArgs a;
+    int rc = multi_args(a, x, x_dtype, expert_idx, expert_w, expert_table, out, out_dtype, T, H, I, n_experts, top_k,
+                        act_kind, beta, linear_beta, static_cast<char *>(workspace), "moe routed decode");
+    if (rc) return rc;
+    const MultiWs L = multi_ws_layout(T, H, I, top_k);
+    if (workspace_bytes < static_cast<int64_t>(L.total))
+        return set_error(K3_ERR_WORKSPACE, "moe routed decode: workspace %lld < %zu bytes",
+                         (long long)workspace_bytes, L.total);
+    const int n_slots = static_cast<int>(std::min<int64_t>(a.P, n_experts));
+    auto st = static_cast<hipStream_t>(stream);
+    return x_dtype == K3_BF16 ? launch_multi<uint16_t>(a, n_slots, st) : launch_multi<float>(a, n_slots, st);
+}
+
+extern "C" int64_t k3_moe_layer_multi_workspace_size(int64_t T, int64_t H, int64_t I, int64_t shared_I,
+                                                     int64_t n_experts, int64_t top_k) {
+    if (T <= 0 || H <= 0 || I <= 0 || shared_I < 0 || n_experts <= 0 || top_k <= 0) return 0;
+    return static_cast<int64_t>(layer_multi_layout(T, H, I, shared_I, n_experts, top_k).total);
+}
+
+extern "C" int k3_moe_layer_multi_workspace_offsets(int64_t T, int64_t H, int64_t I, int64_t shared_I,
+                                                    int64_t n_experts, int64_t top_k, int64_t *offsets) {
+    if (!offsets) return set_error(K3_ERR_NULL, "moe layer (T tokens) offsets: null pointer");
+    const LayerMultiWs L = layer_multi_layout(T, H, I, shared_I, n_experts, top_k);
+    const size_t v[5] = {L.logits, L.scores, L.corrected, L.idx, L.w};
+    for (int i = 0; i < 5; ++i) offsets[i] = static_cast<int64_t>(v[i]);
+    return K3_OK;
+}
+
+extern "C" int k3_moe_layer_decode_multi(const void *x, int x_dtype, const void *router_w, const void *router_bias,
+                                         int route_kind, int renormalize, float scaling, const void *expert_table,
+                                         const void *shared_gate, const void *shared_up, const void *shared_down,
+                                         void *out, int out_dtype, int64_t T, int64_t H, int64_t I, int64_t shared_I,
+                                         int64_t n_experts, int64_t top_k, int act_kind, float beta,
+                                         float linear_beta, void *workspace, int64_t workspace_bytes, void *stream) {
+    const char *what = "moe layer (T tokens)";
+    if (!x || !router_w || !expert_table || !out || !workspace) return set_error(K3_ERR_NULL, "%s: null pointer", what);
+    if (route_kind != K3_ROUTE_SOFTMAX && route_kind != K3_ROUTE_SIGMOID_BIAS)
+        return set_error(K3_ERR_SHAPE, "%s: route_kind %d", what, route_kind);
+    const bool has_shared = shared_gate || shared_up || shared_down;
+    if (has_shared && (!shared_gate || !shared_up || !shared_down || shared_I <= 0 || shared_I % 128 ||
+                       shared_I > 8192))
+        return set_error(K3_ERR_SHAPE, "%s: shared expert needs gate, up and down with shared_I a multiple of 128, "
+                         "<= 8192", what);
+    if (!aligned16(router_w) || (has_shared && (!aligned16(shared_gate) || !aligned16(shared_up) ||
+                                                !aligned16(shared_down))))
+        return set_error(K3_ERR_ALIGN, "%s: router and shared weights must be 16-byte aligned", what);
+    char *w = static_cast<char *>(workspace);
+    const LayerMultiWs L = layer_multi_layout(T, H, I, has_shared ? shared_I : 0, n_experts, top_k);
+    float *logits = reinterpret_cast<float *>(w + L.logits);
+    int32_t *idx = reinterpret_cast<int32_t *>(w + L.idx);
+    float *wts = reinterpret_cast<float *>(w + L.w);
+    MultiArgs a;
+    int rc = multi_args(a, x, x_dtype, idx, wts, expert_table, out, out_dtype, T, H, I, n_experts, top_k, act_kind,
+                        beta, linear_beta, w, what);
+    if (rc) return rc;
+    if (workspace_bytes < static_cast<int64_t>(L.total))
+        return set_error(K3_ERR_WORKSPACE, "%s: workspace %lld < %zu bytes", what, (long long)workspace_bytes, L.total);
+    auto st = static_cast<hipStream_t>(stream);
+    const bool bf = x_dtype == K3_BF16;
+    // R: router logits [T, E] and the shared gate/up act [T, shared_I], one launch on x
+    MRowsArgs r{};
+    r.in = x;
+    r.T = a.T;
+    r.K = a.Hr;
+    r.w0 = static_cast<const uint16_t *>(router_w);
+    r.N0 = a.E;
+    r.out0 = logits;
+    r.ld0 = a.E;
+    float *act_sh = reinterpret_cast<float *>(w + L.act_sh);
+    if (has_shared) {
+        r.wg = static_cast<const uint16_t *>(shared_gate);
+        r.wu = static_cast<const uint16_t *>(shared_up);
+        r.N1 = static_cast<int>(shared_I);
+        r.act = act_sh;
+        r.ld1 = static_cast<int>(shared_I);
+    }
+    r.act_kind = act_kind;
+    r.beta = beta;
+    r.lbeta = linear_beta;
+    rc = bf ? launch_rows_multi<uint16_t>(r, st) : launch_rows_multi<float>(r, st);
+    if (rc) return rc;
+    // the batched top-k on those logits (softmax / sigmoid + bias, renormalised, scaled)
+    rc = k3_moe_topk(logits, a.E, a.T, a.E, static_cast<const float *>(router_bias), route_kind, renormalize, scaling,
+                     a.k, idx, wts, reinterpret_cast<float *>(w + L.scores), reinterpret_cast<float *>(w + L.corrected),
+                     stream);
+    if (rc) return rc;
+    const int n_slots = static_cast<int>(std::min<int64_t>(a.P, n_experts));
+    rc = bf ? launch_union_gateup<uint16_t>(a, n_slots, st) : launch_union_gateup<float>(a, n_slots, st);
+    if (rc) return rc;
+    if (has_shared) {
+        // the shared down rows [H, shared_I] against the fp32 act -> [T, H], added in D's combine
+        MRowsArgs d{};
+        d.in = act_sh;
+        d.T = a.T;
+        d.K = static_cast<int>(shared_I);
+        d.w0 = static_cast<const uint16_t *>(shared_down);
+        d.N0 = a.Hr;
+        d.out0 = reinterpret_cast<float *>(w + L.ysh);
+        d.ld0 = a.Hr;
+        rc = launch_rows_multi<float>(d, st);
+        if (rc) return rc;
+        a.yadd = d.out0;
+    }
+    return launch_down(a, n_slots, st);
+}

@@ -49,6 +49,8 @@ SIGNATURES: dict[str, list] = {
     "k3_mla_workspace_size": [_I64, _I64],
     "k3_mla_decode_absorbed": [_P, _P, _I64, _I64, _I32, _P, _P, _P, _I64, _P, _I64, _I64, _I64, _I64, _I64,
                                _I64, _I64, _F32, _P, _I32, _I64, _P, _I64, _P],
+    "k3_mla_decode_absorbed_f32": [_P, _P, _I64, _I64, _I32, _P, _P, _P, _I64, _P, _I64, _I64, _I64, _I64, _I64,
+                                   _I64, _I64, _F32, _P, _I32, _I64, _P, _I64, _P],
     "k3_mla_step_workspace_size": [_I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64],
     "k3_mla_step_decode": [_P, _I32, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _P, _I64, _I64, _I64, _F32,
                            _F32, _P, _I32, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _P, _I64, _P],
@@ -60,6 +62,13 @@ SIGNATURES: dict[str, list] = {
     "k3_moe_grouped_workspace_size": [_I64, _I64, _I64, _I64, _I64],
     "k3_moe_grouped_ffn": [_P, _I32, _P, _P, _P, _P, _I32, _I64, _I64, _I64, _I64, _I64, _I32, _F32, _F32,
                            _P, _I64, _P],
+    "k3_moe_routed_workspace_size": [_I64, _I64, _I64, _I64, _I64],
+    "k3_moe_routed_decode": [_P, _I32, _P, _P, _P, _P, _I32, _I64, _I64, _I64, _I64, _I64, _I32, _F32, _F32,
+                             _P, _I64, _P],
+    "k3_moe_layer_multi_workspace_size": [_I64, _I64, _I64, _I64, _I64, _I64],
+    "k3_moe_layer_multi_workspace_offsets": [_I64, _I64, _I64, _I64, _I64, _I64, _P],
+    "k3_moe_layer_decode_multi": [_P, _I32, _P, _P, _I32, _I32, _F32, _P, _P, _P, _P, _P, _I32, _I64, _I64,
+                                  _I64, _I64, _I64, _I64, _I32, _F32, _F32, _P, _I64, _P],
     "k3_stream_read": [_P, _I64, _P, _P],
     "k3_stream_copy": [_P, _P, _I64, _P],
 }
@@ -70,7 +79,9 @@ _RESTYPE = {"k3_last_error": ctypes.c_char_p, "k3_version": ctypes.c_char_p,
             "k3_mla_workspace_size": ctypes.c_int64,
             "k3_mla_step_workspace_size": ctypes.c_int64,
             "k3_kda_step_workspace_size": ctypes.c_int64,
-            "k3_moe_grouped_workspace_size": ctypes.c_int64}
+            "k3_moe_grouped_workspace_size": ctypes.c_int64,
+            "k3_moe_routed_workspace_size": ctypes.c_int64,
+            "k3_moe_layer_multi_workspace_size": ctypes.c_int64}
 
 
 class K3LibraryError(ImportError):

@@ -3,9 +3,10 @@ air_llm/models/kimi_k3/attention_mla.py (``MLACache``, ``MLAAttention``).
 
 ``mla_decode_absorbed(q_nope, q_rot, wk, wv, lat, rot, scale)`` is the attention core of
 ``MLAAttention.__call__`` for one decode token (``attention_mla.py:193-212``): it runs on
-the bf16 latent cache in place (four HIP launches: query absorption, split-T flash
-decoding on bf16 MFMA with hi/lo-split fp32 operands, log-sum-exp merge of the splits, the
-W_UV absorption) and returns ``[H, v_head_dim]``.
+the latent cache in place, bf16 or the reference's fp32 (four HIP launches: query
+absorption, split-T flash decoding on bf16 MFMA with hi/lo-split fp32 operands -- fp32
+cache rows split into hi/lo bf16 planes as they are staged --, log-sum-exp merge of the
+splits, the W_UV absorption) and returns ``[H, v_head_dim]``.
 
 ``MLACache`` keeps the reference's surface (``latent``/``rot`` backing buffers with spare
 capacity, valid prefix ``length``, ``append`` with chunked doubling growth, ``view``,
@@ -22,8 +23,10 @@ in torch on the GPU.
 The cache defaults to bf16 (``cfg.mla_cache_dtype``), which the HIP core reads in place; the
 reference's default is an fp32 cache (``attention_mla.py:164``), which it calls lossless.
 An fp32 cache (``mla_cache_dtype=torch.float32``, or a caller's fp32 ``MLACache``) is
-accepted: every step on it, one token included, runs the fp32 masked form on the GPU (no
-HIP core), the exact-but-slower validation route.
+accepted: a decode token on it runs the HIP core on the fp32 rows
+(``k3_mla_decode_absorbed_f32``; with bf16 ``kv_b``, the checkpoint dtype, whose halves the
+core takes as they are), the projections around it in fp32; fp32 ``kv_b`` (validation mode)
+and prefill run the fp32 masked form.
 """
 from __future__ import annotations
 
@@ -117,17 +120,17 @@ def _heads(w: torch.Tensor, name: str) -> torch.Tensor:
 
 
 def _cache_rows(c: torch.Tensor, width: int, name: str) -> torch.Tensor:
-    """[T, width] or [1, T, width] bf16 with unit inner stride and a row stride that is a
-    multiple of 8 elements (cache backing buffers qualify); copies otherwise."""
+    """[T, width] or [1, T, width] bf16 or fp32 with unit inner stride and a row stride of
+    whole 16-byte units (cache backing buffers qualify); copies otherwise."""
     if c.dim() == 3:
         if c.shape[0] != 1:
             raise ValueError(f"{name}: the decode kernel takes batch 1; got {tuple(c.shape)}")
         c = c[0]
     if c.dim() != 2 or c.shape[1] != width:
         raise ValueError(f"{name} must be [T, {width}]; got {tuple(c.shape)}")
-    if c.dtype != torch.bfloat16:
-        raise TypeError(f"{name} must be bfloat16: the kernels read the bf16 latent cache")
-    if c.stride(1) != 1 or c.stride(0) % 8 or c.data_ptr() % 16:
+    if c.dtype not in (torch.bfloat16, torch.float32):
+        raise TypeError(f"{name} must be bfloat16 or float32 (the latent cache dtypes); got {c.dtype}")
+    if c.stride(1) != 1 or c.stride(0) % (16 // c.element_size()) or c.data_ptr() % 16:
         c = c.contiguous()
         if c.data_ptr() % 16:
             c = c.clone()
@@ -140,8 +143,10 @@ def mla_decode_absorbed(q_nope: torch.Tensor, q_rot: torch.Tensor, wk: torch.Ten
     """Absorbed MLA attention for one query per head (attention_mla.py:193-212, T == 1).
 
     q_nope [H, nope], q_rot [H, rope] (bf16 or fp32); wk [H, nope, r], wv [H, v, r]
-    (bf16, or the reference's [1, H, ., r] views); lat [T, r], rot [T, rope] bf16 cache
-    rows (or [1, T, .]).  Returns o [H, v] in out_dtype (fp32 accumulation throughout).
+    (bf16, or the reference's [1, H, ., r] views); lat [T, r], rot [T, rope] cache rows (or
+    [1, T, .]), both bf16 (k3_mla_decode_absorbed) or both fp32, the reference's default
+    cache dtype (k3_mla_decode_absorbed_f32).  Returns o [H, v] in out_dtype (fp32
+    accumulation throughout).
     """
     if q_nope.dim() != 2 or q_rot.dim() != 2 or q_nope.shape[0] != q_rot.shape[0]:
         raise ValueError(f"q_nope [H, nope] and q_rot [H, rope] expected; got {tuple(q_nope.shape)}, "
@@ -156,6 +161,8 @@ def mla_decode_absorbed(q_nope: torch.Tensor, q_rot: torch.Tensor, wk: torch.Ten
     rot = _cache_rows(rot, q_rot.shape[1], "rot")
     if lat.shape[0] != rot.shape[0]:
         raise ValueError(f"lat has {lat.shape[0]} tokens, rot {rot.shape[0]}")
+    if lat.dtype != rot.dtype:
+        raise TypeError(f"lat and rot must share one dtype; got {lat.dtype}, {rot.dtype}")
     T.require_device(q_nope, q_rot, wk, wv, lat, rot)
     qdt = torch.bfloat16 if (q_nope.dtype == torch.bfloat16 and q_rot.dtype == torch.bfloat16) else torch.float32
     q_nope = q_nope.to(qdt)
@@ -169,7 +176,8 @@ def mla_decode_absorbed(q_nope: torch.Tensor, q_rot: torch.Tensor, wk: torch.Ten
     ntok = lat.shape[0]
     ws_bytes = int(_lib.lib().k3_mla_workspace_size(H, ntok))
     ws = _workspace.get(lat.device, ws_bytes, "mla")
-    _lib.call("k3_mla_decode_absorbed", T.ptr(q_nope), T.ptr(q_rot), q_nope.stride(0), q_rot.stride(0),
+    entry = "k3_mla_decode_absorbed" if lat.dtype == torch.bfloat16 else "k3_mla_decode_absorbed_f32"
+    _lib.call(entry, T.ptr(q_nope), T.ptr(q_rot), q_nope.stride(0), q_rot.stride(0),
               T.dtype_code(qdt),
               T.ptr(wk), T.ptr(wv), T.ptr(lat), lat.stride(0), T.ptr(rot), rot.stride(0), ntok, H, r,
               q_rot.shape[1], nope, V, float(scale), T.ptr(out), T.dtype_code(out_dtype), out.stride(0),
@@ -246,7 +254,11 @@ class MLAAttention:
         cache.append(c_new, r_new)
         lat, rot = cache.view()
         scale = qhd ** -0.5
-        if Tn == 1 and B == 1 and lat.dtype == torch.bfloat16:
+        # one query token: the HIP core, over a bf16 cache or the reference's default fp32
+        # cache; an fp32 cache with fp32 kv_b (validation mode) keeps the exact fp32 form,
+        # since the core takes W_UK / W_UV in bf16
+        if Tn == 1 and B == 1 and (lat.dtype == torch.bfloat16 or
+                                   (lat.dtype == torch.float32 and self.kv_b.dtype == torch.bfloat16)):
             o = mla_decode_absorbed(q[0, :, 0, :nope], q[0, :, 0, nope:], self.wk, self.wv,
                                     lat[0], rot[0], scale).reshape(1, 1, nh * vhd)
         else:

@@ -134,6 +134,8 @@ class RoutedMoE:
     shared expert with the reference's dtype promotion.
     """
 
+    DECODE_TOKENS = 8  # up to this many tokens: decode kernels; more: grouped (prefill)
+
     def __init__(self, cfg, layer: int, w: dict, expert_source: Callable, fused: bool = True):
         self.cfg, self.L = cfg, layer
         self.src = expert_source
@@ -289,13 +291,28 @@ class RoutedMoE:
         """Prefill form of __call__ for x [..., H]: route every token on x as given (or take
         the given RouterResult), then run the routed experts grouped by expert on the device
         (moe_grouped_ffn); the shared expert, if any, runs on the BLAS library."""
+        return self._forward_routed(x, router, out_dtype, moe_grouped_ffn)
+
+    def multi_forward(self, x: torch.Tensor, router: RouterResult | None = None,
+                      out_dtype=torch.float32) -> torch.Tensor:
+        """Decode form of __call__ for a few tokens x [..., H] (at most DECODE_TOKENS): route
+        every token, then every expert any token selects runs once against all the tokens
+        routed to it (moe_routed_decode: the union of the routed experts built on the device,
+        fp32 accumulation); the shared expert, if any, runs on the BLAS library."""
+        return self._forward_routed(x, router, out_dtype, moe_routed_decode)
+
+    def _forward_routed(self, x, router, out_dtype, routed_fn, validate=None):
+        """Routed experts by routed_fn plus the shared expert; a caller's RouterResult has its
+        ids checked on the device (validate), the layer's own routing needs no check."""
         orig = x.shape
         flat = x.reshape(-1, orig[-1])
+        if validate is None:
+            validate = router is not None
         if router is None:
             router = self.route(flat)
         act, beta, lb = self._act()
-        y = moe_grouped_ffn(flat, router.expert_indices, router.expert_weights, self.expert_table(), self._I,
-                            act, beta, lb, out_dtype=torch.float32)
+        y = routed_fn(flat, router.expert_indices, router.expert_weights, self.expert_table(), self._I,
+                      act, beta, lb, out_dtype=torch.float32, validate=validate)
         if self.sh_gate is not None:
             y = y + self.shared_forward(flat)
         return y.to(out_dtype).reshape(*orig[:-1], self._H)
@@ -310,6 +327,14 @@ class RoutedMoE:
                 y = y + self.shared_forward(flat)
             y = y.to(out_dtype).reshape(*orig[:-1], self._H)
             return (y, r) if return_router else y
+        if flat.shape[0] > self.DECODE_TOKENS:
+            # many tokens: grouped GEMMs on MXFP4 MFMA, every routed expert read once per tile
+            r = self.route(flat)
+            y = self._forward_routed(flat, r, out_dtype, moe_grouped_ffn, validate=False)
+            y = y.reshape(*orig[:-1], self._H)
+            return (y, r) if return_router else y
+        if flat.shape[0] > 1:
+            return self._decode_multi(flat, orig, return_router, out_dtype)
         kind, bias = self._route_args()
         act, beta, lb = self._act()
         table = self.expert_table()
@@ -331,6 +356,42 @@ class RoutedMoE:
             return y
         r = RouterResult(*(torch.cat([getattr(rr, f) for rr in recs]) for f in
                            ("expert_indices", "expert_weights", "raw_scores", "corrected_scores")))
+        return y, r
+
+
+    def _decode_multi(self, flat, orig, return_router, out_dtype):
+        """2..DECODE_TOKENS tokens in one pass (k3_moe_layer_decode_multi): router and
+        shared expert on HIP row kernels, every routed expert any token selects read once for
+        all the tokens routed to it; no host synchronisation.  The RouterResult comes from
+        the workspace records."""
+        import ctypes
+        kind, bias = self._route_args()
+        act, beta, lb = self._act()
+        table = self.expert_table()
+        n = flat.shape[0]
+        x = flat if flat.dtype in (torch.float32, torch.bfloat16) else flat.to(torch.float32)
+        x = T.contiguous_aligned(x)
+        H, I, Is, E, k = self._H, self._I, self._Is, self._E, self._k
+        nbytes = int(_lib.lib().k3_moe_layer_multi_workspace_size(n, H, I, Is, E, k))
+        ws = _workspace.get(self.device, nbytes, "moe_layer_multi")
+        out = torch.empty((n, H), dtype=out_dtype, device=self.device)
+        _lib.call("k3_moe_layer_decode_multi", T.ptr(x), T.dtype_code(x.dtype), T.ptr(self.gate_w), T.ptr(bias),
+                  kind, int(bool(self.cfg.moe_renormalize)), float(self.cfg.routed_scaling_factor), T.ptr(table),
+                  T.ptr(self.sh_gate), T.ptr(self.sh_up), T.ptr(self.sh_down), T.ptr(out), T.dtype_code(out_dtype),
+                  n, H, I, Is, E, k, ACTS[act], float(beta), float(lb or 0.0), T.ptr(ws), ws.numel(), T.stream(x))
+        y = out.reshape(*orig[:-1], H)
+        if not return_router:
+            return y
+        off = (ctypes.c_int64 * 5)()
+        _lib.call("k3_moe_layer_multi_workspace_offsets", n, H, I, Is, E, k, off)
+
+        def rec(o, count, dt):
+            return ws[o:o + 4 * count].view(dt).clone()
+
+        r = RouterResult(rec(off[3], n * k, torch.int32).to(torch.int64).reshape(n, k),
+                         rec(off[4], n * k, torch.float32).reshape(n, k),
+                         rec(off[1], n * E, torch.float32).reshape(n, E),
+                         rec(off[2], n * E, torch.float32).reshape(n, E))
         return y, r
 
 
@@ -364,7 +425,7 @@ class LatentMoE:
     (k3_moe_grouped_ffn); neither synchronises with the host.  ``fused=False`` or fp32 dense
     weights run the reference's structure (``RoutedMoE`` describes it)."""
 
-    DECODE_TOKENS = 8  # up to this many tokens: one fused decode per token; more: grouped
+    DECODE_TOKENS = 8  # up to this many tokens: decode kernels; more: grouped
 
     def __init__(self, cfg, layer: int, w: dict, expert_source: Callable, fused: bool = True):
         self.cfg, self.L = cfg, layer
@@ -415,8 +476,10 @@ class LatentMoE:
         flat = x.reshape(-1, orig[-1])
         if not self._fast:
             return self._forward_loop(flat, orig, return_router, out_dtype)
-        if flat.shape[0] <= self.DECODE_TOKENS:
+        if flat.shape[0] == 1:
             return self._decode(flat, orig, return_router, out_dtype)
+        if flat.shape[0] <= self.DECODE_TOKENS:
+            return self._forward_routed(flat, return_router, out_dtype, orig, moe_routed_decode)
         return self.grouped_forward(flat, return_router, out_dtype, orig)
 
     def _forward_loop(self, flat, orig, return_router, out_dtype):
@@ -433,7 +496,7 @@ class LatentMoE:
         return (y, r) if return_router else y
 
     def _decode(self, flat, orig, return_router, out_dtype):
-        """Per token: k3_moe_latent_layer_decode (route, latent down, routed experts,
+        """One token: k3_moe_latent_layer_decode (route, latent down, routed experts,
         norm, up projection, shared experts; four launches, no host synchronisation)."""
         c, R = self.cfg, self._routed
         act, beta, lb = R._act()
@@ -464,6 +527,15 @@ class LatentMoE:
         (bf16 for a bf16 x, fp32 for an fp32 x); the routed experts grouped by expert on the
         device (k3_moe_grouped_ffn); the norm in fp32; the up projection and the shared
         experts on the BLAS library with exact products and fp32 accumulation."""
+        return self._forward_routed(flat, return_router, out_dtype, orig, moe_grouped_ffn)
+
+    def multi_forward(self, flat, return_router=False, out_dtype=torch.float32, orig=None):
+        """A few decode tokens (at most DECODE_TOKENS): as grouped_forward, with the routed
+        experts run by moe_routed_decode, so every expert any token selects is read once
+        against all the tokens routed to it, with fp32 accumulation."""
+        return self._forward_routed(flat, return_router, out_dtype, orig, moe_routed_decode)
+
+    def _forward_routed(self, flat, return_router, out_dtype, orig, routed_fn):
         c = self.cfg
         orig = orig if orig is not None else flat.shape
         flat = flat.reshape(-1, flat.shape[-1])
@@ -472,8 +544,8 @@ class LatentMoE:
         if flat.dtype == torch.bfloat16:
             h = h.to(torch.bfloat16)                                      # the reference's bf16 matmul
         act, beta, lb = self._routed._act()
-        y = moe_grouped_ffn(h.contiguous(), r.expert_indices, r.expert_weights, self._routed.expert_table(),
-                            int(c.moe_intermediate_size), act, beta, lb, out_dtype=torch.float32, validate=False)
+        y = routed_fn(h.contiguous(), r.expert_indices, r.expert_weights, self._routed.expert_table(),
+                      int(c.moe_intermediate_size), act, beta, lb, out_dtype=torch.float32, validate=False)
         y = _rmsnorm32(y, self._norm32, float(c.rms_norm_eps))
         y = _blas.mm_f32(y, self.up)                                      # latent -> hidden
         if self._routed.sh_gate is not None:
@@ -514,6 +586,44 @@ def moe_grouped_ffn(x: torch.Tensor, expert_indices: torch.Tensor, expert_weight
     nbytes = int(_lib.lib().k3_moe_grouped_workspace_size(n_tok, k, E, H, intermediate))
     ws = _workspace.get(x.device, nbytes, "moe_grouped")
     _lib.call("k3_moe_grouped_ffn", T.ptr(x), T.dtype_code(x.dtype), T.ptr(idx), T.ptr(w), T.ptr(table),
+              T.ptr(out), T.dtype_code(out_dtype), n_tok, H, intermediate, E, k, _act_code(act), float(beta),
+              float(linear_beta or 0.0), T.ptr(ws), ws.numel(), T.stream(x))
+    return out
+
+
+def moe_routed_decode(x: torch.Tensor, expert_indices: torch.Tensor, expert_weights: torch.Tensor,
+                      table: torch.Tensor, intermediate: int, act: str = "silu", beta: float = 1.0,
+                      linear_beta: float | None = None, out_dtype: torch.dtype = torch.float32,
+                      validate: bool = True) -> torch.Tensor:
+    """Routed experts for a few decode tokens: x [T, H] (T <= 8, bf16 or fp32),
+    expert_indices / expert_weights [T, k] -> [T, H].  The per-expert loop of
+    LatentMoE.__call__ (moe.py:119-127) as three launches (k3_moe_routed_decode): the union
+    of the routed experts on the device, then every union expert's gate/up and down rows
+    streamed once against all the tokens routed to it.  ``validate`` checks the ids on the
+    device first (one small device->host copy); unchecked, out-of-range ids contribute
+    nothing."""
+    if x.dim() != 2 or expert_indices.shape != expert_weights.shape or expert_indices.shape[0] != x.shape[0]:
+        raise ValueError(f"x [T, H] with expert_indices/expert_weights [T, k] expected; got {tuple(x.shape)}, "
+                         f"{tuple(expert_indices.shape)}, {tuple(expert_weights.shape)}")
+    if x.dtype not in (torch.bfloat16, torch.float32):
+        x = x.to(torch.float32)
+    T.require_device(x, expert_indices, expert_weights, table)
+    n_tok, H = x.shape
+    k = expert_indices.shape[1]
+    E = table.shape[0]
+    idx = expert_indices.to(torch.int32).contiguous()
+    if validate and idx.numel():
+        lo, hi = (int(v) for v in torch.stack([idx.min(), idx.max()]).tolist())
+        if lo < 0 or hi >= E:
+            raise ValueError(f"expert ids {lo}..{hi} outside 0..{E - 1}")
+    w = expert_weights.to(torch.float32).contiguous()
+    x = T.contiguous_aligned(x)
+    out = torch.empty((n_tok, H), dtype=out_dtype, device=x.device)
+    if n_tok == 0:
+        return out
+    nbytes = int(_lib.lib().k3_moe_routed_workspace_size(n_tok, H, intermediate, E, k))
+    ws = _workspace.get(x.device, nbytes, "moe_routed")
+    _lib.call("k3_moe_routed_decode", T.ptr(x), T.dtype_code(x.dtype), T.ptr(idx), T.ptr(w), T.ptr(table),
               T.ptr(out), T.dtype_code(out_dtype), n_tok, H, intermediate, E, k, _act_code(act), float(beta),
               float(linear_beta or 0.0), T.ptr(ws), ws.numel(), T.stream(x))
     return out

@@ -36,7 +36,9 @@ from __future__ import annotations
 
 import numpy as np
 
-from .mxfp4 import decode_mxfp4
+from concurrent.futures import ThreadPoolExecutor
+
+from .mxfp4 import decode_mxfp4, decode_mxfp4_f64
 
 
 def sigmoid(g: np.ndarray) -> np.ndarray:
@@ -116,27 +118,44 @@ def expert_ffn(x, gate, up, down, kind="silu", beta=1.0, linear_beta=None):
 
 
 def moe_layer(x, idx, weights, experts, shared=None, kind="silu", beta=1.0,
-              linear_beta=None):
+              linear_beta=None, workers: int = 1):
     """Weighted sum of routed experts (+ shared expert on the same hidden state).
 
     ``experts[e]`` is ``(gate, up, down)`` of (packed, scales) pairs; ``shared`` is
-    ``(wg, wu, wd)`` of dense float weights or None.  Tokens are processed one at a time,
-    experts visited in ascending id as in ``k3ref/layers.py:252-256``.
+    ``(wg, wu, wd)`` of dense float weights or None.  Each expert's tokens are gathered and
+    its output scattered back as in ``k3ref/layers.py:252-256``; the weighted outputs are
+    added to ``y`` in ascending expert id.  ``workers > 1`` computes the experts' outputs
+    on that many threads (for full-size layers whose experts are all distinct; the sums are
+    still taken in ascending id, so the result does not depend on ``workers``).
     """
     x = np.atleast_2d(np.asarray(x, np.float64))
     idx = np.atleast_2d(idx)
     weights = np.atleast_2d(weights)
     y = np.zeros((x.shape[0], x.shape[1]), np.float64)
-    # expert ids that share one weight tuple (tests alias them) decode it once; the cache
-    # holds the tuple itself, so its id cannot be reused by another object meanwhile
-    dense = {}
-    for e in sorted({int(v) for v in idx.reshape(-1)}):
+    ids = sorted({int(v) for v in idx.reshape(-1)})
+
+    def routed(e, dense_w):
         tok, slot = np.nonzero(idx == e)
-        ex = experts[e]
-        if id(ex) not in dense:
-            dense[id(ex)] = (ex, tuple(decode_mxfp4(*pair).astype(np.float64) for pair in ex))
-        out = dense_ffn(x[tok], *dense[id(ex)][1], kind=kind, beta=beta, linear_beta=linear_beta)[0]
-        y[tok] += out * weights[tok, slot][:, None]
+        out = dense_ffn(x[tok], *dense_w, kind=kind, beta=beta, linear_beta=linear_beta)[0]
+        return tok, out * weights[tok, slot][:, None]
+
+    if workers > 1:
+        def one(e):
+            return routed(e, tuple(decode_mxfp4_f64(*pair) for pair in experts[e]))
+        with ThreadPoolExecutor(max_workers=workers) as pool:
+            parts = list(pool.map(one, ids))
+    else:
+        # expert ids that share one weight tuple (tests alias them) decode it once; the cache
+        # holds the tuple itself, so its id cannot be reused by another object meanwhile
+        dense = {}
+        parts = []
+        for e in ids:
+            ex = experts[e]
+            if id(ex) not in dense:
+                dense[id(ex)] = (ex, tuple(decode_mxfp4_f64(*pair) for pair in ex))
+            parts.append(routed(e, dense[id(ex)][1]))
+    for tok, contrib in parts:
+        y[tok] += contrib
     if shared is not None:
         y += dense_ffn(x, *shared, kind=kind, beta=beta, linear_beta=linear_beta)[0]
     return y
@@ -150,21 +169,23 @@ def rmsnorm(x, w, eps: float):
 
 def latent_moe(x, router_w, bias, down_w, up_w, norm_w, experts, shared, k: int,
                renormalize: bool = True, scaling: float = 1.0, beta: float = 1.0,
-               linear_beta=None, eps: float = 1e-5, kind: str = "situ", h_bf16: bool = False):
+               linear_beta=None, eps: float = 1e-5, kind: str = "situ", h_bf16: bool = False,
+               workers: int = 1):
     """K3's routed layer (``moe.py:110-132``).
 
     x [T, H]; router_w [E, H] and bias [E] (sigmoid + bias routing); down_w [L, H] and
     up_w [H, L] the latent projections; norm_w [L]; ``experts[e]`` = (gate, up, down)
     (packed, scales) pairs of latent-width experts; ``shared`` = (wg, wu, wd) dense or
     None.  ``h_bf16`` rounds the latent state to bf16, as the reference's bf16 matmul
-    ``flat @ self.down.T`` does (``moe.py:117``).  Returns (y [T, H], idx, weights)."""
+    ``flat @ self.down.T`` does (``moe.py:117``); ``workers`` is ``moe_layer``'s.
+    Returns (y [T, H], idx, weights)."""
     x = np.atleast_2d(np.asarray(x, np.float64))
     idx, w, _, _ = route_sigmoid_bias(x, router_w, bias, k, renormalize, scaling)
     h = x @ np.asarray(down_w, np.float64).T
     if h_bf16:
         from .mxfp4 import bf16_round
         h = bf16_round(h.astype(np.float32)).astype(np.float64)
-    y = moe_layer(h, idx, w, experts, None, kind, beta, linear_beta)
+    y = moe_layer(h, idx, w, experts, None, kind, beta, linear_beta, workers)
     y = rmsnorm(y, norm_w, eps) @ np.asarray(up_w, np.float64).T
     if shared is not None:
         y = y + dense_ffn(x, *shared, kind=kind, beta=beta, linear_beta=linear_beta)[0]

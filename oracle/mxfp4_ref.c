@@ -11,6 +11,8 @@
  *                    output, K walked in ascending order, fmaf per element, scale built
  *                    as the float whose bit pattern is (byte << 23) -- so byte 0 gives
  *                    +0.0 there, exactly like the Metal source.
+ * oracle_decode_f64  oracle_decode_f32 widened to float64, built from a per-group table of
+ *                    the 16 float32 code values (fast enough for full-size oracles).
  *
  * Build: gcc -O2 -fPIC -shared -ffp-contract=off (no fast-math: subnormals matter).
  */
@@ -60,6 +62,29 @@ void oracle_matvec_seqfma(const float *x, const uint8_t *packed, const uint8_t *
                 acc = fmaf(x[t * k + k0 + 1], v1, acc);
             }
             out[t * n + r] = acc;
+        }
+    }
+}
+
+/* oracle_decode_f64: the float64 widening of oracle_decode_f32, bit for bit, for the
+ * full-size oracles.  Per row group the 16 code values are formed once exactly as
+ * oracle_decode_f32 forms each element (code value times ldexpf(1, b-127) in float32,
+ * so byte 255 gives inf/NaN and bytes 253..254 overflow as there), then widened; each
+ * packed byte then reads two of them from that table. */
+void oracle_decode_f64(const uint8_t *packed, const uint8_t *scales,
+                       int64_t n, int64_t k, double *out) {
+    const int64_t kh = k / 2, g = k / 32;
+    double vals[16];
+    for (int64_t r = 0; r < n; ++r) {
+        for (int64_t j = 0; j < g; ++j) {
+            const float s = ldexpf(1.0f, (int)scales[r * g + j] - 127);
+            for (unsigned c = 0; c < 16; ++c) vals[c] = (double)(code_value(c) * s);
+            const uint8_t *p = packed + r * kh + j * 16;
+            double *o = out + r * k + j * 32;
+            for (int i = 0; i < 16; ++i) {
+                o[2 * i] = vals[p[i] & 0x0F];
+                o[2 * i + 1] = vals[p[i] >> 4];
+            }
         }
     }
 }

@@ -39,6 +39,8 @@ def load():
         i64 = ctypes.c_int64
         lib.oracle_decode_f32.argtypes = [p, p, i64, i64, p]
         lib.oracle_decode_f32.restype = None
+        lib.oracle_decode_f64.argtypes = [p, p, i64, i64, p]
+        lib.oracle_decode_f64.restype = None
         lib.oracle_matvec_seqfma.argtypes = [p, p, p, i64, i64, i64, p]
         lib.oracle_matvec_seqfma.restype = None
         _lib = lib
@@ -55,6 +57,19 @@ def decode_f32(packed: np.ndarray, scales: np.ndarray) -> np.ndarray:
     n, kh = packed.shape
     out = np.empty((n, kh * 2), dtype=np.float32)
     load().oracle_decode_f32(_ptr(packed), _ptr(scales), n, kh * 2, _ptr(out))
+    return out
+
+
+def decode_f64(packed: np.ndarray, scales: np.ndarray) -> np.ndarray:
+    """float64 decode, bit-identical to ``decode_f32(...).astype(float64)``; the ctypes call
+    releases the GIL, so threads decode experts in parallel."""
+    packed = np.ascontiguousarray(packed, dtype=np.uint8)
+    scales = np.ascontiguousarray(scales, dtype=np.uint8)
+    n, kh = packed.shape
+    if scales.shape != (n, kh * 2 // 32):
+        raise ValueError(f"scales shape {scales.shape} does not match packed {packed.shape}")
+    out = np.empty((n, kh * 2), dtype=np.float64)
+    load().oracle_decode_f64(_ptr(packed), _ptr(scales), n, kh * 2, _ptr(out))
     return out
 
 

@@ -6,11 +6,19 @@ here (the decode kernel rounds its fp32 row dots; the grouped path uses torch's 
 and the oracle rounds it the same way; a 1-ulp difference in a
 few elements of h (fp32 vs fp64 accumulation before the rounding) and the grouped MFMA
 path's ~1e-4 error set the bar of the grouped path (T > 8): normwise max-relative 5e-4 (its
-own bar), under the 1e-3 bar of the matvec gate.  The decode path (T <= 8) rounds h exactly as the oracle
-does and accumulates in fp32: 1e-5.  The router result is compared exactly (ids) and to 1e-5 (weights).
+own bar), under the 1e-3 bar of the matvec gate; at K3 shapes with all 896 experts distinct
+the grouped path reaches 6.6e-4 (the scaled MFMA sums each 128-element dot about 12 bits
+below its largest product, and SiTU's act carries about 12 bits in three E4M3 terms), so
+that case is held to the 1e-3 gate itself.  One token runs the fused decode kernels,
+which round h as the oracle does and accumulate in fp32: 1e-5.  Two to eight tokens run the
+multi-token decode (k3_moe_routed_decode, fp32 accumulation, 1e-7 on its own) on h from the
+BLAS GEMM, where more latent elements can land one bf16 ulp from the oracle's rounding
+(observed 2.6e-5 at K3 shapes and four tokens): 1e-4.  The router result is compared exactly
+(ids) and to 1e-5 (weights).
 """
 from __future__ import annotations
 
+import os
 from dataclasses import dataclass
 
 import numpy as np
@@ -24,6 +32,8 @@ pytestmark = pytest.mark.gpu
 DEV = "cuda"
 TOL_GROUPED = 5e-4
 TOL_DECODE = 1e-5
+TOL_MULTI = 1e-4
+TOL_GATE = 1e-3   # the matvec gate (normwise max-relative, fp32-accumulated)
 
 
 @dataclass
@@ -41,12 +51,41 @@ class K3Cfg:
     rms_norm_eps: float = 1e-5
 
 
-def make(seed, H, L, I, E, k, Is, distinct=None):
+class HostExperts:
+    """experts[e] for the oracle: the device expert's (packed, scales) pairs copied to host
+    memory on access, so only the experts the tokens select are ever copied."""
+
+    def __init__(self, ex_dev):
+        self.ex_dev = ex_dev
+
+    def __getitem__(self, e):
+        return tuple(tuple(a.cpu().numpy() for a in pair) for pair in self.ex_dev[e])
+
+
+def device_experts(E, L, I, seed):
+    """E distinct MXFP4 experts drawn on the device (scale bytes in [118, 130])."""
+    g = torch.Generator(device=DEV)
+    g.manual_seed(seed)
+
+    def mx(n, kk):
+        return (torch.randint(0, 256, (n, kk // 2), dtype=torch.uint8, device=DEV, generator=g),
+                torch.randint(118, 131, (n, kk // 32), dtype=torch.uint8, device=DEV, generator=g))
+
+    return [(mx(I, L), mx(I, L), mx(L, I)) for _ in range(E)]
+
+
+def make(seed, H, L, I, E, k, Is, distinct=None, on_device=False):
+    """Weights of one layer.  ``distinct`` weight sets behind the E table rows (all E by
+    default), drawn on the host; ``on_device`` draws all E experts distinct on the device
+    instead (full-size tables) and hands the oracle a copy-on-access mapping."""
     rng = np.random.default_rng(seed)
     D = distinct or E
-    experts_np = [(om.random_mxfp4(rng, I, L), om.random_mxfp4(rng, I, L), om.random_mxfp4(rng, L, I))
-                  for _ in range(D)]
-    experts_dev = [tuple(tuple(torch.from_numpy(a).to(DEV) for a in pair) for pair in ex) for ex in experts_np]
+    if on_device:
+        experts_dev = device_experts(E, L, I, seed)
+    else:
+        experts_np = [(om.random_mxfp4(rng, I, L), om.random_mxfp4(rng, I, L), om.random_mxfp4(rng, L, I))
+                      for _ in range(D)]
+        experts_dev = [tuple(tuple(torch.from_numpy(a).to(DEV) for a in pair) for pair in ex) for ex in experts_np]
     bf = lambda a: om.bf16_round(np.asarray(a, np.float32))  # noqa: E731
     router_w = bf(rng.standard_normal((E, H)) * 0.02)
     bias = (rng.standard_normal(E) * 0.05).astype(np.float32)
@@ -65,51 +104,60 @@ def make(seed, H, L, I, E, k, Is, distinct=None):
     def source(layer, e, which):
         return experts_dev[e % D][which_ix[which]]
 
-    oracle_args = (router_w, bias, down, up, norm_w, {e: experts_np[e % D] for e in range(E)}, shared)
+    oracle_experts = HostExperts(experts_dev) if on_device else {e: experts_np[e % D] for e in range(E)}
+    oracle_args = (router_w, bias, down, up, norm_w, oracle_experts, shared)
     return w, source, oracle_args
 
 
-def check(cfg, seed, T, distinct=None):
+def check(cfg, seed, T, distinct=None, on_device=False, tol=None):
     from k3hip.moe import LatentMoE
     w, source, (router_w, bias, down, up, norm_w, experts, shared) = make(
         seed, cfg.hidden_size, cfg.routed_expert_hidden_size, cfg.moe_intermediate_size, cfg.num_experts,
-        cfg.num_experts_per_token, 2 * cfg.moe_intermediate_size, distinct)
+        cfg.num_experts_per_token, 2 * cfg.moe_intermediate_size, distinct, on_device)
     moe = LatentMoE(cfg, 0, w, source)
     rng = np.random.default_rng(seed + 1)
     x = om.bf16_round(rng.standard_normal((T, cfg.hidden_size)).astype(np.float32))
     y, r = moe(torch.from_numpy(x).to(DEV).to(torch.bfloat16), return_router=True)
     want, idx, wts = omoe.latent_moe(x, router_w, bias, down, up, norm_w, experts, shared,
                                      cfg.num_experts_per_token, cfg.moe_renormalize, cfg.routed_scaling_factor,
-                                     cfg.situ_beta, cfg.situ_linear_beta, cfg.rms_norm_eps, h_bf16=True)
+                                     cfg.situ_beta, cfg.situ_linear_beta, cfg.rms_norm_eps, h_bf16=True,
+                                     workers=max(1, min(16, len(os.sched_getaffinity(0)))) if on_device else 1)
     assert np.array_equal(r.expert_indices.cpu().numpy(), idx)
     assert np.allclose(r.expert_weights.cpu().numpy(), wts, rtol=1e-5, atol=1e-7)
     rel = om.normwise_rel(y.float().cpu().numpy(), want)
-    print(f"T={T} E={cfg.num_experts} k={cfg.num_experts_per_token} rel={rel:.2e}")
-    assert rel <= (TOL_DECODE if T <= moe.DECODE_TOKENS else TOL_GROUPED), rel
+    print(f"T={T} E={cfg.num_experts} k={cfg.num_experts_per_token} distinct experts used "
+          f"{len(set(idx.ravel().tolist()))} rel={rel:.2e}")
+    if tol is None:
+        tol = TOL_DECODE if T == 1 else TOL_MULTI if T <= moe.DECODE_TOKENS else TOL_GROUPED
+    per_tok = [om.normwise_rel(y.float().cpu().numpy()[t], want[t]) for t in range(T)]
+    print("per-token rel: " + " ".join(f"{v:.1e}" for v in per_tok))
+    assert rel <= tol, rel
 
 
 @pytest.mark.parametrize("T", [1, 5, 12])
 def test_latent_moe_small(T):
-    """T <= 8: the fused decode (k3_moe_latent_layer_decode) per token; T = 12: the
-    grouped path."""
+    """T = 1: the fused decode (k3_moe_latent_layer_decode); T = 5: the multi-token decode
+    (k3_moe_routed_decode); T = 12: the grouped path."""
     check(K3Cfg(hidden_size=256, routed_expert_hidden_size=128, moe_intermediate_size=128, num_experts=16,
                 num_experts_per_token=4), seed=40 + T, T=T)
 
 
+K3_CFG = dict(hidden_size=7168, routed_expert_hidden_size=3584, moe_intermediate_size=3072, num_experts=896,
+              num_experts_per_token=16)
+
+
 def test_latent_moe_k3_shapes_decode():
     """K3's routed layer shapes: hidden 7168, latent 3584, experts [3072 x 3584], top-16 of
-    896 (four distinct expert weight sets behind the 896 table rows), two shared experts
-    (one MLP of width 6144); one decode token."""
-    check(K3Cfg(hidden_size=7168, routed_expert_hidden_size=3584, moe_intermediate_size=3072, num_experts=896,
-                num_experts_per_token=16), seed=50, T=1, distinct=4)
+    896, all 896 experts distinct (15.7 GB drawn on the device), two shared experts (one MLP
+    of width 6144); one decode token."""
+    check(K3Cfg(**K3_CFG), seed=50, T=1, on_device=True)
 
 
 def test_latent_moe_k3_shapes_grouped():
     """The same K3 shapes with 16 tokens: more than DECODE_TOKENS, so the grouped path runs
-    (batched routing, latent down GEMM, k3_moe_grouped_ffn over 896 table rows aliasing
-    eight distinct weight sets, norm, up and shared GEMMs)."""
-    check(K3Cfg(hidden_size=7168, routed_expert_hidden_size=3584, moe_intermediate_size=3072, num_experts=896,
-                num_experts_per_token=16), seed=51, T=16, distinct=8)
+    (batched routing, latent down GEMM, k3_moe_grouped_ffn over 896 distinct experts, norm,
+    up and shared GEMMs); 256 (token, slot) pairs each reach their own expert's weights."""
+    check(K3Cfg(**K3_CFG), seed=51, T=16, on_device=True, tol=TOL_GATE)
 
 
 def test_latent_moe_rejects_wrong_projection_shapes():

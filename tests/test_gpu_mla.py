@@ -70,6 +70,22 @@ def test_mla_decode_matches_oracle(H, T):
     assert rel <= 1e-4, f"hi/lo MFMA path should be near fp32: {rel:.3e}"
 
 
+@pytest.mark.parametrize("nope,v", [(128, 72), (128, 256), (128, 1024), (64, 128), (256, 128), (64, 200)])
+def test_mla_decode_other_head_dims(nope, v):
+    """q_nope widths other than 128 (W_UK rows of 64 and 256) and v_head_dim other than 128:
+    v not a multiple of 16 (72, 200), and v past the merge's first batch of 128 W_UV rows
+    (256, 1024), which reloads W_UV in further batches."""
+    H, T = 16, 300
+    args = make(2000 + nope + v, H, T, nope=nope, v=v)
+    scale = (nope + 64) ** -0.5
+    got = run(*args, scale)
+    want = omla.mla_decode_absorbed(*args, scale)[0]
+    rel = om.normwise_rel(got, want)
+    print(f"nope={nope} v={v} rel={rel:.3e}")
+    assert got.shape == (H, v)
+    assert rel <= 1e-4, rel
+
+
 def test_mla_decode_full_size_config():
     """64 heads, 32768 cached tokens, kv_lora_rank 512 + rope 64, scale 1/sqrt(192)."""
     args = make(1005, 64, 32768)
@@ -78,6 +94,67 @@ def test_mla_decode_full_size_config():
     rel = om.normwise_rel(got, want)
     print(f"full size rel={rel:.3e}")
     assert rel <= TOL
+    assert rel <= 1e-4, f"hi/lo MFMA path should be near fp32: {rel:.3e}"
+
+
+def make_f32(seed, H, T):
+    """As make(), with an fp32 cache whose values are not bf16 values (N(0,1) in fp32)."""
+    q_nope, q_rot, w_uk, w_uv, _, _ = make(seed, H, 1)
+    rng = np.random.default_rng(seed + 1)
+    lat = rng.standard_normal((T, 512)).astype(np.float32)
+    rot = rng.standard_normal((T, 64)).astype(np.float32)
+    return q_nope, q_rot, w_uk, w_uv, lat, rot
+
+
+def run_f32(q_nope, q_rot, w_uk, w_uv, lat, rot, scale, cap=None, qdtype=torch.bfloat16):
+    """The core on an fp32 cache (k3_mla_decode_absorbed_f32), optionally inside a larger
+    backing buffer."""
+    from k3hip.mla import mla_decode_absorbed
+    T = lat.shape[0]
+    if cap:
+        lb = torch.zeros(cap, 512, dtype=torch.float32, device=DEV)
+        rb = torch.zeros(cap, 64, dtype=torch.float32, device=DEV)
+        lb[:T] = to_dev(lat, torch.float32)
+        rb[:T] = to_dev(rot, torch.float32)
+        ld, rd = lb[:T], rb[:T]
+    else:
+        ld, rd = to_dev(lat, torch.float32), to_dev(rot, torch.float32)
+    out = mla_decode_absorbed(to_dev(q_nope, qdtype), to_dev(q_rot, qdtype), to_dev(w_uk), to_dev(w_uv), ld, rd,
+                              scale)
+    torch.cuda.synchronize()
+    return out.float().cpu().numpy()
+
+
+@pytest.mark.parametrize("H,T", [(32, 1), (32, 17), (32, 33), (64, 257), (8, 48), (96, 777), (16, 4321)])
+def test_mla_decode_f32_cache_matches_oracle(H, T):
+    """The reference's default fp32 cache: rows split into hi/lo bf16 planes as they are
+    staged, all four products kept: within 1e-5 of the fp64 oracle on the fp32 values."""
+    args = make_f32(3000 + H + T, H, T)
+    scale = 192 ** -0.5
+    got = run_f32(*args, scale)
+    want = omla.mla_decode_absorbed(*args, scale)[0]
+    rel = om.normwise_rel(got, want)
+    print(f"fp32 cache H={H} T={T} rel={rel:.3e}")
+    assert rel <= 1e-5, rel
+
+
+def test_mla_decode_f32_cache_full_size_strided_fp32_query():
+    """64 heads over 32768 fp32 cache rows inside a larger backing buffer (capacity 33024,
+    as MLACache grows), fp32 queries: within 1e-5 of fp64; the bf16 core on the bf16
+    rounding of the same cache differs from it by the cache rounding only."""
+    args = make_f32(3005, 64, 32768)
+    scale = 192 ** -0.5
+    got = run_f32(*args, scale, cap=33024, qdtype=torch.float32)
+    q_nope, q_rot, w_uk, w_uv, lat, rot = args
+    want = omla.mla_decode_absorbed(*args, scale)[0]
+    rel = om.normwise_rel(got, want)
+    print(f"fp32 cache full size rel={rel:.3e}")
+    assert rel <= 1e-5, rel
+    lat16, rot16 = bf(lat), bf(rot)
+    got16 = run(q_nope, q_rot, w_uk, w_uv, lat16, rot16, scale, qdtype=torch.float32)
+    want16 = omla.mla_decode_absorbed(q_nope, q_rot, w_uk, w_uv, lat16, rot16, scale)[0]
+    assert om.normwise_rel(got16, want16) <= 1e-4
+    assert om.normwise_rel(got, got16) > 10 * rel   # the fp32 rows did not go through bf16
 
 
 def test_mla_decode_strided_cache_and_fp32_query_and_bf16_out():
@@ -140,7 +217,9 @@ def test_mla_decode_errors():
     with pytest.raises(ValueError):
         mla_decode_absorbed(q, qr, wk, wv, lat, rot[:9], 0.1)                # T mismatch
     with pytest.raises(TypeError):
-        mla_decode_absorbed(q, qr, wk, wv, lat.float(), rot.float(), 0.1)    # fp32 cache
+        mla_decode_absorbed(q, qr, wk, wv, lat.half(), rot.half(), 0.1)      # fp16 cache
+    with pytest.raises(TypeError):
+        mla_decode_absorbed(q, qr, wk, wv, lat.float(), rot, 0.1)            # mixed cache dtypes
     with pytest.raises(ValueError):
         mla_decode_absorbed(q, qr, wk[:, :, :256], wv[:, :, :256], lat[:, :256], rot, 0.1)  # r != 512
 
@@ -158,6 +237,7 @@ class Cfg:
     v_head_dim: int = 128
     rms_norm_eps: float = 1e-5
     mla_use_output_gate: bool = True
+    mla_cache_dtype: torch.dtype = torch.bfloat16
 
     @property
     def q_head_dim(self):
@@ -209,6 +289,47 @@ def test_mla_layer_incremental_decode_matches_one_shot_oracle():
     assert om.normwise_rel(inc[prefill:], full[prefill:]) <= 2e-2
     assert cache.bytes_per_token() == (512 + 64) * 2
     assert cache.nbytes_used() == T * (512 + 64) * 2
+
+
+def test_mla_layer_fp32_cache_decode_runs_hip_core():
+    """The reference's default fp32 cache with the checkpoint's bf16 kv_b: a decode token
+    runs the HIP core on the fp32 rows (k3_mla_decode_absorbed_f32); prefill, then
+    single-token steps, each against the fp64 expanded one-shot layer
+    (k3ref/layers.py:152-185) within 1e-5."""
+    from k3hip import mla as kmla
+    cfg = Cfg(mla_cache_dtype=torch.float32)
+    rng = np.random.default_rng(23)
+    w32 = omla.random_mla_weights(rng, cfg)
+    w32["kv_b_proj.weight"] = bf(w32["kv_b_proj.weight"])
+    wdev = {k: torch.from_numpy(v).to(DEV) for k, v in w32.items()}
+    wdev["kv_b_proj.weight"] = wdev["kv_b_proj.weight"].to(torch.bfloat16)
+    attn = kmla.MLAAttention(cfg, wdev)
+    calls = []
+    core = kmla.mla_decode_absorbed
+
+    def counting(*a, **k):
+        calls.append(a[4].dtype)
+        return core(*a, **k)
+
+    kmla.mla_decode_absorbed = counting
+    try:
+        T, prefill = 300, 290
+        x = (rng.standard_normal((1, T, cfg.hidden_size)) * 0.5).astype(np.float32)
+        xd = torch.from_numpy(x).to(DEV)
+        out, cache = attn(xd[:, :prefill])
+        steps = [out.cpu().numpy()]
+        for t in range(prefill, T):
+            o, cache = attn(xd[:, t:t + 1], cache=cache)
+            steps.append(o.cpu().numpy())
+    finally:
+        kmla.mla_decode_absorbed = core
+    assert calls == [torch.float32] * (T - prefill)           # every decode step ran the fp32 core
+    assert cache.latent.dtype == torch.float32 and cache.length == T and cache.capacity == 512
+    got = np.concatenate(steps, axis=1)[0]
+    want = omla.mla_layer_expanded(cfg, {k: v.astype(np.float64) for k, v in w32.items()}, x)[0]
+    rel = om.normwise_rel(got[prefill:], want[prefill:])
+    print(f"fp32 cache decode steps rel {rel:.2e}")
+    assert rel <= 1e-5
 
 
 def test_mla_fused_decode_step_matches_torch_step_and_oracle():
@@ -315,10 +436,14 @@ def test_mla_fused_decode_step_fp32_input_and_bf16_output():
     assert om.normwise_rel(outs[1], outs[0]) <= 2 ** -8
 
 
-@pytest.mark.parametrize("hidden,heads,q_lora,gate", [(1024, 16, 512, False), (768, 4, 1536, True)])
+@pytest.mark.parametrize("hidden,heads,q_lora,gate", [(1024, 16, 512, False), (768, 4, 1536, True),
+                                                      (9216, 80, 512, True)])
 def test_mla_fused_decode_step_other_shapes(hidden, heads, q_lora, gate):
     """Other head counts, q_lora ranks and no output gate: the fused step against the
-    fp64 restatement on the latents it stored, nine tokens from an empty cache."""
+    fp64 restatement on the latents it stored, nine tokens from an empty cache.  Hidden 9216
+    with 80 heads sends the x rows (q_a, kv_a, g_proj over 9216 values) and the o_proj rows
+    (over 80 x 128 = 10240 values) through the dense row kernel's widest per-block form
+    (rows of 8193..12288 values, two rows per wave)."""
     from k3hip.mla import MLAAttention
     cfg = Cfg(hidden_size=hidden, num_attention_heads=heads, q_lora_rank=q_lora, mla_use_output_gate=gate)
     rng = np.random.default_rng(hidden + heads)

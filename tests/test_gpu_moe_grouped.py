@@ -8,6 +8,8 @@ path is expected within 5e-4 (observed 2.5e-5 .. 1.4e-4 on these cases).
 """
 from __future__ import annotations
 
+import os
+
 import numpy as np
 import pytest
 import torch
@@ -97,33 +99,45 @@ def test_grouped_matches_oracle(T, H, I, E, k, D, routing, act):
     assert rel <= PATH_TOL, f"scaled-MFMA path above its expected error level: {rel:.3e}"
 
 
-def sampled_oracle(x32, idx, w, ex_np, sample, act="silu", beta=1.0, lbeta=None):
-    """fp64 routed outputs of the sampled tokens: each distinct weight set is decoded and
-    widened once and takes all the sampled (token, slot) pairs routed to it in one product."""
-    D = len(ex_np)
-    T, k = idx.shape
-    H = x32.shape[1]
-    want = np.zeros((len(sample), H))
-    pairs = [(r, j, int(idx[t, j]) % D) for r, t in enumerate(sample) for j in range(k)]
-    for d in sorted({p[2] for p in pairs}):
-        mine = [(r, j) for r, j, dd in pairs if dd == d]
-        xs = np.stack([x32[sample[r]] for r, _ in mine]).astype(np.float64)
-        wg, wu, wd = (om.decode_mxfp4(*pair).astype(np.float64) for pair in ex_np[d])
-        y = omoe.dense_ffn(xs, wg, wu, wd, act, beta, lbeta)[0]
-        for (r, j), yy in zip(mine, y):
-            want[r] += w[sample[r], j] * yy
-    return want
+def device_experts(E, H, I, seed):
+    """E distinct MXFP4 experts drawn on the device (scale bytes in [118, 130], as the
+    benchmark's generator), so no two table rows alias one weight set."""
+    g = torch.Generator(device=DEV)
+    g.manual_seed(seed)
+
+    def mx(n, kk):
+        return (torch.randint(0, 256, (n, kk // 2), dtype=torch.uint8, device=DEV, generator=g),
+                torch.randint(118, 131, (n, kk // 32), dtype=torch.uint8, device=DEV, generator=g))
+
+    return [(mx(I, H), mx(I, H), mx(H, I)) for _ in range(E)]
 
 
-def test_grouped_full_shape_sampled_tokens_and_determinism():
-    """2048 tokens x top-8 over 384 experts (16 distinct weight sets aliased), Zipf(1.1)
-    load, hidden 7168, intermediate 2048: 60 tokens against the oracle -- every 64-token tile
-    boundary of the hottest expert (first and last token of each of its tiles, in the grouped
-    order, which is token order), tokens routed to the coldest experts (single partly filled
-    tiles), the first and last tokens and a random draw -- and two runs bit-identical."""
-    T, H, I, E, k, D = 2048, 7168, 2048, 384, 8, 16
+class HostExperts:
+    """experts[e] for the oracle: the device expert's (packed, scales) pairs copied to host
+    memory on access (only the experts the sampled tokens use are ever copied)."""
+
+    def __init__(self, ex_dev):
+        self.ex_dev = ex_dev
+
+    def __getitem__(self, e):
+        return tuple(tuple(a.cpu().numpy() for a in pair) for pair in self.ex_dev[e])
+
+
+def oracle_workers():
+    return max(1, min(16, len(os.sched_getaffinity(0))))
+
+
+def test_grouped_full_shape_every_expert_distinct():
+    """2048 tokens x top-8 over 384 distinct experts (9 GB of weights drawn on the device),
+    Zipf(1.1) load, hidden 7168, intermediate 2048.  At least 320 tokens against the fp64
+    oracle: the first and last token of every 64-token tile of the four hottest experts (in
+    the grouped order, which is token order), the token of every expert routed exactly
+    once, the first and last tokens, and a random draw; two runs bit-identical.  Every
+    (token, slot) pair of the sample reaches its own expert's weights, so a wrong
+    expert-to-weight mapping fails."""
+    T, H, I, E, k = 2048, 7168, 2048, 384, 8
+    ex_dev = device_experts(E, H, I, seed=1004)
     rng = np.random.default_rng(1004)
-    ex_np, ex_dev = make_experts(rng, D, H, I)
     idx, w = zipf_routing(rng, T, E, k)
     x32 = om.bf16_round(rng.standard_normal((T, H)).astype(np.float32))
     counts = np.bincount(idx.ravel(), minlength=E)
@@ -131,18 +145,20 @@ def test_grouped_full_shape_sampled_tokens_and_determinism():
     got = run(x32, idx, w, ex_dev, E, I)
     again = run(x32, idx, w, ex_dev, E, I)
     assert np.array_equal(got, again)
-    hot = int(np.argmax(counts))
-    hot_tokens = np.nonzero((idx == hot).any(axis=1))[0]        # grouped rows of the hot expert, in order
-    edges = sorted({int(hot_tokens[m]) for m0 in range(0, len(hot_tokens), 64)
-                    for m in (m0, min(m0 + 63, len(hot_tokens) - 1))})
-    cold = [e for e in np.argsort(counts) if counts[e] > 0][:8]
-    cold_tokens = [int(np.nonzero((idx == e).any(axis=1))[0][0]) for e in cold]
-    sample = sorted(set(edges[:40] + cold_tokens + [0, 1, T - 2, T - 1]
-                        + [int(t) for t in rng.choice(T, 8, replace=False)]))
-    want = sampled_oracle(x32, idx, w, ex_np, sample)
+    edges = set()
+    for hot in np.argsort(-counts, kind="stable")[:4]:
+        toks = np.nonzero((idx == hot).any(axis=1))[0]        # grouped rows of the expert, in order
+        edges |= {int(toks[m]) for m0 in range(0, len(toks), 64) for m in (m0, min(m0 + 63, len(toks) - 1))}
+    singles = {int(np.nonzero((idx == e).any(axis=1))[0][0]) for e in np.nonzero(counts == 1)[0]}
+    sample = edges | singles | {0, 1, T - 2, T - 1}
+    rest = np.setdiff1d(np.arange(T), sorted(sample))
+    sample = sorted(sample | {int(t) for t in rng.choice(rest, max(0, 320 - len(sample)), replace=False)})
+    want = omoe.moe_layer(x32[sample], idx[sample], w[sample], HostExperts(ex_dev), workers=oracle_workers())
     rel = om.normwise_rel(got[sample], want)
-    print(f"full shape: {len(sample)} sampled tokens, rel={rel:.3e}")
-    assert len(sample) >= 50
+    used = len(set(idx[sample].ravel().tolist()))
+    print(f"full shape: {len(sample)} sampled tokens ({len(edges)} hot-tile edges, {len(singles)} single-token "
+          f"experts) over {used} distinct experts, rel={rel:.3e}")
+    assert len(sample) >= 320 and used > 280
     assert rel <= TOL
     assert rel <= PATH_TOL
 

@@ -226,3 +226,43 @@ def test_layer_counter_bytes_garbage():
     moe(x)
     assert int(ctr[0]) == 0
     assert om.normwise_rel(moe(x).cpu().numpy(), want) < 2e-5
+
+
+@pytest.mark.parametrize("router", ["softmax", "sigmoid_bias"])
+def test_route_only_with_garbage_counter(router):
+    """k3_moe_route (router + top-k only) on a workspace whose router arrival counter holds
+    garbage: the call resets the counter itself, so its first call already writes the
+    oracle's selection and weights, and it leaves the counter at zero."""
+    import ctypes
+
+    from k3hip import _lib
+    from k3hip import _torch as T
+    H, E, k = 2048, 64, 6
+    rng = np.random.default_rng(31 + len(router))
+    router_w = om.bf16_round((rng.standard_normal((E, H)) * 0.02).astype(np.float32))
+    bias = (rng.standard_normal(E) * 0.05).astype(np.float32)
+    kind = _lib.K3_ROUTE_SOFTMAX if router == "softmax" else _lib.K3_ROUTE_SIGMOID_BIAS
+    rw = torch.from_numpy(router_w).to(DEV).to(torch.bfloat16)
+    bd = torch.from_numpy(bias).to(DEV) if router == "sigmoid_bias" else None
+    nbytes = int(_lib.lib().k3_moe_layer_workspace_size(H, 128, 0, E, k))
+    ws = torch.zeros(nbytes, dtype=torch.uint8, device=DEV)
+    off = (ctypes.c_int64 * 8)()
+    _lib.call("k3_moe_layer_workspace_offsets", H, 128, 0, E, k, off)
+    for garbage in (0x5A5A5A5A, 3, 0):
+        x32 = om.bf16_round(rng.standard_normal((1, H)).astype(np.float32))
+        x = torch.from_numpy(x32).to(DEV).to(torch.bfloat16)
+        ws[:4].view(torch.int32).fill_(garbage)
+        _lib.call("k3_moe_route", T.ptr(x), _lib.K3_BF16, T.ptr(rw), T.ptr(bd), kind, 1, 2.5, H, E, k,
+                  T.ptr(ws), ws.numel(), T.stream(x))
+        torch.cuda.synchronize()
+        if router == "softmax":
+            idx, wts, raw, _ = omoe.route_softmax(x32, router_w, k, True, 2.5)
+        else:
+            idx, wts, raw, corr = omoe.route_sigmoid_bias(x32, router_w, bias, k, True, 2.5)
+        got_idx = ws[off[3]:off[3] + 4 * k].view(torch.int32).cpu().numpy()
+        got_w = ws[off[4]:off[4] + 4 * k].view(torch.float32).cpu().numpy()
+        got_raw = ws[off[1]:off[1] + 4 * E].view(torch.float32).cpu().numpy()
+        assert np.array_equal(got_idx, idx[0]), (garbage, got_idx, idx[0])
+        assert np.allclose(got_w, wts[0], rtol=1e-5, atol=1e-7)
+        assert np.allclose(got_raw, raw[0], rtol=1e-4, atol=1e-7)
+        assert int(ws[:4].view(torch.int32).item()) == 0

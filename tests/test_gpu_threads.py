@@ -62,7 +62,12 @@ def test_threads_on_their_own_streams_match_one_thread():
         # different K each time, so each message must name the K of its own call
         from k3hip import _lib
         from k3hip import _torch as T
-        x0, (p0, s0) = xs[0], experts[0][0]
+        # buffers sized for the largest K passed, so a regression in the library's own
+        # validation shows up as a missing error rather than as reads past an allocation
+        kmax = H + 16 + 32 * (rounds - 1)
+        x0 = torch.zeros((1, kmax), dtype=torch.bfloat16, device=DEV)
+        p0 = torch.zeros((I, kmax // 2), dtype=torch.uint8, device=DEV)
+        s0 = torch.full((I, -(-kmax // 32)), 127, dtype=torch.uint8, device=DEV)
         out = torch.empty((1, I), dtype=torch.float32, device=DEV)
         start.wait()
         for i in range(rounds):

@@ -110,6 +110,28 @@ def test_numpy_oracle_matches_c_restatement():
     assert np.array_equal(a.view(np.uint32)[~nan], b.view(np.uint32)[~nan])
 
 
+def test_f64_decode_is_the_widened_f32_decode():
+    """The full-size oracles' float64 decode (C per-group table form) against the NumPy
+    decode widened: every (code, scale byte) pair, with NaN from byte 255 x code 0/8, and a
+    random tensor over every scale byte."""
+    native.build(force=False)
+    codes = np.arange(16, dtype=np.uint8)
+    packed = np.zeros((256, 16), dtype=np.uint8)
+    packed[:, :8] = (codes[0::2] | (codes[1::2] << 4))[None, :]
+    scales = np.arange(256, dtype=np.uint8).reshape(256, 1)
+    rng = np.random.default_rng(124)
+    cases = [(packed, scales),
+             (rng.integers(0, 256, size=(64, 512), dtype=np.uint8), rng.integers(0, 256, size=(64, 32), dtype=np.uint8))]
+    for p, s in cases:
+        a = om.decode_mxfp4(p, s).astype(np.float64)
+        b = om.decode_mxfp4_f64(p, s)
+        assert b.dtype == np.float64
+        nan = np.isnan(a)
+        assert np.array_equal(nan, np.isnan(b))
+        assert np.array_equal(a.view(np.uint64)[~nan], b.view(np.uint64)[~nan])
+    assert np.isinf(om.decode_mxfp4_f64(packed, scales)[255, 1])   # code 1 at byte 255
+
+
 def test_matvec_onehot_returns_decoded_columns():
     rng = np.random.default_rng(5)
     packed, scales = om.random_mxfp4(rng, 48, 256)
