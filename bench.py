@@ -686,14 +686,34 @@ def bench_cpu(sample_s=12.0):
     return out
 
 
+def kernel_sources_sha256():
+    """sha256 over the kernel sources (csrc/*.hip, *.h, in name order): the identity of the
+    kernels a counter record was measured on."""
+    import hashlib
+    h = hashlib.sha256()
+    for f in sorted((ROOT / "kimi-k3-mlx-macmini_amd" / "csrc").glob("*")):
+        if f.suffix in (".hip", ".h"):
+            h.update(f.name.encode())
+            h.update(f.read_bytes())
+    return h.hexdigest()
+
+
+COUNTERS_CURRENT = None   # set by counters_from_profiles: the record matches today's kernel sources
+
+
 def counters_from_profiles():
     """Per-workload counter figures (rocprofv3 FETCH_SIZE / WRITE_SIZE / MFMA counts over the
-    same workloads, calibrated bytes, kernel times) from the committed profiles/counters.json."""
+    same workloads, calibrated bytes, kernel times) from the committed profiles/counters.json,
+    with whether its kernel-source hash matches the sources of this run (the fields say
+    "stale" when it does not)."""
+    global COUNTERS_CURRENT
     f = ROOT / "profiles" / "counters.json"
     try:
-        return json.loads(f.read_text()).get("workloads", {})
+        d = json.loads(f.read_text())
     except (ValueError, OSError):
         return {}
+    COUNTERS_CURRENT = d.get("csrc_sha256") == kernel_sources_sha256()
+    return d.get("workloads", {})
 
 
 def counter_fields(rec):
@@ -701,14 +721,17 @@ def counter_fields(rec):
     `mfma_util`, from one profiles/counters.json record."""
     if not rec:
         return {}
+    src = "profiles/counters.json" + ("" if COUNTERS_CURRENT else " (stale: measured on other kernel sources)")
     out = {"traffic": {"ratio": rec["traffic_ratio"], "counter_bytes": rec["counter_bytes"],
-                       "algorithmic_bytes": rec["algorithmic_bytes"], "source": "profiles/counters.json"}}
+                       "algorithmic_bytes": rec["algorithmic_bytes"], "source": src,
+                       "current": bool(COUNTERS_CURRENT)}}
     m = rec.get("mfma")
     if m:
         u = {"mfma": m["type"], "executed_TFLOP/s": m["executed_TFLOP/s"],
              "frac_of_issue_peak": m["executed_frac_of_issue_peak"], "issue_peak_TFLOP/s": m["issue_peak_TFLOP/s"]}
         if "useful_frac_of_mxfp4_peak" in m:
             u["useful_frac_of_mxfp4_peak"] = m["useful_frac_of_mxfp4_peak"]
+        u["current"] = bool(COUNTERS_CURRENT)
         out["mfma_util"] = u
     return out
 
@@ -765,7 +788,7 @@ def main():
         "pct_hbm_peak": round(100 * gbs / HBM_PEAK_GBS, 1),
         "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(gbs / HBM_PEAK_GBS, 4),
-                     "traffic": cnt.get("expert_swiglu_ffn_b1", {}).get("counter_bytes"),
+                     "traffic": cnt.get("expert_swiglu_ffn_b1", {}).get("counter_bytes") if COUNTERS_CURRENT else None,
                      "kernel": "expert FFN step: expert_gateup_kernel then gemv_kernel (down)",
                      "launches_per_step": 2, "bytes_per_step": EXPERT_BYTES,
                      "avg_step_us": round(per_step * 1e6, 3)},

@@ -25,14 +25,26 @@ from .mxfp4 import bf16_round, decode_mxfp4, random_mxfp4
 
 
 def _cpu_model() -> str:
+    """The host CPU's model name as /proc/cpuinfo and lscpu give it (lscpu's BIOS model name
+    added when it says more, e.g. on virtual machines that report a generic family name)."""
+    names = []
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.lower().startswith("model name"):
+                    names.append(line.split(":", 1)[1].strip())
+                    break
+    except OSError:
+        pass
     try:
         out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
         for line in out.splitlines():
-            if line.lower().startswith("model name"):
-                return line.split(":", 1)[1].strip()
+            key, _, val = line.partition(":")
+            if key.strip().lower() in ("model name", "bios model name") and val.strip() and val.strip() not in names:
+                names.append(val.strip())
     except (OSError, subprocess.SubprocessError):
         pass
-    return platform.processor() or "unknown"
+    return " / ".join(names) or platform.processor() or "unknown"
 
 
 def time_expert(H: int, I: int, sample_s: float = 12.0, threads: int | None = None, seed: int = 1002) -> dict:
