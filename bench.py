@@ -298,6 +298,7 @@ K3_LAYER_BYTES = (K3_E * K3_H * 2 + 2 * K3_L * K3_H * 2 + K3_K * 3 * proj_bytes(
                   + 3 * K3_IS * K3_H * 2)                                 # 660,602,880
 K3_PF_T = 2048
 K3_PREFILL = True
+K3_MULTI = True
 
 
 def bench_k3_layer(torch, steps, warmup, dev):
@@ -336,6 +337,31 @@ def bench_k3_layer(torch, steps, warmup, dev):
     touched = set()
     for i in range(min(steps, 32)):
         touched.update(moe.route(xs[i:i + 1]).expert_indices.view(-1).tolist())
+    multi = None
+    if K3_MULTI:
+        # four decode tokens per step through k3_moe_latent_layer_decode_multi (each expert
+        # any of them selects read once), against four single-token steps
+        import numpy as np
+        ms = min(steps, 64)
+        x4 = rn((ms + warmup + 3) * MULTI_T, K3_H).to(bf)
+
+        def mstep(i):
+            moe(x4[i * MULTI_T:(i + 1) * MULTI_T])
+
+        msec, _ = graph_time(torch, mstep, ms, min(warmup, 8))
+        unions = [len(set(moe.route(x4[i * MULTI_T:(i + 1) * MULTI_T]).expert_indices.view(-1).tolist()))
+                  for i in range(ms)]
+        u = float(np.mean(unions))
+        mbytes = (K3_E * K3_H * 2 + 2 * K3_L * K3_H * 2 + u * 3 * proj_bytes(K3_I, K3_L) + 3 * K3_IS * K3_H * 2)
+        mus = msec / ms * 1e6
+        multi = {"tokens_per_step": MULTI_T, "us_per_step": round(mus, 2), "us_per_token": round(mus / MULTI_T, 2),
+                 "union_experts_mean": round(u, 2), "bytes_per_step_mean": int(mbytes),
+                 "GB/s": round(mbytes / (mus * 1e-6) / 1e9, 1),
+                 "pct_hbm_peak": round(100 * mbytes / (mus * 1e-6) / 1e9 / HBM_PEAK_GBS, 1),
+                 "vs_4_single_token_steps": round(MULTI_T * sec / steps * 1e6 / mus, 3),
+                 "what": "LatentMoE.__call__ on 4 tokens: k3_moe_latent_layer_decode_multi (router, latent "
+                         "down, shared and up rows for T tokens in HIP; each selected expert read once)"}
+        del x4
     prefill = None
     if K3_PREFILL:
         # K3 prefill: 2048 tokens through the same layer, routing included (one router GEMM
@@ -361,7 +387,7 @@ def bench_k3_layer(torch, steps, warmup, dev):
                            "GEMM, k3_moe_grouped_ffn, RMSNorm, up GEMM, shared-expert GEMMs"}
         del xp
     del moe, experts, w
-    return sec, len(touched), stats, prefill
+    return sec, len(touched), stats, prefill, multi
 
 
 def bench_ingest(torch, dev, n_experts=32):
@@ -829,7 +855,7 @@ def main():
             line["moe_layer_t4"]["vs_4_single_token_layers"] = round(4 * line["moe_layer"]["us_per_layer"] / mus4, 3)
     if "k3layer" in work:
         ks = min(K, 256)
-        ksec, ktouched, kstats, kpre = bench_k3_layer(torch, ks, min(W, 32), dev)
+        ksec, ktouched, kstats, kpre, kmulti = bench_k3_layer(torch, ks, min(W, 32), dev)
         kus = ksec / ks * 1e6
         kgbs = K3_LAYER_BYTES / (kus * 1e-6) / 1e9
         line["k3_latent_layer"] = {"us_per_token": round(kus, 2), "GB/s": round(kgbs, 1),
@@ -839,6 +865,7 @@ def main():
                                    "shared_intermediate": K3_IS, "router": "sigmoid + bias",
                                    "act": "situ", "distinct_experts_routed_first32": ktouched,
                                    "launches_per_token": 4, "step_us": kstats, "prefill": kpre,
+                                   "four_tokens": kmulti,
                                    **counter_fields(cnt.get("k3_latent_layer_b1"))}
         if kpre is not None:
             kpre.update({"grouped_experts_" + k_: v_ for k_, v_ in

@@ -241,6 +241,36 @@ int k3_moe_layer_decode_multi(const void *x, int x_dtype, const void *router_w, 
                               int64_t n_experts, int64_t top_k, int act_kind, float beta, float linear_beta,
                               void *workspace, int64_t workspace_bytes, void *stream);
 
+/* Workspace bytes for k3_moe_latent_layer_decode_multi (the T-token records of
+ * k3_moe_layer_decode_multi with the routed part at the latent width, plus the latent state
+ * and routed sum [T, latent]).  No initialisation. */
+int64_t k3_moe_latent_layer_multi_workspace_size(int64_t T, int64_t H, int64_t latent, int64_t I,
+                                                 int64_t shared_I, int64_t n_experts, int64_t top_k);
+
+/* Byte offsets of k3_moe_latent_layer_decode_multi's router records, in the order of
+ * k3_moe_layer_multi_workspace_offsets. */
+int k3_moe_latent_layer_multi_workspace_offsets(int64_t T, int64_t H, int64_t latent, int64_t I,
+                                                int64_t shared_I, int64_t n_experts, int64_t top_k,
+                                                int64_t *offsets);
+
+/* k3_moe_latent_layer_decode for T <= 8 decode tokens at once, x [T, H], out [T, H]: the
+ * router, latent down and shared gate/up rows against all T tokens in one launch, the batched
+ * sigmoid + bias top-k, the routed experts on h at the latent width as in
+ * k3_moe_routed_decode (every selected expert read once for all its tokens), the shared down
+ * rows, and the up projection rows against rmsnorm(routed sum) * latent_norm with the shared
+ * output added: seven stream-ordered launches, no host synchronisation.  Arguments as
+ * k3_moe_latent_layer_decode, plus T; shared_I a multiple of 128, <= 8192.
+ * Replaces LatentMoE.__call__ (air_llm/models/kimi_k3/moe.py:110-132) for a decode batch of T
+ * tokens, including the latent down/norm/up wrapper (moe.py:116,129-130). */
+int k3_moe_latent_layer_decode_multi(const void *x, int x_dtype, const void *router_w, const void *router_bias,
+                                     int renormalize, float scaling, const void *expert_table,
+                                     const void *latent_down, const void *latent_up, const void *latent_norm,
+                                     float eps, const void *shared_gate, const void *shared_up,
+                                     const void *shared_down, void *out, int out_dtype, int64_t T, int64_t H,
+                                     int64_t latent, int64_t I, int64_t shared_I, int64_t n_experts,
+                                     int64_t top_k, int act_kind, float beta, float linear_beta, void *workspace,
+                                     int64_t workspace_bytes, void *stream);
+
 /* Workspace bytes for k3_moe_latent_layer_decode: the k3_moe_layer_decode records plus the
  * bf16 latent state and the fp32 routed sum.  Same counter rule as k3_moe_layer_workspace_size
  * (first 4096 bytes zero before the first call; every call returns them to zero). */

@@ -340,20 +340,25 @@ __global__ __launch_bounds__(256, 2) void multi_down_kernel(MultiArgs a) {
 
 // ------------------------------------------------------------------ R: dense rows, T tokens
 // bf16 row sets [N, K] against T input rows [T, K] (bf16 or fp32) staged in LDS in plain
-// 16-byte chunk order, tb tokens at a time; 4 waves per block:
-//   section 0 (blocks [0, blocks0)): R rows per wave (1 for rows of more than 4096 values, up
-//                                    to 4 for rows of at most 2048), out0[t * ld0 + n] = W0[n] . in[t]
-//   section 1 (the next blocks):     one (gate, up) row pair per wave,
-//                                    act[t * ld1 + i] = f(G[i] . in[t], U[i] . in[t])
+// 16-byte chunk order, tb tokens at a time (fp32 rows optionally replaced by
+// rmsnorm(row) * nw as they are staged); 4 waves per block:
+//   plain sets s (blocks in set order): R rows per wave (1 for rows of more than 4096 values,
+//       up to 4 for rows of at most 2048), out_s[t * ld_s + n] = W_s[n] . in[t] (+ add_s[...]),
+//       fp32 or rounded to bf16
+//   the pair set (the last blocks): one (gate, up) row pair per wave,
+//       act[t * ld1 + i] = f(G[i] . in[t], U[i] . in[t])
 // Products are exact (bf16 x bf16 in v_dot2, bf16 x fp32 as fp32 FMAs), accumulation fp32.
+constexpr int kPlainSets = 2;
 struct MRowsArgs {
     const void *in;          // [T, K] rows
     int T, K, tb;
-    const uint16_t *w0;      // section 0 rows [N0, K]
-    int N0, blocks0;
-    float *out0;
-    int ld0;
-    const uint16_t *wg, *wu; // section 1 rows [N1, K] each
+    const float *nw;         // not null (fp32 input): stage rmsnorm(row) * nw instead of the row
+    float eps;
+    const uint16_t *w[kPlainSets];
+    int N[kPlainSets], blocks[kPlainSets], ld[kPlainSets], out_bf16[kPlainSets];
+    void *out[kPlainSets];
+    const float *add[kPlainSets];
+    const uint16_t *wg, *wu; // the pair set, rows [N1, K] each
     int N1;
     float *act;
     int ld1;
@@ -388,21 +393,23 @@ __device__ __forceinline__ float rdot(uint4 w, const float4 *x, int c, float acc
 }
 
 // IT: input element type (uint16_t = bf16, float); CH: 16-byte weight chunks per lane (K <= 512 CH);
-// R: section-0 rows per wave (narrow rows take several, so one staged batch serves more rows).
+// R: plain rows per wave (narrow rows take several, so one staged batch serves more rows).
 template <typename IT, int CH, int R>
 __global__ __launch_bounds__(256) void multi_rows_kernel(MRowsArgs a) {
     extern __shared__ uint4 xs[];  // [tb][K * sizeof(IT) / 16]
+    __shared__ float red[kRowWaves];
     using XC = typename std::conditional<std::is_same<IT, float>::value, float4, uint4>::type;
     constexpr int NR = R > 2 ? R : 2;  // weight rows held per wave (a pair needs two)
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
-    const bool pair = static_cast<int>(blockIdx.x) >= a.blocks0;  // uniform
-    const int nrows = pair ? 2 : R;                                // rows this wave reduces
-    const int n0 = pair ? (static_cast<int>(blockIdx.x) - a.blocks0) * kRowWaves + wave
-                        : (static_cast<int>(blockIdx.x) * kRowWaves + wave) * R;
-    const int N = pair ? a.N1 : a.N0;
+    int b = blockIdx.x, s = 0;
+    while (s < kPlainSets && b >= a.blocks[s]) b -= a.blocks[s++];
+    const bool pair = s == kPlainSets;  // uniform
+    const int nrows = pair ? 2 : R;    // rows this wave reduces
+    const int n0 = pair ? b * kRowWaves + wave : (b * kRowWaves + wave) * R;
+    const int N = pair ? a.N1 : a.N[s];
     const int nch = a.K >> 3;
     const uint32_t rowb = static_cast<uint32_t>(a.K) * 2u;
-    const auto rg = make_rsrc(pair ? a.wg : a.w0, static_cast<uint32_t>(N) * rowb);
+    const auto rg = make_rsrc(pair ? a.wg : a.w[s], static_cast<uint32_t>(N) * rowb);
     const auto ru = make_rsrc(a.wu, pair ? static_cast<uint32_t>(N) * rowb : 0u);
     uint4 w[NR][CH];
 #pragma unroll
@@ -425,6 +432,31 @@ __global__ __launch_bounds__(256) void multi_rows_kernel(MRowsArgs a) {
         if (c0 > 0) __syncthreads();  // every wave is done with the previous batch
         for (int i = threadIdx.x; i < nb * cpr; i += 64 * kRowWaves) xs[i] = in4[static_cast<int64_t>(c0) * cpr + i];
         __syncthreads();
+        if constexpr (std::is_same<IT, float>::value) {
+            if (a.nw) {
+                // KimiRMSNorm of each staged row: row * (1 / sqrt(mean(row^2) + eps)) * nw
+                float4 *x4 = reinterpret_cast<float4 *>(xs);
+                for (int c = 0; c < nb; ++c) {
+                    float ss = 0.f;
+                    for (int i = threadIdx.x; i < cpr; i += 64 * kRowWaves) {
+                        const float4 v = x4[c * cpr + i];
+                        ss = fmaf(v.x, v.x, fmaf(v.y, v.y, fmaf(v.z, v.z, fmaf(v.w, v.w, ss))));
+                    }
+                    ss = wave_sum_all(ss);
+                    if (lane == 0) red[wave] = ss;
+                    __syncthreads();
+                    const float tot = ((red[0] + red[1]) + red[2]) + red[3];
+                    const float rs = 1.0f / sqrtf(tot / static_cast<float>(a.K) + a.eps);
+                    for (int i = threadIdx.x; i < cpr; i += 64 * kRowWaves) {
+                        const float4 g = reinterpret_cast<const float4 *>(a.nw)[i];
+                        float4 v = x4[c * cpr + i];
+                        v.x = v.x * rs * g.x, v.y = v.y * rs * g.y, v.z = v.z * rs * g.z, v.w = v.w * rs * g.w;
+                        x4[c * cpr + i] = v;
+                    }
+                    __syncthreads();
+                }
+            }
+        }
 #pragma unroll 1
         for (int c = 0; c < nb; ++c) {
             // keep the weights packed inside the token loop (no hoisted widening)
@@ -458,8 +490,17 @@ __global__ __launch_bounds__(256) void multi_rows_kernel(MRowsArgs a) {
                     if (n0 < N) a.act[static_cast<int64_t>(t) * a.ld1 + n0] = act_fn(acc[0], acc[1], a.act_kind, a.beta, a.lbeta);
                 } else {
 #pragma unroll
-                    for (int r = 0; r < R; ++r)
-                        if (n0 + r < N) a.out0[static_cast<int64_t>(t) * a.ld0 + n0 + r] = acc[r];
+                    for (int r = 0; r < R; ++r) {
+                        const int n = n0 + r;
+                        if (n < N) {
+                            const int64_t oi = static_cast<int64_t>(t) * a.ld[s] + n;
+                            const float v = a.add[s] ? acc[r] + a.add[s][oi] : acc[r];
+                            if (a.out_bf16[s])
+                                static_cast<uint16_t *>(a.out[s])[oi] = f32_to_bf16(v);
+                            else
+                                static_cast<float *>(a.out[s])[oi] = v;
+                        }
+                    }
                 }
             }
         }
@@ -468,13 +509,18 @@ __global__ __launch_bounds__(256) void multi_rows_kernel(MRowsArgs a) {
 
 template <typename IT>
 int launch_rows_multi(MRowsArgs &r, hipStream_t st) {
+    if (r.nw && !std::is_same<IT, float>::value)
+        return set_error(K3_ERR_DTYPE, "moe layer (T tokens): the normalised row input must be fp32");
     const size_t row = static_cast<size_t>(r.K) * sizeof(IT);
     r.tb = static_cast<int>(std::max<size_t>(1, std::min<size_t>(r.T, kLdsBudgetR / row)));
     const int ch = static_cast<int>(cdiv(r.K / 8, 64));
     const int R = ch <= 4 ? 4 : (ch <= 8 ? 2 : 1);
-    r.blocks0 = r.w0 ? static_cast<int>(cdiv(r.N0, kRowWaves * R)) : 0;
-    const int blocks1 = r.wg ? static_cast<int>(cdiv(r.N1, kRowWaves)) : 0;
-    const int blocks = r.blocks0 + blocks1;
+    int blocks = 0;
+    for (int s = 0; s < kPlainSets; ++s) {
+        r.blocks[s] = r.w[s] ? static_cast<int>(cdiv(r.N[s], kRowWaves * R)) : 0;
+        blocks += r.blocks[s];
+    }
+    blocks += r.wg ? static_cast<int>(cdiv(r.N1, kRowWaves)) : 0;
     if (blocks == 0) return K3_OK;
     const size_t lds = static_cast<size_t>(r.tb) * row;
     const dim3 g(static_cast<unsigned>(blocks));
@@ -608,14 +654,17 @@ int multi_args(MultiArgs &a, const void *x, int x_dtype, const int32_t *expert_i
     return K3_OK;
 }
 
-// The whole layer for T tokens: router and shared records after the routed part's.
+// The whole layer for T tokens: router and shared records after the routed part's (whose
+// width is Hr: H, or the latent width of K3's layer, which adds its latent state h and
+// routed sum ylat [T, Hr]).
 struct LayerMultiWs {
-    size_t routed, logits, scores, corrected, idx, w, act_sh, ysh, total;
+    size_t routed, logits, scores, corrected, idx, w, act_sh, ysh, h, ylat, total;
 };
 
-LayerMultiWs layer_multi_layout(int64_t T, int64_t H, int64_t I, int64_t Is, int64_t E, int64_t k) {
+LayerMultiWs layer_multi_layout(int64_t T, int64_t H, int64_t Hr, int64_t I, int64_t Is, int64_t E, int64_t k,
+                                bool latent) {
     LayerMultiWs L{};
-    size_t o = multi_ws_layout(T, H, I, k).total;
+    size_t o = multi_ws_layout(T, Hr, I, k).total;
     L.routed = 0;
     L.logits = o, o += up256(T * E * 4);
     L.scores = o, o += up256(T * E * 4);
@@ -624,6 +673,8 @@ LayerMultiWs layer_multi_layout(int64_t T, int64_t H, int64_t I, int64_t Is, int
     L.w = o, o += up256(T * k * 4);
     L.act_sh = o, o += up256(std::max<int64_t>(T * Is, 1) * 4);
     L.ysh = o, o += up256(T * H * 4);
+    L.h = o, o += latent ? up256(T * Hr * 4) : 0;
+    L.ylat = o, o += latent ? up256(T * Hr * 4) : 0;
     L.total = o;
     return L;
 }
@@ -661,13 +712,13 @@ extern "C" int k3_moe_routed_decode(const void *x, int x_dtype, const int32_t *e
 extern "C" int64_t k3_moe_layer_multi_workspace_size(int64_t T, int64_t H, int64_t I, int64_t shared_I,
                                                      int64_t n_experts, int64_t top_k) {
     if (T <= 0 || H <= 0 || I <= 0 || shared_I < 0 || n_experts <= 0 || top_k <= 0) return 0;
-    return static_cast<int64_t>(layer_multi_layout(T, H, I, shared_I, n_experts, top_k).total);
+    return static_cast<int64_t>(layer_multi_layout(T, H, H, I, shared_I, n_experts, top_k, false).total);
 }
 
 extern "C" int k3_moe_layer_multi_workspace_offsets(int64_t T, int64_t H, int64_t I, int64_t shared_I,
                                                     int64_t n_experts, int64_t top_k, int64_t *offsets) {
     if (!offsets) return set_error(K3_ERR_NULL, "moe layer (T tokens) offsets: null pointer");
-    const LayerMultiWs L = layer_multi_layout(T, H, I, shared_I, n_experts, top_k);
+    const LayerMultiWs L = layer_multi_layout(T, H, H, I, shared_I, n_experts, top_k, false);
     const size_t v[5] = {L.logits, L.scores, L.corrected, L.idx, L.w};
     for (int i = 0; i < 5; ++i) offsets[i] = static_cast<int64_t>(v[i]);
     return K3_OK;
@@ -692,7 +743,7 @@ extern "C" int k3_moe_layer_decode_multi(const void *x, int x_dtype, const void 
                                                 !aligned16(shared_down))))
         return set_error(K3_ERR_ALIGN, "%s: router and shared weights must be 16-byte aligned", what);
     char *w = static_cast<char *>(workspace);
-    const LayerMultiWs L = layer_multi_layout(T, H, I, has_shared ? shared_I : 0, n_experts, top_k);
+    const LayerMultiWs L = layer_multi_layout(T, H, H, I, has_shared ? shared_I : 0, n_experts, top_k, false);
     float *logits = reinterpret_cast<float *>(w + L.logits);
     int32_t *idx = reinterpret_cast<int32_t *>(w + L.idx);
     float *wts = reinterpret_cast<float *>(w + L.w);
@@ -709,10 +760,10 @@ extern "C" int k3_moe_layer_decode_multi(const void *x, int x_dtype, const void 
     r.in = x;
     r.T = a.T;
     r.K = a.Hr;
-    r.w0 = static_cast<const uint16_t *>(router_w);
-    r.N0 = a.E;
-    r.out0 = logits;
-    r.ld0 = a.E;
+    r.w[0] = static_cast<const uint16_t *>(router_w);
+    r.N[0] = a.E;
+    r.out[0] = logits;
+    r.ld[0] = a.E;
     float *act_sh = reinterpret_cast<float *>(w + L.act_sh);
     if (has_shared) {
         r.wg = static_cast<const uint16_t *>(shared_gate);
@@ -740,13 +791,137 @@ extern "C" int k3_moe_layer_decode_multi(const void *x, int x_dtype, const void 
         d.in = act_sh;
         d.T = a.T;
         d.K = static_cast<int>(shared_I);
-        d.w0 = static_cast<const uint16_t *>(shared_down);
-        d.N0 = a.Hr;
-        d.out0 = reinterpret_cast<float *>(w + L.ysh);
-        d.ld0 = a.Hr;
+        d.w[0] = static_cast<const uint16_t *>(shared_down);
+        d.N[0] = a.Hr;
+        d.out[0] = w + L.ysh;
+        d.ld[0] = a.Hr;
         rc = launch_rows_multi<float>(d, st);
         if (rc) return rc;
-        a.yadd = d.out0;
+        a.yadd = reinterpret_cast<const float *>(w + L.ysh);
     }
     return launch_down(a, n_slots, st);
+}
+
+extern "C" int64_t k3_moe_latent_layer_multi_workspace_size(int64_t T, int64_t H, int64_t latent, int64_t I,
+                                                            int64_t shared_I, int64_t n_experts, int64_t top_k) {
+    if (T <= 0 || H <= 0 || latent <= 0 || I <= 0 || shared_I < 0 || n_experts <= 0 || top_k <= 0) return 0;
+    return static_cast<int64_t>(layer_multi_layout(T, H, latent, I, shared_I, n_experts, top_k, true).total);
+}
+
+extern "C" int k3_moe_latent_layer_multi_workspace_offsets(int64_t T, int64_t H, int64_t latent, int64_t I,
+                                                           int64_t shared_I, int64_t n_experts, int64_t top_k,
+                                                           int64_t *offsets) {
+    if (!offsets) return set_error(K3_ERR_NULL, "moe latent layer (T tokens) offsets: null pointer");
+    const LayerMultiWs L = layer_multi_layout(T, H, latent, I, shared_I, n_experts, top_k, true);
+    const size_t v[5] = {L.logits, L.scores, L.corrected, L.idx, L.w};
+    for (int i = 0; i < 5; ++i) offsets[i] = static_cast<int64_t>(v[i]);
+    return K3_OK;
+}
+
+extern "C" int k3_moe_latent_layer_decode_multi(const void *x, int x_dtype, const void *router_w,
+                                                const void *router_bias, int renormalize, float scaling,
+                                                const void *expert_table, const void *latent_down,
+                                                const void *latent_up, const void *latent_norm, float eps,
+                                                const void *shared_gate, const void *shared_up,
+                                                const void *shared_down, void *out, int out_dtype, int64_t T,
+                                                int64_t H, int64_t latent, int64_t I, int64_t shared_I,
+                                                int64_t n_experts, int64_t top_k, int act_kind, float beta,
+                                                float linear_beta, void *workspace, int64_t workspace_bytes,
+                                                void *stream) {
+    const char *what = "moe latent layer (T tokens)";
+    if (!x || !router_w || !expert_table || !latent_down || !latent_up || !latent_norm || !out || !workspace)
+        return set_error(K3_ERR_NULL, "%s: null pointer", what);
+    if (out_dtype != K3_F32 && out_dtype != K3_BF16)
+        return set_error(K3_ERR_DTYPE, "%s: out_dtype %d", what, out_dtype);
+    if (H <= 0 || H % 128 || H > 8192)
+        return set_error(K3_ERR_SHAPE, "%s: H=%lld must be a multiple of 128, <= 8192", what, (long long)H);
+    const bool has_shared = shared_gate || shared_up || shared_down;
+    if (has_shared && (!shared_gate || !shared_up || !shared_down || shared_I <= 0 || shared_I % 128 ||
+                       shared_I > 8192))
+        return set_error(K3_ERR_SHAPE, "%s: shared expert needs gate, up and down with shared_I a multiple of 128, "
+                         "<= 8192", what);
+    if (!aligned16(router_w) || !aligned16(latent_down) || !aligned16(latent_up) || !aligned16(latent_norm) ||
+        (has_shared && (!aligned16(shared_gate) || !aligned16(shared_up) || !aligned16(shared_down))))
+        return set_error(K3_ERR_ALIGN, "%s: dense weights must be 16-byte aligned", what);
+    char *w = static_cast<char *>(workspace);
+    const LayerMultiWs L = layer_multi_layout(T, H, latent, I, has_shared ? shared_I : 0, n_experts, top_k, true);
+    int32_t *idx = reinterpret_cast<int32_t *>(w + L.idx);
+    float *wts = reinterpret_cast<float *>(w + L.w);
+    void *h = w + L.h;
+    float *ylat = reinterpret_cast<float *>(w + L.ylat);
+    MultiArgs a;
+    // the routed part reads h (x's dtype) and writes the fp32 routed sum ylat
+    int rc = multi_args(a, h, x_dtype, idx, wts, expert_table, ylat, K3_F32, T, latent, I, n_experts, top_k, act_kind,
+                        beta, linear_beta, w, what);
+    if (rc) return rc;
+    if (workspace_bytes < static_cast<int64_t>(L.total))
+        return set_error(K3_ERR_WORKSPACE, "%s: workspace %lld < %zu bytes", what, (long long)workspace_bytes, L.total);
+    auto st = static_cast<hipStream_t>(stream);
+    const bool bf = x_dtype == K3_BF16;
+    float *logits = reinterpret_cast<float *>(w + L.logits);
+    float *act_sh = reinterpret_cast<float *>(w + L.act_sh);
+    float *ysh = reinterpret_cast<float *>(w + L.ysh);
+    // R1 on x: router logits, h = W_down x (bf16 for a bf16 x, as the reference's bf16
+    // matmul; fp32 for an fp32 x), the shared gate/up act
+    MRowsArgs r{};
+    r.in = x;
+    r.T = a.T;
+    r.K = static_cast<int>(H);
+    r.w[0] = static_cast<const uint16_t *>(router_w);
+    r.N[0] = a.E;
+    r.out[0] = logits;
+    r.ld[0] = a.E;
+    r.w[1] = static_cast<const uint16_t *>(latent_down);
+    r.N[1] = a.Hr;
+    r.out[1] = h;
+    r.ld[1] = a.Hr;
+    r.out_bf16[1] = bf;
+    if (has_shared) {
+        r.wg = static_cast<const uint16_t *>(shared_gate);
+        r.wu = static_cast<const uint16_t *>(shared_up);
+        r.N1 = static_cast<int>(shared_I);
+        r.act = act_sh;
+        r.ld1 = static_cast<int>(shared_I);
+    }
+    r.act_kind = act_kind;
+    r.beta = beta;
+    r.lbeta = linear_beta;
+    rc = bf ? launch_rows_multi<uint16_t>(r, st) : launch_rows_multi<float>(r, st);
+    if (rc) return rc;
+    // sigmoid + bias routing (moe.py:65-76) on the logits
+    rc = k3_moe_topk(logits, a.E, a.T, a.E, static_cast<const float *>(router_bias), K3_ROUTE_SIGMOID_BIAS,
+                     renormalize, scaling, a.k, idx, wts, reinterpret_cast<float *>(w + L.scores),
+                     reinterpret_cast<float *>(w + L.corrected), stream);
+    if (rc) return rc;
+    const int n_slots = static_cast<int>(std::min<int64_t>(a.P, n_experts));
+    rc = bf ? launch_union_gateup<uint16_t>(a, n_slots, st) : launch_union_gateup<float>(a, n_slots, st);
+    if (rc) return rc;
+    if (has_shared) {
+        MRowsArgs d{};
+        d.in = act_sh;
+        d.T = a.T;
+        d.K = static_cast<int>(shared_I);
+        d.w[0] = static_cast<const uint16_t *>(shared_down);
+        d.N[0] = static_cast<int>(H);
+        d.out[0] = ysh;
+        d.ld[0] = static_cast<int>(H);
+        rc = launch_rows_multi<float>(d, st);
+        if (rc) return rc;
+    }
+    rc = launch_down(a, n_slots, st);
+    if (rc) return rc;
+    // R3: out = W_up rmsnorm(ylat) * norm (+ the shared output), in out_dtype
+    MRowsArgs u{};
+    u.in = ylat;
+    u.T = a.T;
+    u.K = a.Hr;
+    u.nw = static_cast<const float *>(latent_norm);
+    u.eps = eps;
+    u.w[0] = static_cast<const uint16_t *>(latent_up);
+    u.N[0] = static_cast<int>(H);
+    u.out[0] = out;
+    u.ld[0] = static_cast<int>(H);
+    u.out_bf16[0] = out_dtype == K3_BF16;
+    u.add[0] = has_shared ? ysh : nullptr;
+    return launch_rows_multi<float>(u, st);
 }

@@ -69,6 +69,10 @@ SIGNATURES: dict[str, list] = {
     "k3_moe_layer_multi_workspace_offsets": [_I64, _I64, _I64, _I64, _I64, _I64, _P],
     "k3_moe_layer_decode_multi": [_P, _I32, _P, _P, _I32, _I32, _F32, _P, _P, _P, _P, _P, _I32, _I64, _I64,
                                   _I64, _I64, _I64, _I64, _I32, _F32, _F32, _P, _I64, _P],
+    "k3_moe_latent_layer_multi_workspace_size": [_I64, _I64, _I64, _I64, _I64, _I64, _I64],
+    "k3_moe_latent_layer_multi_workspace_offsets": [_I64, _I64, _I64, _I64, _I64, _I64, _I64, _P],
+    "k3_moe_latent_layer_decode_multi": [_P, _I32, _P, _P, _I32, _F32, _P, _P, _P, _P, _F32, _P, _P, _P, _P, _I32,
+                                         _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I32, _F32, _F32, _P, _I64, _P],
     "k3_stream_read": [_P, _I64, _P, _P],
     "k3_stream_copy": [_P, _P, _I64, _P],
 }
@@ -81,7 +85,8 @@ _RESTYPE = {"k3_last_error": ctypes.c_char_p, "k3_version": ctypes.c_char_p,
             "k3_kda_step_workspace_size": ctypes.c_int64,
             "k3_moe_grouped_workspace_size": ctypes.c_int64,
             "k3_moe_routed_workspace_size": ctypes.c_int64,
-            "k3_moe_layer_multi_workspace_size": ctypes.c_int64}
+            "k3_moe_layer_multi_workspace_size": ctypes.c_int64,
+            "k3_moe_latent_layer_multi_workspace_size": ctypes.c_int64}
 
 
 class K3LibraryError(ImportError):

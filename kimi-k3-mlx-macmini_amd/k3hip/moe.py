@@ -419,10 +419,11 @@ class LatentMoE:
     ``__call__(x)`` (moe.py:110-132): route on x; h = x W_down^T (bf16 for a bf16 x, as the
     reference's bf16 matmul gives; fp32 for an fp32 x); the routed experts (SiTU) on h;
     KimiRMSNorm of their weighted sum in fp32; the up projection in fp32; plus the shared
-    expert on the original x.  With ``fused=True`` and bf16 dense weights, up to
-    DECODE_TOKENS tokens run one by one through k3_moe_latent_layer_decode (four launches
-    per token) and more tokens run the routed experts grouped by expert
-    (k3_moe_grouped_ffn); neither synchronises with the host.  ``fused=False`` or fp32 dense
+    expert on the original x.  With ``fused=True`` and bf16 dense weights, one token runs
+    k3_moe_latent_layer_decode (four launches), 2..DECODE_TOKENS tokens
+    k3_moe_latent_layer_decode_multi (seven launches, every selected expert read once for
+    all its tokens) and more tokens run the routed experts grouped by expert
+    (k3_moe_grouped_ffn); none synchronises with the host.  ``fused=False`` or fp32 dense
     weights run the reference's structure (``RoutedMoE`` describes it)."""
 
     DECODE_TOKENS = 8  # up to this many tokens: decode kernels; more: grouped
@@ -479,7 +480,7 @@ class LatentMoE:
         if flat.shape[0] == 1:
             return self._decode(flat, orig, return_router, out_dtype)
         if flat.shape[0] <= self.DECODE_TOKENS:
-            return self._forward_routed(flat, return_router, out_dtype, orig, moe_routed_decode)
+            return self._decode_multi(flat, orig, return_router, out_dtype)
         return self.grouped_forward(flat, return_router, out_dtype, orig)
 
     def _forward_loop(self, flat, orig, return_router, out_dtype):
@@ -522,6 +523,42 @@ class LatentMoE:
         return y, RouterResult(*(torch.cat([getattr(rr, f) for rr in recs]) for f in
                                  ("expert_indices", "expert_weights", "raw_scores", "corrected_scores")))
 
+    def _decode_multi(self, flat, orig, return_router, out_dtype):
+        """2..DECODE_TOKENS tokens in one pass (k3_moe_latent_layer_decode_multi, seven
+        launches, no host synchronisation): router, latent down, shared experts and the up
+        projection on T-token HIP row kernels, every routed expert any token selects read
+        once for all the tokens routed to it.  The RouterResult comes from the workspace."""
+        import ctypes
+        c, R = self.cfg, self._routed
+        act, beta, lb = R._act()
+        table = R.expert_table()
+        n = flat.shape[0]
+        x = flat if flat.dtype in (torch.float32, torch.bfloat16) else flat.to(torch.float32)
+        x = T.contiguous_aligned(x)
+        H, Lw, I, Is, E, k = R._H, self.latent, R._I, R._Is, R._E, R._k
+        nbytes = int(_lib.lib().k3_moe_latent_layer_multi_workspace_size(n, H, Lw, I, Is, E, k))
+        ws = _workspace.get(R.device, nbytes, "moe_latent_multi")
+        out = torch.empty((n, H), dtype=out_dtype, device=R.device)
+        _lib.call("k3_moe_latent_layer_decode_multi", T.ptr(x), T.dtype_code(x.dtype), T.ptr(R.gate_w),
+                  T.ptr(R.gate_b), int(bool(c.moe_renormalize)), float(c.routed_scaling_factor), T.ptr(table),
+                  T.ptr(self.down), T.ptr(self.up), T.ptr(self._norm32), float(c.rms_norm_eps), T.ptr(R.sh_gate),
+                  T.ptr(R.sh_up), T.ptr(R.sh_down), T.ptr(out), T.dtype_code(out_dtype), n, H, Lw, I, Is, E, k,
+                  ACTS[act], float(beta), float(lb or 0.0), T.ptr(ws), ws.numel(), T.stream(x))
+        y = out.reshape(*orig[:-1], H)
+        if not return_router:
+            return y
+        off = (ctypes.c_int64 * 5)()
+        _lib.call("k3_moe_latent_layer_multi_workspace_offsets", n, H, Lw, I, Is, E, k, off)
+
+        def rec(o, count, dt):
+            return ws[o:o + 4 * count].view(dt).clone()
+
+        r = RouterResult(rec(off[3], n * k, torch.int32).to(torch.int64).reshape(n, k),
+                         rec(off[4], n * k, torch.float32).reshape(n, k),
+                         rec(off[1], n * E, torch.float32).reshape(n, E),
+                         rec(off[2], n * E, torch.float32).reshape(n, E))
+        return y, r
+
     def grouped_forward(self, flat, return_router=False, out_dtype=torch.float32, orig=None):
         """Many tokens: route every token on x as given; h = x W_down^T on the BLAS library
         (bf16 for a bf16 x, fp32 for an fp32 x); the routed experts grouped by expert on the
@@ -530,9 +567,10 @@ class LatentMoE:
         return self._forward_routed(flat, return_router, out_dtype, orig, moe_grouped_ffn)
 
     def multi_forward(self, flat, return_router=False, out_dtype=torch.float32, orig=None):
-        """A few decode tokens (at most DECODE_TOKENS): as grouped_forward, with the routed
-        experts run by moe_routed_decode, so every expert any token selects is read once
-        against all the tokens routed to it, with fp32 accumulation."""
+        """A few decode tokens (at most DECODE_TOKENS) with the dense projections on the BLAS
+        library: as grouped_forward, with the routed experts run by moe_routed_decode, so
+        every expert any token selects is read once against all the tokens routed to it.
+        ``__call__`` runs the same step with every projection in HIP (_decode_multi)."""
         return self._forward_routed(flat, return_router, out_dtype, orig, moe_routed_decode)
 
     def _forward_routed(self, flat, return_router, out_dtype, orig, routed_fn):
