@@ -269,11 +269,11 @@ MULTI_T = 4                     # decode tokens per step of the multi-token laye
 
 
 def bench_layer_multi(torch, steps, warmup, dev, T=MULTI_T):
-    """The 384-expert layer for T decode tokens per step (RoutedMoE.__call__: router GEMM and
-    top-k, k3_moe_routed_decode over the union of the routed experts, shared expert on the
-    BLAS library).  Returns seconds for `steps` steps and the mean union size / bytes per
-    step, the algorithmic bytes when every union expert, the router and the shared expert
-    are read once."""
+    """The 384-expert layer for T decode tokens per step (RoutedMoE.__call__ on
+    k3_moe_layer_decode_multi: router and shared gate/up rows, top-k, the routed experts over
+    the union of the tokens' choices, shared down rows).  Returns seconds for `steps` steps
+    and the mean union size / bytes per step, the algorithmic bytes when every union expert,
+    the router and the shared expert are read once."""
     import numpy as np
     moe, _ = build_layer(torch, dev)
     gen = torch.Generator(device=dev)
@@ -848,8 +848,8 @@ def main():
             "GB/s": round(bytes4 / (mus4 * 1e-6) / 1e9, 1),
             "pct_hbm_peak": round(100 * bytes4 / (mus4 * 1e-6) / 1e9 / HBM_PEAK_GBS, 1),
             "bytes_if_per_token": MULTI_T * LAYER_BYTES,
-            "what": "RoutedMoE on 4 tokens: router GEMM + k3_moe_topk, k3_moe_routed_decode over the union "
-                    "of the routed experts (each read once), shared expert on the BLAS library",
+            "what": "RoutedMoE on 4 tokens: k3_moe_layer_decode_multi (router and shared rows on the "
+                    "T-token row kernel, top-k, the union of the routed experts each read once)",
             "step_us": mstats4, **counter_fields(cnt.get("moe_layer_t4"))}
         if "moe_layer" in line:
             line["moe_layer_t4"]["vs_4_single_token_layers"] = round(4 * line["moe_layer"]["us_per_layer"] / mus4, 3)

@@ -11,9 +11,9 @@ the grouped path reaches 6.6e-4 (the scaled MFMA sums each 128-element dot about
 below its largest product, and SiTU's act carries about 12 bits in three E4M3 terms), so
 that case is held to the 1e-3 gate itself.  One token runs the fused decode kernels,
 which round h as the oracle does and accumulate in fp32: 1e-5.  Two to eight tokens run the
-multi-token decode (k3_moe_routed_decode, fp32 accumulation, 1e-7 on its own) on h from the
-BLAS GEMM, where more latent elements can land one bf16 ulp from the oracle's rounding
-(observed 2.6e-5 at K3 shapes and four tokens): 1e-4.  The router result is compared exactly
+multi-token decode (k3_moe_latent_layer_decode_multi, fp32 accumulation, 1e-7 on the routed
+part alone), where more latent elements can land one bf16 ulp from the oracle's rounding
+(observed 5.3e-5 at K3 shapes and four tokens): 1e-4.  The router result is compared exactly
 (ids) and to 1e-5 (weights).
 """
 from __future__ import annotations
@@ -137,7 +137,7 @@ def check(cfg, seed, T, distinct=None, on_device=False, tol=None):
 @pytest.mark.parametrize("T", [1, 5, 12])
 def test_latent_moe_small(T):
     """T = 1: the fused decode (k3_moe_latent_layer_decode); T = 5: the multi-token decode
-    (k3_moe_routed_decode); T = 12: the grouped path."""
+    (k3_moe_latent_layer_decode_multi); T = 12: the grouped path."""
     check(K3Cfg(hidden_size=256, routed_expert_hidden_size=128, moe_intermediate_size=128, num_experts=16,
                 num_experts_per_token=4), seed=40 + T, T=T)
 
