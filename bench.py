@@ -867,6 +867,8 @@ def main():
                                    "launches_per_token": 4, "step_us": kstats, "prefill": kpre,
                                    "four_tokens": kmulti,
                                    **counter_fields(cnt.get("k3_latent_layer_b1"))}
+        if kmulti is not None:
+            kmulti.update(counter_fields(cnt.get("k3_latent_layer_t4")))
         if kpre is not None:
             kpre.update({"grouped_experts_" + k_: v_ for k_, v_ in
                          counter_fields(cnt.get("k3_prefill_t2048_e896_grouped")).items()})
@@ -903,7 +905,7 @@ def main():
             "us": round(fus, 2), "GB/s": round(fgbs, 1), "pct_hbm_peak": round(100 * fgbs / HBM_PEAK_GBS, 1),
             "bytes": MLA_F32_BYTES, "heads": MLA_H, "tokens": MLA_T, "cache": "fp32 (the reference's default)",
             "what": "k3_mla_decode_absorbed_f32: fp32 rows split into hi/lo bf16 planes as staged",
-            "launches": 4, "step_us": fstats}
+            "launches": 4, "step_us": fstats, **counter_fields(cnt.get("mla_decode_f32_cache_h64_t32768"))}
     if "mlastep" in work:
         ms_ = min(K, 128)
         ssec, sstats = bench_mla_step(torch, ms_, min(W, 16), dev)
