@@ -32,6 +32,7 @@
 // Every selected expert's gate, up and down bytes are read once per call, whatever the
 // number of tokens routed to it.  Deterministic: no float atomics, fixed orders.
 #include <algorithm>
+#include <atomic>
 #include <type_traits>
 
 #include "moe_common.h"
@@ -364,6 +365,7 @@ struct MRowsArgs {
     int ld1;
     int act_kind;
     float beta, lbeta;
+    int wv[3];               // persistent form: waves on plain set 0, plain set 1, the pair set
 };
 constexpr int kRowWaves = 4;
 // small enough that LDS allows more blocks per CU than the registers do (three at 133 VGPRs)
@@ -507,11 +509,241 @@ __global__ __launch_bounds__(256) void multi_rows_kernel(MRowsArgs a) {
     }
 }
 
+// R in its persistent form, for T input rows that fit in LDS together (up to 128 KB; taken
+// for fp32 rows that multi_rows_kernel would stage in three or more batches): a few blocks per CU
+// (eight waves each) stage all T rows once (normalised as they are staged when nw is set).
+// Every wave of the grid works on one row set for the whole launch -- plain set 0, plain set
+// 1 or the pair set, wv[0], wv[1] and wv[2] waves of them, in proportion to the sets' bytes --
+// taking the set's rows first, first + stride, ... (stride: the set's wave count), and
+// streams them through two register buffers, so one row is in flight while the other is
+// reduced against the staged tokens: a plain set's rows alternate between the buffers, a pair
+// holds its gate row in one and its up row in the other.  Per row and token the same
+// products and the same lane / wave sum order as multi_rows_kernel.
+constexpr int kLoopWaves = 8;
+constexpr int kStageLoads = 16;                                   // 16-byte loads per thread
+constexpr size_t kLoopLdsMax = size_t(kStageLoads) * 16 * 64 * kLoopWaves;  // 128 KB
+
+// res[t] (lane 63) = row . token t for t < T: w one row's 16-byte chunks (chunk c * 64 + lane),
+// x the staged tokens (cpr chunks each)
+template <typename IT, int CH>
+__device__ __forceinline__ void row_dots(uint4 (&w)[CH], const uint4 *x, int cpr, int nch, int lane, int T,
+                                         float (&res)[kMaxTokens]) {
+    using XC = typename std::conditional<std::is_same<IT, float>::value, float4, uint4>::type;
+#pragma unroll
+    for (int t = 0; t < kMaxTokens; ++t) {
+        if (t >= T) break;
+        // keep the weights packed inside the token loop (no hoisted widening)
+#pragma unroll
+        for (int c = 0; c < CH; ++c) asm volatile("" : "+v"(w[c].x), "+v"(w[c].y), "+v"(w[c].z), "+v"(w[c].w));
+        const XC *xr = reinterpret_cast<const XC *>(x + t * cpr);
+        float a0 = 0.f, a1 = 0.f;
+#pragma unroll
+        for (int c = 0; c < CH; ++c) {
+            const int cc = c * 64 + lane;
+            if (cc < nch) {
+                if (c & 1)
+                    a1 = rdot(w[c], xr, cc, a1);
+                else
+                    a0 = rdot(w[c], xr, cc, a0);
+            }
+        }
+        res[t] = wave_sum_to_lane63(a0 + a1);
+    }
+}
+
+template <int CH>
+__device__ __forceinline__ void load_row(uint4 (&w)[CH], __amdgpu_buffer_rsrc_t rs, int n, int N, uint32_t rowb,
+                                         int nch, int lane) {
+#pragma unroll
+    for (int c = 0; c < CH; ++c) {
+        const int cc = c * 64 + lane;
+        w[c] = buf_load16(rs, (n < N && cc < nch) ? static_cast<uint32_t>(n) * rowb + cc * 16u : kOobOffset);
+    }
+}
+
+template <typename IT, int CH>
+__global__ __launch_bounds__(64 * kLoopWaves) void multi_rows_loop_kernel(MRowsArgs a) {
+    extern __shared__ uint4 xs[];  // [T][K * sizeof(IT) / 16]
+    __shared__ float red[kLoopWaves];
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+    const int gw = static_cast<int>(blockIdx.x) * kLoopWaves + wave;
+    const int nch = a.K >> 3, T = a.T;
+    const uint32_t rowb = static_cast<uint32_t>(a.K) * 2u;
+    const int cpr = static_cast<int>(a.K * sizeof(IT) / 16);  // 16-byte chunks per input row
+
+    // this wave's set (wave-uniform) and its rows
+    const int v0 = a.wv[0], v1 = a.wv[1], v2 = a.wv[2];
+    const bool pair = gw >= v0 + v1;
+    const int s = gw < v0 ? 0 : 1;
+    const int first = gw < v0 ? gw : (pair ? gw - v0 - v1 : gw - v0);
+    const int stride = gw < v0 ? v0 : (pair ? v2 : v1);
+    const int N = (gw >= v0 + v1 + v2) ? 0 : (pair ? a.N1 : a.N[s]);  // idle waves: no rows
+    const uint32_t bytes = static_cast<uint32_t>(N) * rowb;
+    const auto ra = make_rsrc(N ? (pair ? a.wg : a.w[s]) : nullptr, bytes);
+    const auto rb = make_rsrc(N ? (pair ? a.wu : a.w[s]) : nullptr, bytes);
+    const int step = pair ? stride : 2 * stride;
+    int na = first, nb = pair ? first : first + stride;
+
+    uint4 wa[CH], wb[CH];
+    load_row<CH>(wa, ra, na, N, rowb, nch, lane);
+    load_row<CH>(wb, rb, nb, N, rowb, nch, lane);
+    // stage the T input rows: every load issued (past the end: zeros, no access), then the stores
+    {
+        const int total = T * cpr;
+        const auto rin = make_rsrc(a.in, static_cast<uint32_t>(total) * 16u);
+        uint4 v[kStageLoads];
+#pragma unroll
+        for (int j = 0; j < kStageLoads; ++j)
+            v[j] = buf_load16(rin, static_cast<uint32_t>(j * 64 * kLoopWaves + static_cast<int>(threadIdx.x)) * 16u);
+#pragma unroll
+        for (int j = 0; j < kStageLoads; ++j) {
+            const int i = j * 64 * kLoopWaves + static_cast<int>(threadIdx.x);
+            if (i < total) xs[i] = v[j];
+        }
+    }
+    __syncthreads();
+    if constexpr (std::is_same<IT, float>::value) {
+        if (a.nw) {
+            // KimiRMSNorm of each staged row: row * (1 / sqrt(mean(row^2) + eps)) * nw
+            float4 *x4 = reinterpret_cast<float4 *>(xs);
+            for (int t = 0; t < T; ++t) {
+                float ss = 0.f;
+                for (int i = threadIdx.x; i < cpr; i += 64 * kLoopWaves) {
+                    const float4 v = x4[t * cpr + i];
+                    ss = fmaf(v.x, v.x, fmaf(v.y, v.y, fmaf(v.z, v.z, fmaf(v.w, v.w, ss))));
+                }
+                ss = wave_sum_all(ss);
+                if (lane == 0) red[wave] = ss;
+                __syncthreads();
+                float tot = red[0];
+#pragma unroll
+                for (int w = 1; w < kLoopWaves; ++w) tot += red[w];
+                const float rs = 1.0f / sqrtf(tot / static_cast<float>(a.K) + a.eps);
+                for (int i = threadIdx.x; i < cpr; i += 64 * kLoopWaves) {
+                    const float4 g = reinterpret_cast<const float4 *>(a.nw)[i];
+                    float4 v = x4[t * cpr + i];
+                    v.x = v.x * rs * g.x, v.y = v.y * rs * g.y, v.z = v.z * rs * g.z, v.w = v.w * rs * g.w;
+                    x4[t * cpr + i] = v;
+                }
+                __syncthreads();
+            }
+        }
+    }
+
+    // plain rows: out[t * ld + n] = dot (+ add), fp32 or bf16
+    auto store_plain = [&a, s, lane, T](const float (&res)[kMaxTokens], int n) {
+        if (lane != 63) return;
+#pragma unroll
+        for (int t = 0; t < kMaxTokens; ++t) {
+            if (t >= T) break;
+            const int64_t oi = static_cast<int64_t>(t) * a.ld[s] + n;
+            const float y = a.add[s] ? res[t] + a.add[s][oi] : res[t];
+            if (a.out_bf16[s])
+                static_cast<uint16_t *>(a.out[s])[oi] = f32_to_bf16(y);
+            else
+                static_cast<float *>(a.out[s])[oi] = y;
+        }
+    };
+    float ga[kMaxTokens], gb[kMaxTokens];
+#pragma unroll 1
+    while (na < N) {
+        row_dots<IT, CH>(wa, xs, cpr, nch, lane, T, ga);
+        if (!pair) store_plain(ga, na);
+        load_row<CH>(wa, ra, na + step, N, rowb, nch, lane);
+        if (nb >= N) break;
+        row_dots<IT, CH>(wb, xs, cpr, nch, lane, T, gb);
+        if (pair) {
+            if (lane == 63) {
+#pragma unroll
+                for (int t = 0; t < kMaxTokens; ++t) {
+                    if (t >= T) break;
+                    a.act[static_cast<int64_t>(t) * a.ld1 + nb] = act_fn(ga[t], gb[t], a.act_kind, a.beta, a.lbeta);
+                }
+            }
+        } else {
+            store_plain(gb, nb);
+        }
+        load_row<CH>(wb, rb, nb + step, N, rowb, nch, lane);
+        na += step, nb += step;
+    }
+}
+
+// Blocks of multi_rows_loop_kernel<IT, CH> resident per CU for lds dynamic bytes (the
+// register-bound count, cached per device, capped by the CU's LDS).
+template <typename IT, int CH>
+int loop_blocks_per_cu(size_t lds, int &cus) {
+    constexpr int kDevs = 64;
+    static std::atomic<int> cached_occ[kDevs], cached_cus[kDevs], cached_lds[kDevs];
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kDevs) return 0;
+    int occ = cached_occ[dev].load(std::memory_order_relaxed);
+    if (!occ) {
+        int per_cu = 0, n = 0, l = 0;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, multi_rows_loop_kernel<IT, CH>, 64 * kLoopWaves, 0) !=
+                hipSuccess ||
+            hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+            hipDeviceGetAttribute(&l, hipDeviceAttributeMaxSharedMemoryPerMultiprocessor, dev) != hipSuccess)
+            return 0;
+        cached_cus[dev].store(n, std::memory_order_relaxed);
+        cached_lds[dev].store(l, std::memory_order_relaxed);
+        occ = std::max(1, per_cu);
+        cached_occ[dev].store(occ, std::memory_order_relaxed);
+    }
+    cus = cached_cus[dev].load(std::memory_order_relaxed);
+    const size_t l = static_cast<size_t>(cached_lds[dev].load(std::memory_order_relaxed));
+    const int by_lds = static_cast<int>(l / (lds + 64 * sizeof(float)));
+    return std::max(1, std::min(occ, by_lds));
+}
+
+template <typename IT, int CH>
+int launch_rows_loop(MRowsArgs &r, size_t lds, hipStream_t st) {
+    int cus = 0;
+    const int per_cu = loop_blocks_per_cu<IT, CH>(lds, cus);
+    if (per_cu <= 0 || cus <= 0) return check_hip(hipErrorInvalidDevice, "moe layer (T tokens): device query");
+    // up to 128 KB of dynamic LDS: above the 64 KB default, so opt in once per form
+    static const hipError_t lds_rc = hipFuncSetAttribute(reinterpret_cast<const void *>(&multi_rows_loop_kernel<IT, CH>),
+                                                         hipFuncAttributeMaxDynamicSharedMemorySize,
+                                                         static_cast<int>(kLoopLdsMax));
+    const int rc = check_hip(lds_rc, "moe layer (T tokens): dense rows LDS size");
+    if (rc) return rc;
+    // the grid's waves split over the sets in proportion to their rows (a pair is two rows),
+    // each set at least one wave and at most one wave per unit
+    const int64_t units[3] = {r.w[0] ? r.N[0] : 0, r.w[1] ? r.N[1] : 0, r.wg ? r.N1 : 0};
+    const int64_t rows = units[0] + units[1] + 2 * units[2];
+    const int64_t waves = static_cast<int64_t>(per_cu) * cus * kLoopWaves;
+    int total = 0;
+    for (int i = 0; i < 3; ++i) {
+        const int64_t share = cdiv(waves * units[i] * (i == 2 ? 2 : 1), rows);
+        r.wv[i] = units[i] ? static_cast<int>(std::max<int64_t>(1, std::min<int64_t>(share, units[i]))) : 0;
+        total += r.wv[i];
+    }
+    const int blocks = static_cast<int>(cdiv(total, kLoopWaves));
+    multi_rows_loop_kernel<IT, CH><<<dim3(static_cast<unsigned>(blocks)), 64 * kLoopWaves, lds, st>>>(r);
+    return check_hip(hipGetLastError(), "moe layer (T tokens): dense rows launch");
+}
+
 template <typename IT>
 int launch_rows_multi(MRowsArgs &r, hipStream_t st) {
     if (r.nw && !std::is_same<IT, float>::value)
         return set_error(K3_ERR_DTYPE, "moe layer (T tokens): the normalised row input must be fp32");
+    if (r.T < 1 || r.T > kMaxTokens) return set_error(K3_ERR_SHAPE, "moe layer (T tokens): %d tokens", r.T);
     const size_t row = static_cast<size_t>(r.K) * sizeof(IT);
+    // fp32 rows that the batched kernel would stage in three or more batches (K3's shared
+    // down projection at four tokens: 53.7 -> 36.6 us) take the persistent form; elsewhere the
+    // batched kernel measured faster (the 384-expert layer's router and shared rows at four
+    // tokens: 21.9 against 30 us in the persistent form)
+    const size_t in_bytes = static_cast<size_t>(r.T) * row;
+    if (std::is_same<IT, float>::value && in_bytes > 2 * static_cast<size_t>(kLdsBudgetR) && in_bytes <= kLoopLdsMax &&
+        r.K <= 8192) {
+        const int units = (r.w[0] ? r.N[0] : 0) + (r.w[1] ? r.N[1] : 0) + (r.wg ? r.N1 : 0);
+        if (units == 0) return K3_OK;
+        const size_t lds = static_cast<size_t>(r.T) * row;
+        const int ch = static_cast<int>(cdiv(r.K / 8, 64));
+        if (ch <= 4) return launch_rows_loop<IT, 4>(r, lds, st);
+        if (ch <= 8) return launch_rows_loop<IT, 8>(r, lds, st);
+        if (ch <= 14) return launch_rows_loop<IT, 14>(r, lds, st);
+        return launch_rows_loop<IT, 16>(r, lds, st);
+    }
     r.tb = static_cast<int>(std::max<size_t>(1, std::min<size_t>(r.T, kLdsBudgetR / row)));
     const int ch = static_cast<int>(cdiv(r.K / 8, 64));
     const int R = ch <= 4 ? 4 : (ch <= 8 ? 2 : 1);

@@ -142,6 +142,16 @@ def test_latent_moe_small(T):
                 num_experts_per_token=4), seed=40 + T, T=T)
 
 
+@pytest.mark.parametrize("T", [5, 8])
+def test_latent_moe_few_tokens_wide_rows(T):
+    """Two to eight tokens with fp32 row inputs too wide to stage in one batch: the shared
+    down rows (act [T, 4096] fp32: 80 / 128 KB) run the persistent row kernel, and the
+    normalised up rows (the latent state [T, 3072] fp32: 60 / 96 KB) the batched kernel at
+    T = 5 and the persistent one, normalising as it stages, at T = 8."""
+    check(K3Cfg(hidden_size=1024, routed_expert_hidden_size=3072, moe_intermediate_size=2048, num_experts=16,
+                num_experts_per_token=4), seed=60 + T, T=T)
+
+
 K3_CFG = dict(hidden_size=7168, routed_expert_hidden_size=3584, moe_intermediate_size=3072, num_experts=896,
               num_experts_per_token=16)
 
