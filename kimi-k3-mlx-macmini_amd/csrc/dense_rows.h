@@ -55,60 +55,131 @@ __device__ __forceinline__ float block_sum(float v, float *red) {
     return t;
 }
 
-// v (fp32, K values) into LDS; ends with a block barrier
-template <int MODE, int NW>
+// v (fp32, K values) into LDS; ends with a block barrier.  CH bounds K (K <= 512 CH), so a
+// thread's share is at most NF float4 chunks (c = j * NT + threadIdx.x); they are loaded in
+// batches of VB chunks with every load of a batch issued before any is used (buffer loads:
+// past the end, zeros and no access), so the staging costs one memory round trip per batch.
+template <int MODE, int NW, int CH>
 __device__ __forceinline__ void stage_vector(const RowsArgs &a, float *vs, float *red) {
     constexpr int NT = 64 * NW;
-    const int K = a.K;
+    constexpr int NF = (2 * CH + NW - 1) / NW;  // float4 chunks per thread
+    constexpr int VB = CH >= 24 ? 2 : 4;         // chunks per batch (registers beside the rows)
+    const int K = a.K, n4 = K / 4;
+    const int tid = static_cast<int>(threadIdx.x);
+    float4 *v4 = reinterpret_cast<float4 *>(vs);
+    auto off = [tid](int j) { return static_cast<uint32_t>(j * NT + tid) * 16u; };
     if (MODE == kModeX) {
         if (a.x_bf16) {
-            const uint4 *x8 = static_cast<const uint4 *>(a.x);
-            for (int c = threadIdx.x; c < K / 8; c += NT) {
-                const uint4 q = x8[c];
-                const uint32_t d[4] = {q.x, q.y, q.z, q.w};
+            constexpr int NB = (CH + NW - 1) / NW;  // 16-byte bf16 chunks per thread
+            const auto rx = make_rsrc(a.x, static_cast<uint32_t>(K) * 2u);
+            uint4 q[NB];
 #pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    vs[8 * c + 2 * i] = __uint_as_float(d[i] << 16);
-                    vs[8 * c + 2 * i + 1] = __uint_as_float(d[i] & 0xffff0000u);
+            for (int j = 0; j < NB; ++j) q[j] = buf_load16(rx, off(j));
+#pragma unroll
+            for (int j = 0; j < NB; ++j) {
+                const int c = j * NT + tid;
+                if (c < K / 8) {
+                    const uint32_t d[4] = {q[j].x, q[j].y, q[j].z, q[j].w};
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        vs[8 * c + 2 * i] = __uint_as_float(d[i] << 16);
+                        vs[8 * c + 2 * i + 1] = __uint_as_float(d[i] & 0xffff0000u);
+                    }
                 }
             }
         } else {
-            const float4 *x4 = static_cast<const float4 *>(a.x);
-            for (int c = threadIdx.x; c < K / 4; c += NT) reinterpret_cast<float4 *>(vs)[c] = x4[c];
+            const auto rx = make_rsrc(a.x, static_cast<uint32_t>(K) * 4u);
+#pragma unroll
+            for (int j0 = 0; j0 < NF; j0 += VB) {
+                float4 q[VB];
+#pragma unroll
+                for (int j = 0; j < VB; ++j) q[j] = __builtin_bit_cast(float4, buf_load16(rx, off(j0 + j)));
+#pragma unroll
+                for (int j = 0; j < VB; ++j)
+                    if ((j0 + j) * NT + tid < n4) v4[(j0 + j) * NT + tid] = q[j];
+            }
         }
     } else if (MODE == kModeNorm) {
+        // src and nw of the batch together; the sum of squares in the lane's chunk order
+        const auto rsrc = make_rsrc(a.src, static_cast<uint32_t>(K) * 4u);
+        const auto rnw = make_rsrc(a.nw, static_cast<uint32_t>(K) * 4u);
+        float4 sv[NF], gv[NF];
         float ss = 0.f;
-        for (int c = threadIdx.x; c < K / 4; c += NT) {
-            const float4 s = reinterpret_cast<const float4 *>(a.src)[c];
-            ss = fmaf(s.x, s.x, fmaf(s.y, s.y, fmaf(s.z, s.z, fmaf(s.w, s.w, ss))));
-            reinterpret_cast<float4 *>(vs)[c] = s;
+#pragma unroll
+        for (int j0 = 0; j0 < NF; j0 += VB) {
+#pragma unroll
+            for (int j = j0; j < j0 + VB && j < NF; ++j) {
+                sv[j] = __builtin_bit_cast(float4, buf_load16(rsrc, off(j)));
+                gv[j] = __builtin_bit_cast(float4, buf_load16(rnw, off(j)));
+            }
+#pragma unroll
+            for (int j = j0; j < j0 + VB && j < NF; ++j) {
+                const float4 x = sv[j];
+                ss = fmaf(x.x, x.x, fmaf(x.y, x.y, fmaf(x.z, x.z, fmaf(x.w, x.w, ss))));
+            }
         }
         const float rs = 1.0f / sqrtf(block_sum<NW>(ss, red) / static_cast<float>(K) + a.eps);
-        for (int c = threadIdx.x; c < K / 4; c += NT) {
-            const float4 g = reinterpret_cast<const float4 *>(a.nw)[c];
-            float4 v = reinterpret_cast<float4 *>(vs)[c];
-            v.x = v.x * rs * g.x, v.y = v.y * rs * g.y, v.z = v.z * rs * g.z, v.w = v.w * rs * g.w;
-            reinterpret_cast<float4 *>(vs)[c] = v;
+#pragma unroll
+        for (int j = 0; j < NF; ++j) {
+            const int c = j * NT + tid;
+            if (c < n4) {
+                float4 v = sv[j];
+                const float4 g = gv[j];
+                v.x = v.x * rs * g.x, v.y = v.y * rs * g.y, v.z = v.z * rs * g.z, v.w = v.w * rs * g.w;
+                v4[c] = v;
+            }
         }
     } else if (MODE == kModeHeadNorm) {
         // heads of 128 values = 32 float4; gl holds four partial sums of squares per head
-        for (int c = threadIdx.x; c < K / 4; c += NT) {
-            const float4 p = reinterpret_cast<const float4 *>(a.gl)[c >> 5];
-            const float rs = 1.0f / sqrtf((((p.x + p.y) + p.z) + p.w) / 128.0f + a.eps);
-            const float4 w = reinterpret_cast<const float4 *>(a.nw)[c & 31];
-            float4 v = reinterpret_cast<const float4 *>(a.o)[c];
-            v.x = v.x * rs * w.x, v.y = v.y * rs * w.y, v.z = v.z * rs * w.z, v.w = v.w * rs * w.w;
-            reinterpret_cast<float4 *>(vs)[c] = v;
+        const auto ro = make_rsrc(a.o, static_cast<uint32_t>(K) * 4u);
+        const auto rgl = make_rsrc(a.gl, static_cast<uint32_t>(K / 128) * 16u);
+        const auto rnw = make_rsrc(a.nw, 128u * 4u);
+#pragma unroll
+        for (int j0 = 0; j0 < NF; j0 += VB) {
+            float4 ov[VB], pv[VB], wv[VB];
+#pragma unroll
+            for (int j = 0; j < VB; ++j) {
+                const int c = (j0 + j) * NT + tid;
+                ov[j] = __builtin_bit_cast(float4, buf_load16(ro, off(j0 + j)));
+                pv[j] = __builtin_bit_cast(float4, buf_load16(rgl, c < n4 ? static_cast<uint32_t>(c >> 5) * 16u : kOobOffset));
+                wv[j] = __builtin_bit_cast(float4, buf_load16(rnw, static_cast<uint32_t>(c & 31) * 16u));
+            }
+#pragma unroll
+            for (int j = 0; j < VB; ++j) {
+                const int c = (j0 + j) * NT + tid;
+                if (c < n4) {
+                    const float4 p = pv[j], w = wv[j];
+                    const float rs = 1.0f / sqrtf((((p.x + p.y) + p.z) + p.w) / 128.0f + a.eps);
+                    float4 v = ov[j];
+                    v.x = v.x * rs * w.x, v.y = v.y * rs * w.y, v.z = v.z * rs * w.z, v.w = v.w * rs * w.w;
+                    v4[c] = v;
+                }
+            }
         }
     } else {
-        for (int c = threadIdx.x; c < K / 4; c += NT) {
-            float4 v = reinterpret_cast<const float4 *>(a.o)[c];
-            if (a.gl) {
-                const float4 g = reinterpret_cast<const float4 *>(a.gl)[c];
-                v.x /= 1.0f + expf(-g.x), v.y /= 1.0f + expf(-g.y), v.z /= 1.0f + expf(-g.z),
-                    v.w /= 1.0f + expf(-g.w);
+        const auto ro = make_rsrc(a.o, static_cast<uint32_t>(K) * 4u);
+        const auto rgl = make_rsrc(a.gl, a.gl ? static_cast<uint32_t>(K) * 4u : 0u);
+#pragma unroll
+        for (int j0 = 0; j0 < NF; j0 += VB) {
+            float4 ov[VB], gv[VB];
+#pragma unroll
+            for (int j = 0; j < VB; ++j) {
+                ov[j] = __builtin_bit_cast(float4, buf_load16(ro, off(j0 + j)));
+                gv[j] = __builtin_bit_cast(float4, buf_load16(rgl, off(j0 + j)));
             }
-            reinterpret_cast<float4 *>(vs)[c] = v;
+#pragma unroll
+            for (int j = 0; j < VB; ++j) {
+                const int c = (j0 + j) * NT + tid;
+                if (c < n4) {
+                    float4 v = ov[j];
+                    if (a.gl) {
+                        const float4 g = gv[j];
+                        v.x /= 1.0f + expf(-g.x), v.y /= 1.0f + expf(-g.y), v.z /= 1.0f + expf(-g.z),
+                            v.w /= 1.0f + expf(-g.w);
+                    }
+                    v4[c] = v;
+                }
+            }
         }
     }
     __syncthreads();
@@ -164,7 +235,7 @@ __global__ __launch_bounds__(64 * NW) void step_rows_kernel(RowsArgs a) {
             wr[r][u] = buf_load16(rw, (n < N && c < nch) ? static_cast<uint32_t>(n) * rowb + c * 16u : kOobOffset);
         }
     // 2. the input vector
-    stage_vector<MODE, NW>(a, vs, red);
+    stage_vector<MODE, NW, CH>(a, vs, red);
     // 3. row dots
     const float4 *v4 = reinterpret_cast<const float4 *>(vs);
 #pragma unroll
@@ -262,7 +333,7 @@ __global__ __launch_bounds__(64 * NW) void step_rows_loop_kernel(RowsArgs a) {
     uint4 wa[CH], wb[CH];
     int g = static_cast<int>(blockIdx.x);
     load_row(wa, g);
-    stage_vector<MODE, NW>(a, vs, red);
+    stage_vector<MODE, NW, CH>(a, vs, red);
     for (; g < total; g += 2 * G) {
         load_row(wb, g + G);
         reduce_row(wa, g);

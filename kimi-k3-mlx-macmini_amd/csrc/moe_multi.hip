@@ -370,6 +370,9 @@ struct MRowsArgs {
 constexpr int kRowWaves = 4;
 // small enough that LDS allows more blocks per CU than the registers do (three at 133 VGPRs)
 constexpr int kLdsBudgetR = 32768;
+// 16-byte staging loads per thread and batch: a batch is at most max(kLdsBudgetR, one row of
+// 8192 fp32) bytes
+constexpr int kStageR = 32768 / 16 / (64 * kRowWaves);
 
 // 8 bf16 weights . 8 bf16 inputs (exact products)
 __device__ __forceinline__ float rdot(uint4 w, const uint4 *x, int c, float acc) {
@@ -432,7 +435,19 @@ __global__ __launch_bounds__(256) void multi_rows_kernel(MRowsArgs a) {
     for (int c0 = 0; c0 < a.T; c0 += a.tb) {
         const int nb = min(a.tb, a.T - c0);
         if (c0 > 0) __syncthreads();  // every wave is done with the previous batch
-        for (int i = threadIdx.x; i < nb * cpr; i += 64 * kRowWaves) xs[i] = in4[static_cast<int64_t>(c0) * cpr + i];
+        {
+            // every load of the batch issued before the stores (past the end: zeros, no access)
+            const auto rin = make_rsrc(in4 + static_cast<int64_t>(c0) * cpr, static_cast<uint32_t>(nb * cpr) * 16u);
+            uint4 v[kStageR];
+#pragma unroll
+            for (int j = 0; j < kStageR; ++j)
+                v[j] = buf_load16(rin, static_cast<uint32_t>(j * 64 * kRowWaves + static_cast<int>(threadIdx.x)) * 16u);
+#pragma unroll
+            for (int j = 0; j < kStageR; ++j) {
+                const int i = j * 64 * kRowWaves + static_cast<int>(threadIdx.x);
+                if (i < nb * cpr) xs[i] = v[j];
+            }
+        }
         __syncthreads();
         if constexpr (std::is_same<IT, float>::value) {
             if (a.nw) {
