@@ -132,19 +132,27 @@ __global__ __launch_bounds__(256) void multi_union_kernel(MultiArgs a) {
 template <typename XT, int GA>
 __global__ __launch_bounds__(256) void multi_gateup_kernel(MultiArgs a) {
     extern __shared__ uint4 smem[];  // [tb_x][Hr / 8 (bf16) or Hr / 4 (fp32) chunks], swizzled
+    __shared__ uint32_t tok_s[kMaxTokens];  // byte offsets of the slot's token rows in x
+    __shared__ int pair_s[kMaxTokens];      // the slot's pair ids
     constexpr int CPGX = XTile<XT>::kChunks;
     const int nrb = a.I / kGRows;
     const int u = blockIdx.x / nrb, rb = blockIdx.x % nrb;
-    if (u >= *a.nu) return;  // uniform over the block
+    // The slot count, the slot's pair count, weight pointers and pair ids (all in the
+    // workspace for every slot index of the grid) are read in one round before the exit test.
+    const int nu = *a.nu, cnt = a.u_count[u];
+    const uint64_t *t = a.u_ptrs + u * 6;
+    const uint64_t t0 = t[0], t1 = t[1], t2 = t[2], t3 = t[3];
+    const int pid = a.u_pairs[u * a.T + min(static_cast<int>(threadIdx.x), a.T - 1)];
+    asm volatile("" ::"s"(nu), "s"(cnt), "s"(t0), "s"(t1), "s"(t2), "s"(t3));
+    if (u >= nu) return;  // uniform over the block
+    __builtin_amdgcn_sched_barrier(0);  // pid's load ahead of the weight rows: its wait skips them
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
     const int GH = a.Hr >> 5, nch = GH * CPGX;
     const uint32_t rowA = static_cast<uint32_t>(a.Hr >> 1);
-    const int cnt = a.u_count[u];
-    const uint64_t *t = a.u_ptrs + u * 6;
-    const auto rg = make_rsrc(uniform_ptr(t[0]), static_cast<uint32_t>(a.I) * rowA);
-    const auto rgs = make_rsrc(uniform_ptr(t[1]), static_cast<uint32_t>(a.I * GH));
-    const auto ru = make_rsrc(uniform_ptr(t[2]), static_cast<uint32_t>(a.I) * rowA);
-    const auto rus = make_rsrc(uniform_ptr(t[3]), static_cast<uint32_t>(a.I * GH));
+    const auto rg = make_rsrc(uniform_ptr(t0), static_cast<uint32_t>(a.I) * rowA);
+    const auto rgs = make_rsrc(uniform_ptr(t1), static_cast<uint32_t>(a.I * GH));
+    const auto ru = make_rsrc(uniform_ptr(t2), static_cast<uint32_t>(a.I) * rowA);
+    const auto rus = make_rsrc(uniform_ptr(t3), static_cast<uint32_t>(a.I * GH));
     // the wave's weight rows, issued before anything is staged
     uint4 wg[kPairsPerWave][GA], wu[kPairsPerWave][GA];
     uint32_t sg[kPairsPerWave][GA], su[kPairsPerWave][GA];
@@ -159,22 +167,43 @@ __global__ __launch_bounds__(256) void multi_gateup_kernel(MultiArgs a) {
             const uint32_t soff = ok ? static_cast<uint32_t>(i * GH + g) : kOobOffset;
             wg[q][v] = buf_load16(rg, off);
             wu[q][v] = buf_load16(ru, off);
-            sg[q][v] = __builtin_amdgcn_raw_buffer_load_b8(rgs, soff, 0, 0);
-            su[q][v] = __builtin_amdgcn_raw_buffer_load_b8(rus, soff, 0, 0);
+            // the scale byte's aligned dword (the byte is picked out where it is used, so no
+            // widening of the loaded value is hoisted above the staging)
+            sg[q][v] = __builtin_amdgcn_raw_buffer_load_b32(rgs, ok ? soff & ~3u : kOobOffset, 0, 0);
+            su[q][v] = __builtin_amdgcn_raw_buffer_load_b32(rus, ok ? soff & ~3u : kOobOffset, 0, 0);
         }
     }
-    const char *xb = static_cast<const char *>(a.x);
-#pragma unroll 1
-    for (int c0 = 0; c0 < cnt; c0 += a.tb_x) {
-        const int nb = min(a.tb_x, cnt - c0);
-        if (c0 > 0) __syncthreads();  // every wave is done with the previous batch
-        for (int c = 0; c < nb; ++c) {
-            const int tok = a.u_pairs[u * a.T + c0 + c] / a.k;
-            stage_x_tile<XT>(smem + c * nch, xb + static_cast<int64_t>(tok) * a.Hr * sizeof(XT), nch);
+    // the slot's pair ids and the byte offsets of their token rows in x
+    if (static_cast<int>(threadIdx.x) < a.T) {
+        pair_s[threadIdx.x] = pid;
+        tok_s[threadIdx.x] = static_cast<uint32_t>(pid / a.k) * static_cast<uint32_t>(a.Hr * sizeof(XT));
+    }
+    const auto rx = make_rsrc(a.x, static_cast<uint32_t>(a.T * a.Hr * sizeof(XT)));
+    // four staging loads per thread in flight before their stores
+    auto stage4 = [&](int c0, int nb, int i0) {
+        uint4 v[4];
+        int dst[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int i = i0 + j * 256 + static_cast<int>(threadIdx.x);
+            const bool ok = i < nb * nch;
+            const int c = ok ? i / nch : 0, cc = ok ? i - c * nch : 0;
+            v[j] = buf_load16(rx, ok ? tok_s[c0 + c] + cc * 16u : kOobOffset);
+            dst[j] = ok ? c * nch + XTile<XT>::slot(cc / CPGX, cc % CPGX) : -1;
         }
-        __syncthreads();
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            if (dst[j] >= 0) smem[dst[j]] = v[j];
+    };
+    auto compute = [&](int c0, int nb) {
 #pragma unroll 1
         for (int c = 0; c < nb; ++c) {
+            // the scale bytes are picked out here, not hoisted above the staging (whose
+            // stores would then wait for every weight load)
+#pragma unroll
+            for (int q = 0; q < kPairsPerWave; ++q)
+#pragma unroll
+                for (int v = 0; v < GA; ++v) asm volatile("" : "+v"(sg[q][v]), "+v"(su[q][v]));
             const uint4 *xs = smem + c * nch;
             float accg[kPairsPerWave], accu[kPairsPerWave];
 #pragma unroll
@@ -188,12 +217,14 @@ __global__ __launch_bounds__(256) void multi_gateup_kernel(MultiArgs a) {
                     for (int q = 0; q < CPGX; ++q) xc[q] = reinterpret_cast<const XChunk<XT> *>(xs)[XTile<XT>::slot(g, q)];
 #pragma unroll
                     for (int q = 0; q < kPairsPerWave; ++q) {
-                        accg[q] = fmaf(group_dot(wg[q][v], xc), e8m0_to_f32(sg[q][v]), accg[q]);
-                        accu[q] = fmaf(group_dot(wu[q][v], xc), e8m0_to_f32(su[q][v]), accu[q]);
+                        const uint32_t sh =
+                            ((static_cast<uint32_t>(rb * kGRows + wave * kPairsPerWave + q) * GH + g) & 3u) * 8u;
+                        accg[q] = fmaf(group_dot(wg[q][v], xc), e8m0_to_f32((sg[q][v] >> sh) & 0xffu), accg[q]);
+                        accu[q] = fmaf(group_dot(wu[q][v], xc), e8m0_to_f32((su[q][v] >> sh) & 0xffu), accu[q]);
                     }
                 }
             }
-            const int pair = a.u_pairs[u * a.T + c0 + c];
+            const int pair = pair_s[c0 + c];
 #pragma unroll
             for (int q = 0; q < kPairsPerWave; ++q) {
                 const float gs = wave_sum_to_lane63(accg[q]);
@@ -202,6 +233,25 @@ __global__ __launch_bounds__(256) void multi_gateup_kernel(MultiArgs a) {
                 if (lane == 63) a.act[static_cast<int64_t>(pair) * a.I + i] = act_fn(gs, us, a.act_kind, a.beta, a.lbeta);
             }
         }
+    };
+    // The first batch straight-line (a batch of bf16 rows fits in one round of four loads),
+    // so the waits before its stores do not cover the weight rows still in flight; further
+    // batches (fp32 rows, or more tokens than tb_x) in a loop.
+    int nb = min(a.tb_x, cnt);
+    __syncthreads();  // pair_s, tok_s
+    stage4(0, nb, 0);
+#pragma unroll 1
+    for (int i0 = 4 * 256; i0 < nb * nch; i0 += 4 * 256) stage4(0, nb, i0);
+    __syncthreads();
+    compute(0, nb);
+#pragma unroll 1
+    for (int c0 = a.tb_x; c0 < cnt; c0 += a.tb_x) {
+        nb = min(a.tb_x, cnt - c0);
+        __syncthreads();  // every wave is done with the previous batch
+#pragma unroll 1
+        for (int i0 = 0; i0 < nb * nch; i0 += 4 * 256) stage4(c0, nb, i0);
+        __syncthreads();
+        compute(c0, nb);
     }
 }
 
@@ -220,28 +270,37 @@ __global__ __launch_bounds__(256, 2) void multi_down_kernel(MultiArgs a) {
     constexpr int AV = NA * 256 + 1; // staged float4 per pair (the last one is the sink)
     extern __shared__ float4 act_s[];  // [tb_act][AV]
     __shared__ uint32_t last_s;
+    __shared__ int pair_s[kMaxTokens];  // the slot's pair ids
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
     const int nR = (a.Hr + RB - 1) / RB;
     const int u = blockIdx.x / nR, rr = blockIdx.x % nR;
-    const int nu = *a.nu;
+    // the slot count, the slot's pair count and down pointers in one round before the exit
+    // test (every slot index of the grid has its entries in the workspace)
+    const int nu = *a.nu, cnt_u = a.u_count[u];
+    const uint64_t t4 = a.u_ptrs[u * 6 + 4], t5 = a.u_ptrs[u * 6 + 5];
+    const int pid = a.u_pairs[u * a.T + min(static_cast<int>(threadIdx.x), a.T - 1)];  // the slot's pair ids
+    asm volatile("" ::"s"(nu), "s"(cnt_u), "s"(t4), "s"(t5));
     // with no live pair at all, the blocks of slot 0 still count in and write zeros
     if (u >= max(nu, 1)) return;
-    const int cnt = u < nu ? a.u_count[u] : 0;
+    __builtin_amdgcn_sched_barrier(0);  // pid's load ahead of the weight rows: its wait skips them
+    const int cnt = u < nu ? cnt_u : 0;
     const int GI = a.I >> 5, P = a.I / S;
     const uint32_t rowB = static_cast<uint32_t>(a.I >> 1);
     const int n0 = rr * RB + wave * RW;
     uint32_t wd[RW][NP][ND];
     uint32_t sd[RW][NP];
-    if (cnt > 0) {
-        const uint64_t *t = a.u_ptrs + u * 6;
-        const auto rd = make_rsrc(uniform_ptr(t[4]), static_cast<uint32_t>(a.Hr) * rowB);
-        const auto rds = make_rsrc(uniform_ptr(t[5]), static_cast<uint32_t>(a.Hr * GI));
+    {
+        // issued on every path (a slot with no pairs loads out of range: zeros, no access),
+        // so the waits below count the same loads whatever the slot
+        const bool has = cnt > 0;
+        const auto rd = make_rsrc(has ? uniform_ptr(t4) : nullptr, has ? static_cast<uint32_t>(a.Hr) * rowB : 0u);
+        const auto rds = make_rsrc(has ? uniform_ptr(t5) : nullptr, has ? static_cast<uint32_t>(a.Hr * GI) : 0u);
 #pragma unroll
         for (int r = 0; r < RW; ++r)
 #pragma unroll
             for (int p = 0; p < NP; ++p) {
                 const int n = n0 + r, pc = p * 64 + lane;
-                const bool ok = n < a.Hr && pc < P;
+                const bool ok = has && n < a.Hr && pc < P;
                 const uint32_t off = ok ? static_cast<uint32_t>(n) * rowB + pc * (S / 2u) : kOobOffset;
                 if constexpr (S == 32) {
                     const uint4 v = buf_load16(rd, off);
@@ -250,16 +309,20 @@ __global__ __launch_bounds__(256, 2) void multi_down_kernel(MultiArgs a) {
                     const auto v = __builtin_amdgcn_raw_buffer_load_b64(rd, off, 0, 0);
                     wd[r][p][0] = v[0], wd[r][p][1] = v[1];
                 }
-                sd[r][p] = __builtin_amdgcn_raw_buffer_load_b8(
-                    rds, ok ? static_cast<uint32_t>(n * GI + pc * S / 32) : kOobOffset, 0, 0);
+                // the scale byte's aligned dword (picked out where it is used, so no widening
+                // of the loaded value is hoisted above the act staging)
+                sd[r][p] = __builtin_amdgcn_raw_buffer_load_b32(
+                    rds, ok ? static_cast<uint32_t>(n * GI + pc * S / 32) & ~3u : kOobOffset, 0, 0);
             }
     }
+    if (static_cast<int>(threadIdx.x) < a.T) pair_s[threadIdx.x] = pid;
+    __syncthreads();
 #pragma unroll 1
     for (int c0 = 0; c0 < cnt; c0 += a.tb_act) {
         const int nb = min(a.tb_act, cnt - c0);
         if (c0 > 0) __syncthreads();  // every wave is done with the previous batch
         for (int c = 0; c < nb; ++c) {
-            const int pair = a.u_pairs[u * a.T + c0 + c];
+            const int pair = pair_s[c0 + c];
             const auto ra = make_rsrc(a.act + static_cast<int64_t>(pair) * a.I, static_cast<uint32_t>(a.I) * 4u);
             float4 *dst = act_s + c * AV;
 #pragma unroll
@@ -280,21 +343,26 @@ __global__ __launch_bounds__(256, 2) void multi_down_kernel(MultiArgs a) {
 #pragma unroll
                 for (int q = 0; q < NC; ++q) av[p][q] = src[pc < P ? q * P + pc : NA * 256];
             }
-            const int pair = a.u_pairs[u * a.T + c0 + c];
+            const int pair = pair_s[c0 + c];
             // The packed weights stay packed across the token loop: without this, the
             // compiler hoists their fp4 -> fp32 conversion out of the loop (8 floats per
             // dword) and spills.  An empty asm that claims to modify them keeps it inside.
 #pragma unroll
             for (int r = 0; r < RW; ++r)
 #pragma unroll
-                for (int p = 0; p < NP; ++p)
+                for (int p = 0; p < NP; ++p) {
 #pragma unroll
                     for (int d = 0; d < ND; ++d) asm volatile("" : "+v"(wd[r][p][d]));
+                    asm volatile("" : "+v"(sd[r][p]));
+                }
 #pragma unroll
             for (int r = 0; r < RW; ++r) {
                 float acc = 0.f;
 #pragma unroll
-                for (int p = 0; p < NP; ++p) acc = fmaf(piece_dot<ND>(wd[r][p], av[p]), e8m0_to_f32(sd[r][p]), acc);
+                for (int p = 0; p < NP; ++p) {
+                    const uint32_t sh = (static_cast<uint32_t>((n0 + r) * GI + (p * 64 + lane) * S / 32) & 3u) * 8u;
+                    acc = fmaf(piece_dot<ND>(wd[r][p], av[p]), e8m0_to_f32((sd[r][p] >> sh) & 0xffu), acc);
+                }
                 const float tot = wave_sum_to_lane63(acc);
                 const int n = n0 + r;
                 if (lane == 63 && n < a.Hr)
