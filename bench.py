@@ -750,7 +750,13 @@ def counter_fields(rec):
     src = "profiles/counters.json" + ("" if COUNTERS_CURRENT else " (stale: measured on other kernel sources)")
     out = {"traffic": {"ratio": rec["traffic_ratio"], "counter_bytes": rec["counter_bytes"],
                        "algorithmic_bytes": rec["algorithmic_bytes"], "source": src,
-                       "current": bool(COUNTERS_CURRENT)}}
+                       "current": bool(COUNTERS_CURRENT)},
+           # each launch's mean kernel time (eager, under the profiler) and the HBM bytes its
+           # counters show, so the throughput of each launch stands beside the step's
+           "launches": [{"kernel": k["kernel"], "avg_us": k["avg_us"], "counter_bytes": k["bytes"],
+                         "GB/s": round(k["bytes"] / (k["avg_us"] * 1e-6) / 1e9, 1),
+                         "pct_hbm_peak": round(100 * k["bytes"] / (k["avg_us"] * 1e-6) / 1e9 / HBM_PEAK_GBS, 1)}
+                        for k in rec.get("kernels", []) if k.get("avg_us")]}
     m = rec.get("mfma")
     if m:
         u = {"mfma": m["type"], "executed_TFLOP/s": m["executed_TFLOP/s"],
