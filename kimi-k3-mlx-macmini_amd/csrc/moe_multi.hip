@@ -26,8 +26,13 @@
 //
 // The whole layer for T tokens (k3_moe_layer_decode_multi) adds the dense bf16 parts on R, a
 // row kernel for T tokens (4 waves, one row or one (gate, up) row pair per wave, the T input
-// rows staged in LDS once per block): the router logits with the shared gate/up rows in one
-// launch, the batched top-k (k3_moe_topk), U, G, the shared down rows, and D.
+// rows staged in LDS once per block; wide fp32 inputs take a persistent form that stages
+// them once per CU): the router logits with the shared gate/up rows in one launch, the
+// batched top-k (k3_moe_topk), U, G, the shared down rows, and D.
+//
+// Every launch issues its weight rows before it waits on anything else, and loads what it
+// stages in batches (every load of a batch issued before the first store), so a block's
+// staging overlaps its weight stream instead of following it.
 //
 // Every selected expert's gate, up and down bytes are read once per call, whatever the
 // number of tokens routed to it.  Deterministic: no float atomics, fixed orders.
