@@ -295,18 +295,31 @@ class MLAAttention:
         cache.length = pos + 1
         return out.reshape(1, 1, hidden), cache
 
+    # bytes of fp32 scores one query chunk of the multi-token form may hold (the scores and
+    # probabilities of a 2048-token prompt over a 32768-token cache at 64 heads would be 17 GB
+    # each if formed at once)
+    DENSE_SCORE_BYTES = 1 << 28
+
     def _dense(self, q, lat, rot, scale):
-        """Multi-token form (prefill): absorbed scores with the causal mask, fp32."""
+        """Multi-token form (prefill): absorbed scores with the causal mask, fp32, in query
+        chunks whose scores stay within DENSE_SCORE_BYTES (every query row's softmax is its
+        own, so the chunks are independent)."""
         nope = self.cfg.qk_nope_head_dim
         latf, rotf = lat.to(torch.float32), rot.to(torch.float32)
-        qa = q[..., :nope] @ self._wk32                              # [B, H, T, r]
-        s = (qa @ latf.unsqueeze(1).transpose(-1, -2).contiguous()
-             + q[..., nope:] @ rotf.unsqueeze(1).transpose(-1, -2).contiguous())
-        s = s * scale
-        Tq, Tk = s.shape[-2], s.shape[-1]
-        qi = torch.arange(Tk - Tq, Tk, device=s.device).reshape(-1, 1)
-        ki = torch.arange(Tk, device=s.device).reshape(1, -1)
-        s = s.masked_fill(ki > qi, float("-inf"))
-        p = torch.softmax(s, dim=-1)
-        ctx = p @ latf.unsqueeze(1)
-        return ctx @ self._wv32.transpose(-1, -2).contiguous()
+        latT = latf.unsqueeze(1).transpose(-1, -2).contiguous()      # [B, 1, r, Tk]
+        rotT = rotf.unsqueeze(1).transpose(-1, -2).contiguous()
+        wvT = self._wv32.transpose(-1, -2).contiguous()
+        B, H, Tq = q.shape[0], q.shape[1], q.shape[2]
+        Tk = latf.shape[1]
+        chunk = max(1, min(Tq, self.DENSE_SCORE_BYTES // max(1, B * H * Tk * 4)))
+        ki = torch.arange(Tk, device=q.device).reshape(1, -1)
+        outs = []
+        for t0 in range(0, Tq, chunk):
+            qc = q[:, :, t0:t0 + chunk]
+            qa = qc[..., :nope] @ self._wk32                          # [B, H, t, r]
+            s = (qa @ latT + qc[..., nope:] @ rotT) * scale
+            qi = torch.arange(Tk - Tq + t0, Tk - Tq + t0 + qc.shape[2], device=q.device).reshape(-1, 1)
+            s = s.masked_fill(ki > qi, float("-inf"))
+            p = torch.softmax(s, dim=-1)
+            outs.append((p @ latf.unsqueeze(1)) @ wvT)
+        return outs[0] if len(outs) == 1 else torch.cat(outs, dim=2)
