@@ -178,6 +178,37 @@ def test_routed_decode_errors():
                   ws.data_ptr(), ws.numel(), None)
 
 
+def test_routed_moe_fp32_wide_rows():
+    """fp32 hidden states too wide to stage in one batch (5 and 8 tokens x 4096 fp32: 80 and
+    128 KB): the router rows and the shared (gate, up) pairs run the persistent row kernel,
+    its plain set and its pair set, the shared down rows the batched one; against the fp64
+    layer."""
+    from k3hip.moe import MoEConfig, RoutedMoE
+    H, I, E, k, Is = 4096, 256, 32, 4, 512
+    rng = np.random.default_rng(97)
+    ex_np, ex_dev = host_experts(rng, E, H, I)
+    router_w = om.bf16_round((rng.standard_normal((E, H)) * 0.02).astype(np.float32))
+    shared = tuple(om.bf16_round((rng.standard_normal(sh) * 0.02).astype(np.float32))
+                   for sh in ((Is, H), (Is, H), (H, Is)))
+    w = {"gate.weight": torch.from_numpy(router_w).to(DEV).to(torch.bfloat16)}
+    for name, a in zip(("gate", "up", "down"), shared):
+        w[f"shared_experts.{name}_proj.weight"] = torch.from_numpy(a).to(DEV).to(torch.bfloat16)
+    cfg = MoEConfig(hidden_size=H, moe_intermediate_size=I, num_experts=E, num_experts_per_token=k,
+                    shared_intermediate_size=Is, router="softmax", activation="silu")
+    which = {"w1": 0, "w3": 1, "w2": 2}
+    moe = RoutedMoE(cfg, 0, w, lambda L, e, wh: ex_dev[e][which[wh]])
+    experts = {e: ex_np[e] for e in range(E)}
+    for T in (5, 8):
+        x32 = rng.standard_normal((T, H)).astype(np.float32)
+        y, r = moe(torch.from_numpy(x32).to(DEV), return_router=True)
+        idx, wts, _, _ = omoe.route_softmax(x32, router_w, k, True, 1.0)
+        assert np.array_equal(np.sort(r.expert_indices.cpu().numpy(), -1), np.sort(idx, -1))
+        want = omoe.moe_layer(x32, idx, wts, experts, shared, kind="silu")
+        rel = om.normwise_rel(y.float().cpu().numpy(), want)
+        print(f"fp32 x, T={T}, H={H}: rel={rel:.3e}")
+        assert rel <= TOL, rel
+
+
 @pytest.mark.parametrize("router,xdt,Is", [("softmax", torch.bfloat16, 512), ("sigmoid_bias", torch.float32, 0),
                                            ("sigmoid_bias", torch.bfloat16, 1024)])
 def test_routed_moe_few_tokens_and_prefill_dispatch(router, xdt, Is):
