@@ -51,8 +51,10 @@ constexpr int kMaxTopK = 16;
 constexpr int kMaxPairs = kMaxTokens * kMaxTopK;  // 128
 constexpr int kMaxExperts = 1024;
 constexpr size_t kCounterBytes = 4096;            // D's row-range arrival counters
-constexpr int kPairsPerWave = 2;                  // G: (gate, up) row pairs per wave
-constexpr int kGRows = 4 * kPairsPerWave;         // G: intermediate rows per block
+// G: (gate, up) row pairs per wave: four for rows of up to 4096 values (K3's latent width:
+// 134.7 -> 131.9 us per four-token step), two for wider rows (the 384-expert layer's 7168:
+// four pairs measured 87.4 -> 90.2 us)
+constexpr int g_pairs_per_wave(int GA) { return GA <= 2 ? 4 : 2; }
 // LDS bytes per block for the staged token batches: small, so that LDS does not cap the
 // blocks per CU below what the registers allow (the launches are bandwidth-bound)
 constexpr int kLdsBudgetG = 16384;
@@ -136,6 +138,8 @@ __global__ __launch_bounds__(256) void multi_union_kernel(MultiArgs a) {
 // GA: MXFP4 groups per lane over Hr (Hr <= 2048 * GA).
 template <typename XT, int GA>
 __global__ __launch_bounds__(256) void multi_gateup_kernel(MultiArgs a) {
+    constexpr int kPairsPerWave = g_pairs_per_wave(GA);
+    constexpr int kGRows = 4 * kPairsPerWave;  // intermediate rows per block
     extern __shared__ uint4 smem[];  // [tb_x][Hr / 8 (bf16) or Hr / 4 (fp32) chunks], swizzled
     __shared__ uint32_t tok_s[kMaxTokens];  // byte offsets of the slot's token rows in x
     __shared__ int pair_s[kMaxTokens];      // the slot's pair ids
@@ -891,7 +895,8 @@ int launch_union_gateup(MultiArgs &a, int n_slots, hipStream_t st) {
     const int GH = a.Hr / 32;
     const size_t xrow = static_cast<size_t>(a.Hr) * sizeof(XT);
     a.tb_x = static_cast<int>(std::max<size_t>(1, std::min<size_t>(a.T, kLdsBudgetG / xrow)));
-    const dim3 gg(static_cast<unsigned>(n_slots * (a.I / kGRows)));
+    const int GA = GH <= 64 ? 1 : (GH <= 128 ? 2 : 4);
+    const dim3 gg(static_cast<unsigned>(n_slots * (a.I / (4 * g_pairs_per_wave(GA)))));
     const size_t lds_g = static_cast<size_t>(a.tb_x) * xrow;
     if (GH <= 64)
         multi_gateup_kernel<XT, 1><<<gg, 256, lds_g, st>>>(a);
