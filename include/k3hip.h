@@ -188,9 +188,9 @@ int k3_moe_grouped_ffn(const void *x, int x_dtype, const int32_t *expert_idx, co
 
 /* ---- routed experts for a few decode tokens, each selected expert read once ---------------- */
 
-/* Workspace bytes k3_moe_routed_decode needs for T tokens (the union records, arrival
- * counters, fp32 act and down-row totals per (token, slot) pair).  No initialisation: every
- * call rewrites it, counters included. */
+/* Workspace bytes k3_moe_routed_decode needs for T tokens (the union records, fp32 act and
+ * down-row totals per (token, slot) pair).  No initialisation: every call rewrites what it
+ * reads. */
 int64_t k3_moe_routed_workspace_size(int64_t T, int64_t H, int64_t I, int64_t n_experts, int64_t top_k);
 
 /* y[t] = sum_j w[t, j] * expert_{idx[t, j]}(x[t]) for T <= 8 decode tokens, with each expert

@@ -6,29 +6,33 @@
 // tokens whose top-k holds e (h[ti]), run expert_forward on them together (the Metal kernel
 // takes M tokens per launch, grid (N, M, 1), mxfp4_matvec.py:89-95), scale each token's
 // output by its gate weight for e and add it into y.  A token is gathered once per expert,
-// with the weight of its first slot holding e (list.index, moe.py:121-122).  Here, three
+// with the weight of its first slot holding e (list.index, moe.py:121-122).  Here, four
 // stream-ordered launches and no host synchronisation:
 //
 //   U   one block: the union of the routed experts (distinct valid ids, ascending), each
 //       union slot's (token, slot) pairs -- one per token, the token's first slot holding
-//       the expert -- in token order, the slots' six weight pointers, a live flag per pair;
-//       it zeroes D's arrival counters.
-//   G   block (union slot u, 8 intermediate rows): each wave holds two (gate row, up row)
-//       pairs of u's expert in registers and reduces them against every token of u, whose
+//       the expert -- in token order, the slots' six weight pointers, a live flag per pair.
+//   G   block (union slot u, 16 or 8 intermediate rows): each wave holds four or two (gate
+//       row, up row) pairs of u's expert in registers and reduces them against every token of u, whose
 //       rows are staged in LDS (up to tb_x tokens at a time, in the swizzled group order of
 //       the batch-1 kernels) -> act[pair][i] = f(gate, up) in fp32.
 //   D   block (union slot u, 4 * RW output rows): the rows of u's down projection in
 //       registers, reduced against the act vector of each of u's pairs (staged in LDS, up to
 //       tb_act at a time, chunk-major as the layer's down launch stages one); the row totals
-//       per pair go to the workspace, and the last of a row range's blocks to finish combines
+//       per pair go to the workspace.
+//   C   one thread per output value:
 //       y[t] = yadd[t] + sum over the token's live slots j, in slot order, of w[t, j] * down_{t, j}
-//       (yadd: the shared expert's output of the whole-layer entry point, or nothing).
+//       (yadd: the shared expert's output of the whole-layer entry point, or nothing).  A
+//       launch of its own (the kernel boundary orders D's stores before its loads): combining
+//       in D's last block per row range cost every D block a wait for its stores and an
+//       arrival counter (without them K3's four-token D 94 -> 79 us, the 384-expert layer's
+//       62 -> 51 us, for a 4.7 us combine launch).
 //
 // The whole layer for T tokens (k3_moe_layer_decode_multi) adds the dense bf16 parts on R, a
 // row kernel for T tokens (4 waves, one row or one (gate, up) row pair per wave, the T input
 // rows staged in LDS once per block; wide fp32 inputs take a persistent form that stages
 // them once per CU): the router logits with the shared gate/up rows in one launch, the
-// batched top-k (k3_moe_topk), U, G, the shared down rows, and D.
+// batched top-k (k3_moe_topk), U, G, the shared down rows, D and C.
 //
 // Every launch issues its weight rows before it waits on anything else, and loads what it
 // stages in batches (every load of a batch issued before the first store), so a block's
@@ -50,7 +54,6 @@ constexpr int kMaxTokens = 8;
 constexpr int kMaxTopK = 16;
 constexpr int kMaxPairs = kMaxTokens * kMaxTopK;  // 128
 constexpr int kMaxExperts = 1024;
-constexpr size_t kCounterBytes = 4096;            // D's row-range arrival counters
 // G: (gate, up) row pairs per wave: four for rows of up to 4096 values (K3's latent width:
 // 134.7 -> 131.9 us per four-token step), two for wider rows (the 384-expert layer's 7168:
 // four pairs measured 87.4 -> 90.2 us)
@@ -71,9 +74,7 @@ struct MultiArgs {
     float beta, lbeta;
     int out_bf16;
     int tb_x, tb_act;        // tokens per staged batch in G and D
-    int n_ranges;            // D row ranges (one arrival counter each)
     // workspace records
-    uint32_t *counter;       // [n_ranges]
     int32_t *nu;             // [1] union size
     int32_t *u_count;        // [P] pairs of union slot u
     int32_t *u_pairs;        // [P][T] pair ids t * k + j of slot u, tokens ascending
@@ -99,27 +100,29 @@ __global__ __launch_bounds__(256) void multi_union_kernel(MultiArgs a) {
     if (p < a.P) {
         e = (v >= 0 && v < a.E) ? v : -1;
         const int t = p / a.k, j = p % a.k;
-        for (int jj = 0; jj < j; ++jj)
-            if (id_s[t * a.k + jj] == v) e = -1;  // an earlier slot of the token holds it
+        int dup = 0;  // an earlier slot of the token holds it
+#pragma unroll 8
+        for (int jj = 0; jj < j; ++jj) dup |= id_s[t * a.k + jj] == v;
+        if (dup) e = -1;
     }
     if (p < kMaxPairs) ex_s[p] = e;
     __syncthreads();
-    bool fst = false;
-    int pos = 0, cnt = 0;
-    if (e >= 0) {
-        fst = true;
-        for (int q = 0; q < a.P; ++q) {
-            if (ex_s[q] == e) {
-                if (q < p) fst = false, ++pos;
-                ++cnt;
-            }
-        }
+    // Scans over the pairs without branches, unrolled, so the LDS reads of a scan are in
+    // flight together (a branch per element made every read wait for the one before).
+    int pos = 0, cnt = 0;  // pairs of e before p; pairs of e
+#pragma unroll 8
+    for (int q = 0; q < a.P; ++q) {
+        const int m = ex_s[q] == e;
+        pos += m & (q < p);
+        cnt += m;
     }
+    const bool fst = e >= 0 && pos == 0;
     if (p < kMaxPairs) first_s[p] = fst;
     __syncthreads();
     if (e >= 0) {
         int slot = 0;  // distinct experts below e
-        for (int q = 0; q < a.P; ++q) slot += first_s[q] && ex_s[q] < e;
+#pragma unroll 8
+        for (int q = 0; q < a.P; ++q) slot += first_s[q] & (ex_s[q] < e);
         a.u_pairs[slot * a.T + pos] = p;
         if (fst) {
             a.u_count[slot] = cnt;
@@ -129,7 +132,6 @@ __global__ __launch_bounds__(256) void multi_union_kernel(MultiArgs a) {
         }
     }
     if (p < a.P) a.live[p] = e >= 0;
-    for (int c = p; c < a.n_ranges; c += 256) a.counter[c] = 0u;
     __syncthreads();
     if (p == 0) *a.nu = nu_s;
 }
@@ -278,7 +280,6 @@ __global__ __launch_bounds__(256, 2) void multi_down_kernel(MultiArgs a) {
     constexpr int NA = S * NP / 16;  // act float4 per thread and pair (I <= S * NP * 64)
     constexpr int AV = NA * 256 + 1; // staged float4 per pair (the last one is the sink)
     extern __shared__ float4 act_s[];  // [tb_act][AV]
-    __shared__ uint32_t last_s;
     __shared__ int pair_s[kMaxTokens];  // the slot's pair ids
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
     const int nR = (a.Hr + RB - 1) / RB;
@@ -289,27 +290,23 @@ __global__ __launch_bounds__(256, 2) void multi_down_kernel(MultiArgs a) {
     const uint64_t t4 = a.u_ptrs[u * 6 + 4], t5 = a.u_ptrs[u * 6 + 5];
     const int pid = a.u_pairs[u * a.T + min(static_cast<int>(threadIdx.x), a.T - 1)];  // the slot's pair ids
     asm volatile("" ::"s"(nu), "s"(cnt_u), "s"(t4), "s"(t5));
-    // with no live pair at all, the blocks of slot 0 still count in and write zeros
-    if (u >= max(nu, 1)) return;
+    if (u >= nu) return;  // uniform over the block
     __builtin_amdgcn_sched_barrier(0);  // pid's load ahead of the weight rows: its wait skips them
-    const int cnt = u < nu ? cnt_u : 0;
+    const int cnt = cnt_u;  // at least one pair in a union slot
     const int GI = a.I >> 5, P = a.I / S;
     const uint32_t rowB = static_cast<uint32_t>(a.I >> 1);
     const int n0 = rr * RB + wave * RW;
     uint32_t wd[RW][NP][ND];
     uint32_t sd[RW][NP];
     {
-        // issued on every path (a slot with no pairs loads out of range: zeros, no access),
-        // so the waits below count the same loads whatever the slot
-        const bool has = cnt > 0;
-        const auto rd = make_rsrc(has ? uniform_ptr(t4) : nullptr, has ? static_cast<uint32_t>(a.Hr) * rowB : 0u);
-        const auto rds = make_rsrc(has ? uniform_ptr(t5) : nullptr, has ? static_cast<uint32_t>(a.Hr * GI) : 0u);
+        const auto rd = make_rsrc(uniform_ptr(t4), static_cast<uint32_t>(a.Hr) * rowB);
+        const auto rds = make_rsrc(uniform_ptr(t5), static_cast<uint32_t>(a.Hr * GI));
 #pragma unroll
         for (int r = 0; r < RW; ++r)
 #pragma unroll
             for (int p = 0; p < NP; ++p) {
                 const int n = n0 + r, pc = p * 64 + lane;
-                const bool ok = has && n < a.Hr && pc < P;
+                const bool ok = n < a.Hr && pc < P;
                 const uint32_t off = ok ? static_cast<uint32_t>(n) * rowB + pc * (S / 2u) : kOobOffset;
                 if constexpr (S == 32) {
                     const uint4 v = buf_load16(rd, off);
@@ -374,46 +371,36 @@ __global__ __launch_bounds__(256, 2) void multi_down_kernel(MultiArgs a) {
                 }
                 const float tot = wave_sum_to_lane63(acc);
                 const int n = n0 + r;
-                if (lane == 63 && n < a.Hr)
-                    __hip_atomic_store(a.yrow + static_cast<int64_t>(pair) * a.Hr + n, tot, __ATOMIC_RELAXED,
-                                       __HIP_MEMORY_SCOPE_AGENT);
+                if (lane == 63 && n < a.Hr) a.yrow[static_cast<int64_t>(pair) * a.Hr + n] = tot;
             }
         }
     }
-    // The block counts itself done once its row stores (agent-scope atomic stores, written
-    // through to the coherence point) have completed; the last of the range's blocks runs an
-    // agent-scope acquire, resets the counter and combines.  U zeroed every counter.
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        uint32_t *ctr = a.counter + rr;
-        const uint32_t old = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        last_s = old + 1 == static_cast<uint32_t>(max(nu, 1));
-        if (last_s) {
-            __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-        }
+}
+
+// ------------------------------------------------------------------ C: combine
+// One thread per output value (token tk, row n), the token's slots in order.  Every load is
+// issued before the sum (slot indices past k are clamped and their terms dropped; a row total
+// of a pair that is not live was never written and is selected away, not multiplied by zero).
+__global__ __launch_bounds__(256) void multi_combine_kernel(MultiArgs a) {
+    const int64_t o = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+    if (o >= static_cast<int64_t>(a.T) * a.Hr) return;
+    const int tk = static_cast<int>(o / a.Hr), n = static_cast<int>(o % a.Hr);
+    float v[kMaxTopK], w[kMaxTopK];
+    int live[kMaxTopK];
+#pragma unroll
+    for (int j = 0; j < kMaxTopK; ++j) {
+        const int pair = tk * a.k + min(j, a.k - 1);
+        v[j] = a.yrow[static_cast<int64_t>(pair) * a.Hr + n];
+        w[j] = a.wts[pair];
+        live[j] = a.live[pair];
     }
-    __syncthreads();
-    if (!last_s) return;
-    for (int o = threadIdx.x; o < a.T * RB; o += 256) {
-        const int tk = o / RB, n = rr * RB + o % RB;
-        if (n >= a.Hr) continue;
-        float y = a.yadd ? a.yadd[static_cast<int64_t>(tk) * a.Hr + n] : 0.f;
-        for (int j = 0; j < a.k; ++j) {
-            const int pair = tk * a.k + j;
-            if (a.live[pair])
-                y = fmaf(a.wts[pair],
-                         __hip_atomic_load(a.yrow + static_cast<int64_t>(pair) * a.Hr + n, __ATOMIC_RELAXED,
-                                           __HIP_MEMORY_SCOPE_AGENT),
-                         y);
-        }
-        const int64_t oi = static_cast<int64_t>(tk) * a.Hr + n;
-        if (a.out_bf16)
-            static_cast<uint16_t *>(a.out)[oi] = f32_to_bf16(y);
-        else
-            static_cast<float *>(a.out)[oi] = y;
-    }
+    float y = a.yadd ? a.yadd[o] : 0.f;
+#pragma unroll
+    for (int j = 0; j < kMaxTopK; ++j) y = (j < a.k && live[j]) ? fmaf(w[j], v[j], y) : y;
+    if (a.out_bf16)
+        static_cast<uint16_t *>(a.out)[o] = f32_to_bf16(y);
+    else
+        static_cast<float *>(a.out)[o] = y;
 }
 
 // ------------------------------------------------------------------ R: dense rows, T tokens
@@ -863,7 +850,7 @@ int launch_rows_multi(MRowsArgs &r, hipStream_t st) {
 
 // ------------------------------------------------------------------ host side
 struct MultiWs {
-    size_t counter, nu, u_count, u_pairs, live, u_ptrs, act, yrow, total;
+    size_t nu, u_count, u_pairs, live, u_ptrs, act, yrow, total;
 };
 
 size_t up256(size_t v) { return (v + 255) & ~size_t(255); }
@@ -872,7 +859,6 @@ MultiWs multi_ws_layout(int64_t T, int64_t H, int64_t I, int64_t k) {
     const int64_t P = T * k;
     MultiWs L{};
     size_t o = 0;
-    L.counter = o, o += kCounterBytes;
     L.nu = o, o += 256;
     L.u_count = o, o += up256(P * 4);
     L.u_pairs = o, o += up256(P * T * 4);
@@ -907,9 +893,10 @@ int launch_union_gateup(MultiArgs &a, int n_slots, hipStream_t st) {
     return check_hip(hipGetLastError(), "moe routed decode: gate/up launch");
 }
 
+// D, then C
 int launch_down(MultiArgs &a, int n_slots, hipStream_t st) {
     const int GI = a.I / 32;
-    const dim3 gd(static_cast<unsigned>(n_slots * a.n_ranges));
+    const dim3 gd(static_cast<unsigned>(n_slots * cdiv(a.Hr, down_rows(GI))));
     auto down = [&](auto kern, int na) {
         const size_t per = (static_cast<size_t>(na) * 256 + 1) * 16;
         a.tb_act = static_cast<int>(std::max<size_t>(1, std::min<size_t>(a.T, kLdsBudgetD / per)));
@@ -921,7 +908,11 @@ int launch_down(MultiArgs &a, int n_slots, hipStream_t st) {
         down(multi_down_kernel<16, 3, 7>, 3);
     else
         down(multi_down_kernel<32, 2, 4>, 4);
-    return check_hip(hipGetLastError(), "moe routed decode: down launch");
+    int rc = check_hip(hipGetLastError(), "moe routed decode: down launch");
+    if (rc) return rc;
+    const int64_t n_out = static_cast<int64_t>(a.T) * a.Hr;
+    multi_combine_kernel<<<dim3(static_cast<unsigned>(cdiv(n_out, 256))), 256, 0, st>>>(a);
+    return check_hip(hipGetLastError(), "moe routed decode: combine launch");
 }
 
 template <typename XT>
@@ -967,8 +958,6 @@ int multi_args(MultiArgs &a, const void *x, int x_dtype, const int32_t *expert_i
     a.beta = beta;
     a.lbeta = linear_beta;
     a.out_bf16 = out_dtype == K3_BF16;
-    a.n_ranges = static_cast<int>(cdiv(H, down_rows(static_cast<int>(I / 32))));
-    a.counter = reinterpret_cast<uint32_t *>(w + L.counter);
     a.nu = reinterpret_cast<int32_t *>(w + L.nu);
     a.u_count = reinterpret_cast<int32_t *>(w + L.u_count);
     a.u_pairs = reinterpret_cast<int32_t *>(w + L.u_pairs);

@@ -262,8 +262,8 @@ def test_routed_moe_few_tokens_and_prefill_dispatch(router, xdt, Is):
 
 
 def test_layer_decode_multi_repeatable_and_bf16_out():
-    """The whole-layer multi-token entry point twice on one workspace (its counters reset by
-    the call itself): bit-identical; bf16 output is the fp32 output rounded."""
+    """The whole-layer multi-token entry point twice on one workspace (every record it reads
+    rewritten by the call itself): bit-identical; bf16 output is the fp32 output rounded."""
     from k3hip import _lib
     from k3hip import _torch as Tt
     from k3hip.moe import MoEConfig, RoutedMoE
