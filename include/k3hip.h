@@ -198,9 +198,9 @@ int64_t k3_moe_routed_workspace_size(int64_t T, int64_t H, int64_t I, int64_t n_
  *   x [T, H] bf16 or fp32 (x_dtype); expert_idx int32 [T, top_k]; expert_w f32 [T, top_k];
  *   expert_table as in k3_moe_layer_decode; out [T, H] f32 or bf16.
  * A token is gathered once per expert, with the weight of its first slot holding it; ids
- * outside 0..n_experts-1 contribute nothing.  Three stream-ordered launches (the union of the
+ * outside 0..n_experts-1 contribute nothing.  Four stream-ordered launches (the union of the
  * routed experts on the device, the gate/up rows of every union expert against its tokens,
- * its down rows with a fixed-order combine), no host synchronisation, fp32 accumulation,
+ * its down rows, a fixed-order combine), no host synchronisation, fp32 accumulation,
  * deterministic.  H and I multiples of 128, H <= 8192, I <= 4096, top_k <= 16,
  * n_experts <= 1024.
  * Replaces the per-expert dispatch loop of LatentMoE.__call__ (air_llm/models/kimi_k3/moe.py:
@@ -227,7 +227,7 @@ int k3_moe_layer_multi_workspace_offsets(int64_t T, int64_t H, int64_t I, int64_
  * rows and the shared gate/up rows against all T tokens in one launch (bf16 rows, exact
  * products, fp32 accumulation), the batched top-k (as k3_moe_topk), the routed experts as in
  * k3_moe_routed_decode (every expert any token selects read once for all the tokens routed to
- * it), the shared down rows, and the fixed-order combine with the shared output: six
+ * it), the shared down rows, and the fixed-order combine with the shared output: seven
  * stream-ordered launches, no host synchronisation.  Arguments as k3_moe_layer_decode, plus T;
  * shared_I a multiple of 128, <= 8192.
  * Replaces LatentMoE.__call__ (air_llm/models/kimi_k3/moe.py:110-132, without the latent
@@ -258,7 +258,7 @@ int k3_moe_latent_layer_multi_workspace_offsets(int64_t T, int64_t H, int64_t la
  * sigmoid + bias top-k, the routed experts on h at the latent width as in
  * k3_moe_routed_decode (every selected expert read once for all its tokens), the shared down
  * rows, and the up projection rows against rmsnorm(routed sum) * latent_norm with the shared
- * output added: seven stream-ordered launches, no host synchronisation.  Arguments as
+ * output added: eight stream-ordered launches, no host synchronisation.  Arguments as
  * k3_moe_latent_layer_decode, plus T; shared_I a multiple of 128, <= 8192.
  * Replaces LatentMoE.__call__ (air_llm/models/kimi_k3/moe.py:110-132) for a decode batch of T
  * tokens, including the latent down/norm/up wrapper (moe.py:116,129-130). */

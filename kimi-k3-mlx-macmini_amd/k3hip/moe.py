@@ -421,7 +421,7 @@ class LatentMoE:
     KimiRMSNorm of their weighted sum in fp32; the up projection in fp32; plus the shared
     expert on the original x.  With ``fused=True`` and bf16 dense weights, one token runs
     k3_moe_latent_layer_decode (four launches), 2..DECODE_TOKENS tokens
-    k3_moe_latent_layer_decode_multi (seven launches, every selected expert read once for
+    k3_moe_latent_layer_decode_multi (eight launches, every selected expert read once for
     all its tokens) and more tokens run the routed experts grouped by expert
     (k3_moe_grouped_ffn); none synchronises with the host.  ``fused=False`` or fp32 dense
     weights run the reference's structure (``RoutedMoE`` describes it)."""
@@ -635,9 +635,9 @@ def moe_routed_decode(x: torch.Tensor, expert_indices: torch.Tensor, expert_weig
                       validate: bool = True) -> torch.Tensor:
     """Routed experts for a few decode tokens: x [T, H] (T <= 8, bf16 or fp32),
     expert_indices / expert_weights [T, k] -> [T, H].  The per-expert loop of
-    LatentMoE.__call__ (moe.py:119-127) as three launches (k3_moe_routed_decode): the union
+    LatentMoE.__call__ (moe.py:119-127) as four launches (k3_moe_routed_decode): the union
     of the routed experts on the device, then every union expert's gate/up and down rows
-    streamed once against all the tokens routed to it.  ``validate`` checks the ids on the
+    streamed once against all the tokens routed to it, then the fixed-order combine.  ``validate`` checks the ids on the
     device first (one small device->host copy); unchecked, out-of-range ids contribute
     nothing."""
     if x.dim() != 2 or expert_indices.shape != expert_weights.shape or expert_indices.shape[0] != x.shape[0]:
