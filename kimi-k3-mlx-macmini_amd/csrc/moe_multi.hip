@@ -434,9 +434,10 @@ struct MRowsArgs {
 constexpr int kRowWaves = 4;
 // small enough that LDS allows more blocks per CU than the registers do (three at 133 VGPRs)
 constexpr int kLdsBudgetR = 32768;
-// 16-byte staging loads per thread and batch: a batch is at most max(kLdsBudgetR, one row of
-// 8192 fp32) bytes
-constexpr int kStageR = 32768 / 16 / (64 * kRowWaves);
+// 16-byte staging loads per thread and batch for a block of NW waves: kLdsBudgetR for four
+// waves, 2 kLdsBudgetR for eight; a batch also always holds one row of 8192 fp32 (32 KB)
+constexpr int stage_loads(int NW) { return (NW == kRowWaves ? kLdsBudgetR : 2 * kLdsBudgetR) / (16 * 64 * NW); }
+constexpr size_t stage_bytes(int NW) { return static_cast<size_t>(stage_loads(NW)) * 16 * 64 * NW; }
 
 // 8 bf16 weights . 8 bf16 inputs (exact products)
 __device__ __forceinline__ float rdot(uint4 w, const uint4 *x, int c, float acc) {
@@ -461,12 +462,58 @@ __device__ __forceinline__ float rdot(uint4 w, const float4 *x, int c, float acc
     return acc;
 }
 
+// KimiRMSNorm, in place, of nb staged fp32 rows of K values (cpr float4 each):
+// row * (1 / sqrt(mean(row^2) + eps)) * nw.  The rows' sums of squares (each thread over its
+// chunks in order, then the wave, then the NW waves in order) meet at one barrier, and the
+// thread's norm weights load once, all in flight together, for every row.  red: [kMaxTokens][NW].
+// CH: the kernel's weight chunks per lane (K <= 512 CH, so a row holds at most 128 CH float4).
+template <int NW, int CH>
+__device__ __forceinline__ void norm_rows(float4 *x4, int nb, int cpr, int K, const float *nw, float eps,
+                                          float (*red)[NW]) {
+    constexpr int NT = 64 * NW;
+    constexpr int NG = (128 * CH + NT - 1) / NT;  // norm-weight chunks per thread
+    const int tid = static_cast<int>(threadIdx.x), lane = tid & 63, wave = tid >> 6;
+    const auto rnw = make_rsrc(nw, static_cast<uint32_t>(K) * 4u);
+    float4 g[NG];
+#pragma unroll
+    for (int j = 0; j < NG; ++j) g[j] = __builtin_bit_cast(float4, buf_load16(rnw, static_cast<uint32_t>(j * NT + tid) * 16u));
+#pragma unroll 1
+    for (int c = 0; c < nb; ++c) {
+        float ss = 0.f;
+        for (int i = tid; i < cpr; i += NT) {
+            const float4 v = x4[c * cpr + i];
+            ss = fmaf(v.x, v.x, fmaf(v.y, v.y, fmaf(v.z, v.z, fmaf(v.w, v.w, ss))));
+        }
+        ss = wave_sum_all(ss);
+        if (lane == 0) red[c][wave] = ss;
+    }
+    __syncthreads();
+#pragma unroll 1
+    for (int c = 0; c < nb; ++c) {
+        float tot = red[c][0];
+#pragma unroll
+        for (int w = 1; w < NW; ++w) tot += red[c][w];
+        const float rs = 1.0f / sqrtf(tot / static_cast<float>(K) + eps);
+#pragma unroll
+        for (int j = 0; j < NG; ++j) {
+            const int i = j * NT + tid;
+            if (i < cpr) {
+                float4 v = x4[c * cpr + i];
+                v.x = v.x * rs * g[j].x, v.y = v.y * rs * g[j].y, v.z = v.z * rs * g[j].z, v.w = v.w * rs * g[j].w;
+                x4[c * cpr + i] = v;
+            }
+        }
+    }
+    __syncthreads();
+}
+
 // IT: input element type (uint16_t = bf16, float); CH: 16-byte weight chunks per lane (K <= 512 CH);
-// R: plain rows per wave (narrow rows take several, so one staged batch serves more rows).
-template <typename IT, int CH, int R>
-__global__ __launch_bounds__(256) void multi_rows_kernel(MRowsArgs a) {
+// R: plain rows per wave (narrow rows take several, so one staged batch serves more rows);
+// NW: waves per block (4, or 8 to stage inputs of up to twice kLdsBudgetR in one batch).
+template <typename IT, int CH, int R, int NW>
+__global__ __launch_bounds__(64 * NW) void multi_rows_kernel(MRowsArgs a) {
     extern __shared__ uint4 xs[];  // [tb][K * sizeof(IT) / 16]
-    __shared__ float red[kRowWaves];
+    __shared__ float red[kMaxTokens][NW];
     using XC = typename std::conditional<std::is_same<IT, float>::value, float4, uint4>::type;
     constexpr int NR = R > 2 ? R : 2;  // weight rows held per wave (a pair needs two)
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
@@ -474,7 +521,7 @@ __global__ __launch_bounds__(256) void multi_rows_kernel(MRowsArgs a) {
     while (s < kPlainSets && b >= a.blocks[s]) b -= a.blocks[s++];
     const bool pair = s == kPlainSets;  // uniform
     const int nrows = pair ? 2 : R;    // rows this wave reduces
-    const int n0 = pair ? b * kRowWaves + wave : (b * kRowWaves + wave) * R;
+    const int n0 = pair ? b * NW + wave : (b * NW + wave) * R;
     const int N = pair ? a.N1 : a.N[s];
     const int nch = a.K >> 3;
     const uint32_t rowb = static_cast<uint32_t>(a.K) * 2u;
@@ -502,40 +549,21 @@ __global__ __launch_bounds__(256) void multi_rows_kernel(MRowsArgs a) {
         {
             // every load of the batch issued before the stores (past the end: zeros, no access)
             const auto rin = make_rsrc(in4 + static_cast<int64_t>(c0) * cpr, static_cast<uint32_t>(nb * cpr) * 16u);
-            uint4 v[kStageR];
+            constexpr int kSt = stage_loads(NW);
+            uint4 v[kSt];
 #pragma unroll
-            for (int j = 0; j < kStageR; ++j)
-                v[j] = buf_load16(rin, static_cast<uint32_t>(j * 64 * kRowWaves + static_cast<int>(threadIdx.x)) * 16u);
+            for (int j = 0; j < kSt; ++j)
+                v[j] = buf_load16(rin, static_cast<uint32_t>(j * 64 * NW + static_cast<int>(threadIdx.x)) * 16u);
 #pragma unroll
-            for (int j = 0; j < kStageR; ++j) {
-                const int i = j * 64 * kRowWaves + static_cast<int>(threadIdx.x);
+            for (int j = 0; j < kSt; ++j) {
+                const int i = j * 64 * NW + static_cast<int>(threadIdx.x);
                 if (i < nb * cpr) xs[i] = v[j];
             }
         }
         __syncthreads();
         if constexpr (std::is_same<IT, float>::value) {
             if (a.nw) {
-                // KimiRMSNorm of each staged row: row * (1 / sqrt(mean(row^2) + eps)) * nw
-                float4 *x4 = reinterpret_cast<float4 *>(xs);
-                for (int c = 0; c < nb; ++c) {
-                    float ss = 0.f;
-                    for (int i = threadIdx.x; i < cpr; i += 64 * kRowWaves) {
-                        const float4 v = x4[c * cpr + i];
-                        ss = fmaf(v.x, v.x, fmaf(v.y, v.y, fmaf(v.z, v.z, fmaf(v.w, v.w, ss))));
-                    }
-                    ss = wave_sum_all(ss);
-                    if (lane == 0) red[wave] = ss;
-                    __syncthreads();
-                    const float tot = ((red[0] + red[1]) + red[2]) + red[3];
-                    const float rs = 1.0f / sqrtf(tot / static_cast<float>(a.K) + a.eps);
-                    for (int i = threadIdx.x; i < cpr; i += 64 * kRowWaves) {
-                        const float4 g = reinterpret_cast<const float4 *>(a.nw)[i];
-                        float4 v = x4[c * cpr + i];
-                        v.x = v.x * rs * g.x, v.y = v.y * rs * g.y, v.z = v.z * rs * g.z, v.w = v.w * rs * g.w;
-                        x4[c * cpr + i] = v;
-                    }
-                    __syncthreads();
-                }
+                norm_rows<NW, CH>(reinterpret_cast<float4 *>(xs), nb, cpr, a.K, a.nw, a.eps, red);
             }
         }
 #pragma unroll 1
@@ -643,7 +671,7 @@ __device__ __forceinline__ void load_row(uint4 (&w)[CH], __amdgpu_buffer_rsrc_t 
 template <typename IT, int CH>
 __global__ __launch_bounds__(64 * kLoopWaves) void multi_rows_loop_kernel(MRowsArgs a) {
     extern __shared__ uint4 xs[];  // [T][K * sizeof(IT) / 16]
-    __shared__ float red[kLoopWaves];
+    __shared__ float red[kMaxTokens][kLoopWaves];
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
     const int gw = static_cast<int>(blockIdx.x) * kLoopWaves + wave;
     const int nch = a.K >> 3, T = a.T;
@@ -683,29 +711,7 @@ __global__ __launch_bounds__(64 * kLoopWaves) void multi_rows_loop_kernel(MRowsA
     __syncthreads();
     if constexpr (std::is_same<IT, float>::value) {
         if (a.nw) {
-            // KimiRMSNorm of each staged row: row * (1 / sqrt(mean(row^2) + eps)) * nw
-            float4 *x4 = reinterpret_cast<float4 *>(xs);
-            for (int t = 0; t < T; ++t) {
-                float ss = 0.f;
-                for (int i = threadIdx.x; i < cpr; i += 64 * kLoopWaves) {
-                    const float4 v = x4[t * cpr + i];
-                    ss = fmaf(v.x, v.x, fmaf(v.y, v.y, fmaf(v.z, v.z, fmaf(v.w, v.w, ss))));
-                }
-                ss = wave_sum_all(ss);
-                if (lane == 0) red[wave] = ss;
-                __syncthreads();
-                float tot = red[0];
-#pragma unroll
-                for (int w = 1; w < kLoopWaves; ++w) tot += red[w];
-                const float rs = 1.0f / sqrtf(tot / static_cast<float>(a.K) + a.eps);
-                for (int i = threadIdx.x; i < cpr; i += 64 * kLoopWaves) {
-                    const float4 g = reinterpret_cast<const float4 *>(a.nw)[i];
-                    float4 v = x4[t * cpr + i];
-                    v.x = v.x * rs * g.x, v.y = v.y * rs * g.y, v.z = v.z * rs * g.z, v.w = v.w * rs * g.w;
-                    x4[t * cpr + i] = v;
-                }
-                __syncthreads();
-            }
+            norm_rows<kLoopWaves, CH>(reinterpret_cast<float4 *>(xs), T, cpr, a.K, a.nw, a.eps, red);
         }
     }
 
@@ -801,6 +807,19 @@ int launch_rows_loop(MRowsArgs &r, size_t lds, hipStream_t st) {
     return check_hip(hipGetLastError(), "moe layer (T tokens): dense rows launch");
 }
 
+// the eight-wave form of multi_rows_kernel: its static LDS and up to 2 kLdsBudgetR of
+// dynamic LDS pass the 64 KB default, so each instance opts in once
+template <typename IT, int CH, int R, int NW>
+int launch_rows_wide(MRowsArgs &r, dim3 g, size_t lds, hipStream_t st) {
+    static const hipError_t lds_rc = hipFuncSetAttribute(reinterpret_cast<const void *>(&multi_rows_kernel<IT, CH, R, NW>),
+                                                         hipFuncAttributeMaxDynamicSharedMemorySize,
+                                                         2 * kLdsBudgetR);
+    const int rc = check_hip(lds_rc, "moe layer (T tokens): dense rows LDS size");
+    if (rc) return rc;
+    multi_rows_kernel<IT, CH, R, NW><<<g, 64 * NW, lds, st>>>(r);
+    return check_hip(hipGetLastError(), "moe layer (T tokens): dense rows launch");
+}
+
 template <typename IT>
 int launch_rows_multi(MRowsArgs &r, hipStream_t st) {
     if (r.nw && !std::is_same<IT, float>::value)
@@ -823,28 +842,39 @@ int launch_rows_multi(MRowsArgs &r, hipStream_t st) {
         if (ch <= 14) return launch_rows_loop<IT, 14>(r, lds, st);
         return launch_rows_loop<IT, 16>(r, lds, st);
     }
-    r.tb = static_cast<int>(std::max<size_t>(1, std::min<size_t>(r.T, kLdsBudgetR / row)));
     const int ch = static_cast<int>(cdiv(r.K / 8, 64));
+    if (ch > 16) return set_error(K3_ERR_SHAPE, "moe layer (T tokens): row width %d above 8192", r.K);
+    // inputs that need two batches of kLdsBudgetR take one batch in blocks of eight waves where
+    // the registers leave room for two such blocks per CU (up to 128 VGPRs: CH <= 8; K3's
+    // normalised latent up rows at four tokens: 28 -> 23.6 us).  Wider rows keep four-wave
+    // blocks and two batches: one batch in six-wave blocks at three waves per SIMD measured
+    // slower (K3's router, latent down and shared gate/up rows at four tokens: 65 -> 90 us).
+    const bool wide = ch <= 8 && in_bytes > static_cast<size_t>(kLdsBudgetR) && in_bytes <= stage_bytes(8);
+    const int nw = wide ? 8 : kRowWaves;
+    r.tb = static_cast<int>(std::max<size_t>(1, std::min<size_t>(r.T, stage_bytes(nw) / row)));
     const int R = ch <= 4 ? 4 : (ch <= 8 ? 2 : 1);
     int blocks = 0;
     for (int s = 0; s < kPlainSets; ++s) {
-        r.blocks[s] = r.w[s] ? static_cast<int>(cdiv(r.N[s], kRowWaves * R)) : 0;
+        r.blocks[s] = r.w[s] ? static_cast<int>(cdiv(r.N[s], nw * R)) : 0;
         blocks += r.blocks[s];
     }
-    blocks += r.wg ? static_cast<int>(cdiv(r.N1, kRowWaves)) : 0;
+    blocks += r.wg ? static_cast<int>(cdiv(r.N1, nw)) : 0;
     if (blocks == 0) return K3_OK;
     const size_t lds = static_cast<size_t>(r.tb) * row;
     const dim3 g(static_cast<unsigned>(blocks));
-    if (ch <= 4)
-        multi_rows_kernel<IT, 4, 4><<<g, 64 * kRowWaves, lds, st>>>(r);
-    else if (ch <= 8)
-        multi_rows_kernel<IT, 8, 2><<<g, 64 * kRowWaves, lds, st>>>(r);
-    else if (ch <= 14)
-        multi_rows_kernel<IT, 14, 1><<<g, 64 * kRowWaves, lds, st>>>(r);
-    else if (ch <= 16)
-        multi_rows_kernel<IT, 16, 1><<<g, 64 * kRowWaves, lds, st>>>(r);
-    else
-        return set_error(K3_ERR_SHAPE, "moe layer (T tokens): row width %d above 8192", r.K);
+    if (wide) {
+        if (ch <= 4) return launch_rows_wide<IT, 4, 4, 8>(r, g, lds, st);
+        return launch_rows_wide<IT, 8, 2, 8>(r, g, lds, st);
+    } else {
+        if (ch <= 4)
+            multi_rows_kernel<IT, 4, 4, kRowWaves><<<g, 64 * kRowWaves, lds, st>>>(r);
+        else if (ch <= 8)
+            multi_rows_kernel<IT, 8, 2, kRowWaves><<<g, 64 * kRowWaves, lds, st>>>(r);
+        else if (ch <= 14)
+            multi_rows_kernel<IT, 14, 1, kRowWaves><<<g, 64 * kRowWaves, lds, st>>>(r);
+        else
+            multi_rows_kernel<IT, 16, 1, kRowWaves><<<g, 64 * kRowWaves, lds, st>>>(r);
+    }
     return check_hip(hipGetLastError(), "moe layer (T tokens): dense rows launch");
 }
 

@@ -152,6 +152,15 @@ def test_latent_moe_few_tokens_wide_rows(T):
                 num_experts_per_token=4), seed=60 + T, T=T)
 
 
+@pytest.mark.parametrize("T", [3, 4])
+def test_latent_moe_few_tokens_wide_hidden(T):
+    """bf16 hidden states of width 7168 at three and four tokens (43 / 57 KB: two staged
+    batches) feeding the router, latent down and shared gate/up rows together; the latent
+    state (fp32 [T, 1024]) stages in one batch."""
+    check(K3Cfg(hidden_size=7168, routed_expert_hidden_size=1024, moe_intermediate_size=512, num_experts=16,
+                num_experts_per_token=4), seed=70 + T, T=T)
+
+
 K3_CFG = dict(hidden_size=7168, routed_expert_hidden_size=3584, moe_intermediate_size=3072, num_experts=896,
               num_experts_per_token=16)
 
