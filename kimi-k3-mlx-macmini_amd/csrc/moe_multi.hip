@@ -42,6 +42,7 @@
 // number of tokens routed to it.  Deterministic: no float atomics, fixed orders.
 #include <algorithm>
 #include <atomic>
+#include <mutex>
 #include <type_traits>
 
 #include "moe_common.h"
@@ -903,11 +904,13 @@ MultiWs multi_ws_layout(int64_t T, int64_t H, int64_t I, int64_t k) {
 // Rows per D block for the intermediate width's groups GI (as the layer's down launch).
 int down_rows(int GI) { return GI <= 64 ? 4 * 14 : (GI <= 96 ? 4 * 7 : 4 * 4); }
 
-template <typename XT>
-int launch_union_gateup(MultiArgs &a, int n_slots, hipStream_t st) {
+int launch_union(MultiArgs &a, hipStream_t st) {
     multi_union_kernel<<<1, 256, 0, st>>>(a);
-    int rc = check_hip(hipGetLastError(), "moe routed decode: union launch");
-    if (rc) return rc;
+    return check_hip(hipGetLastError(), "moe routed decode: union launch");
+}
+
+template <typename XT>
+int launch_gateup(MultiArgs &a, int n_slots, hipStream_t st) {
     const int GH = a.Hr / 32;
     const size_t xrow = static_cast<size_t>(a.Hr) * sizeof(XT);
     a.tb_x = static_cast<int>(std::max<size_t>(1, std::min<size_t>(a.T, kLdsBudgetG / xrow)));
@@ -945,9 +948,60 @@ int launch_down(MultiArgs &a, int n_slots, hipStream_t st) {
     return check_hip(hipGetLastError(), "moe routed decode: combine launch");
 }
 
+// The shared expert's down rows depend only on the first launch (R), so the latent layer's
+// entry point runs them on a side stream, beside the top-k, U, G and D launches on the
+// caller's stream: the few-block top-k and union launches leave most CUs idle.  One side
+// stream and a fork / join event pair per device, created on the device's first such call
+// (default priority, non-blocking) and kept until the process ends.  A call holds side_mutex
+// while it enqueues, so calls from several host threads cannot interleave their records and
+// waits on the shared events; under stream capture the side stream joins the capture at the
+// fork and leaves it at the join.
+struct SideLane {
+    hipStream_t s = nullptr;
+    hipEvent_t fork = nullptr, join = nullptr;
+};
+std::mutex side_mutex;
+
+// lane: the current device's side lane, or null when it does not exist yet and st is
+// capturing (creating a stream or an event is not a capturable call; the caller then runs
+// the rows in st).
+int side_lane(SideLane *&lane, hipStream_t st) {
+    constexpr int kDevs = 64;
+    static SideLane lanes[kDevs];
+    lane = nullptr;
+    int dev = 0;
+    int rc = check_hip(hipGetDevice(&dev), "moe layer (T tokens): device query");
+    if (rc) return rc;
+    if (dev < 0 || dev >= kDevs) return set_error(K3_ERR_SHAPE, "moe layer (T tokens): device %d", dev);
+    SideLane &l = lanes[dev];
+    if (!l.s) {
+        hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+        rc = check_hip(hipStreamIsCapturing(st, &cs), "moe layer (T tokens): capture query");
+        if (rc || cs != hipStreamCaptureStatusNone) return rc;
+        SideLane n;
+        rc = check_hip(hipStreamCreateWithFlags(&n.s, hipStreamNonBlocking), "moe layer (T tokens): side stream");
+        if (!rc) rc = check_hip(hipEventCreateWithFlags(&n.fork, hipEventDisableTiming), "moe layer (T tokens): event");
+        if (!rc) rc = check_hip(hipEventCreateWithFlags(&n.join, hipEventDisableTiming), "moe layer (T tokens): event");
+        if (rc) return rc;
+        l = n;
+    }
+    lane = &l;
+    return K3_OK;
+}
+
+// Fork the side stream from st, run the shared down rows d on it, and record the join event.
+int shared_down_side(MRowsArgs &d, hipStream_t st, SideLane &l) {
+    int rc = check_hip(hipEventRecord(l.fork, st), "moe layer (T tokens): fork");
+    if (!rc) rc = check_hip(hipStreamWaitEvent(l.s, l.fork, 0), "moe layer (T tokens): fork");
+    if (!rc) rc = launch_rows_multi<float>(d, l.s);
+    if (!rc) rc = check_hip(hipEventRecord(l.join, l.s), "moe layer (T tokens): join");
+    return rc;
+}
+
 template <typename XT>
 int launch_multi(MultiArgs &a, int n_slots, hipStream_t st) {
-    const int rc = launch_union_gateup<XT>(a, n_slots, st);
+    int rc = launch_union(a, st);
+    if (!rc) rc = launch_gateup<XT>(a, n_slots, st);
     return rc ? rc : launch_down(a, n_slots, st);
 }
 
@@ -1127,10 +1181,14 @@ extern "C" int k3_moe_layer_decode_multi(const void *x, int x_dtype, const void 
                      stream);
     if (rc) return rc;
     const int n_slots = static_cast<int>(std::min<int64_t>(a.P, n_experts));
-    rc = bf ? launch_union_gateup<uint16_t>(a, n_slots, st) : launch_union_gateup<float>(a, n_slots, st);
+    rc = launch_union(a, st);
+    if (!rc) rc = bf ? launch_gateup<uint16_t>(a, n_slots, st) : launch_gateup<float>(a, n_slots, st);
     if (rc) return rc;
     if (has_shared) {
-        // the shared down rows [H, shared_I] against the fp32 act -> [T, H], added in D's combine
+        // the shared down rows [H, shared_I] against the fp32 act -> [T, H], added in C (in
+        // this stream between G and D: on a side stream from R on, beside the top-k, U, G
+        // and D, these 29 MB rows slowed those launches by more than their own 16 us at the
+        // 384-expert layer's four tokens, 178.4 -> 180.3 us)
         MRowsArgs d{};
         d.in = act_sh;
         d.T = a.T;
@@ -1232,15 +1290,16 @@ extern "C" int k3_moe_latent_layer_decode_multi(const void *x, int x_dtype, cons
     r.lbeta = linear_beta;
     rc = bf ? launch_rows_multi<uint16_t>(r, st) : launch_rows_multi<float>(r, st);
     if (rc) return rc;
-    // sigmoid + bias routing (moe.py:65-76) on the logits
-    rc = k3_moe_topk(logits, a.E, a.T, a.E, static_cast<const float *>(router_bias), K3_ROUTE_SIGMOID_BIAS,
-                     renormalize, scaling, a.k, idx, wts, reinterpret_cast<float *>(w + L.scores),
-                     reinterpret_cast<float *>(w + L.corrected), stream);
-    if (rc) return rc;
-    const int n_slots = static_cast<int>(std::min<int64_t>(a.P, n_experts));
-    rc = bf ? launch_union_gateup<uint16_t>(a, n_slots, st) : launch_union_gateup<float>(a, n_slots, st);
-    if (rc) return rc;
+    std::unique_lock<std::mutex> lock(side_mutex, std::defer_lock);
+    SideLane *side = nullptr;
     if (has_shared) {
+        // the shared down rows (88 MB at K3's shapes, the persistent row form) on the side
+        // stream from here on, beside the top-k, U, G and D launches; R3 adds their output.
+        // K3's four-token step 338 -> 325 us; forked after U instead (beside G and D only):
+        // 337 us
+        lock.lock();
+        rc = side_lane(side, st);
+        if (rc) return rc;
         MRowsArgs d{};
         d.in = act_sh;
         d.T = a.T;
@@ -1249,10 +1308,21 @@ extern "C" int k3_moe_latent_layer_decode_multi(const void *x, int x_dtype, cons
         d.N[0] = static_cast<int>(H);
         d.out[0] = ysh;
         d.ld[0] = static_cast<int>(H);
-        rc = launch_rows_multi<float>(d, st);
-        if (rc) return rc;
+        rc = side ? shared_down_side(d, st, *side) : launch_rows_multi<float>(d, st);
     }
-    rc = launch_down(a, n_slots, st);
+    // sigmoid + bias routing (moe.py:65-76) on the logits
+    if (!rc)
+        rc = k3_moe_topk(logits, a.E, a.T, a.E, static_cast<const float *>(router_bias), K3_ROUTE_SIGMOID_BIAS,
+                         renormalize, scaling, a.k, idx, wts, reinterpret_cast<float *>(w + L.scores),
+                         reinterpret_cast<float *>(w + L.corrected), stream);
+    const int n_slots = static_cast<int>(std::min<int64_t>(a.P, n_experts));
+    if (!rc) rc = launch_union(a, st);
+    if (!rc) rc = bf ? launch_gateup<uint16_t>(a, n_slots, st) : launch_gateup<float>(a, n_slots, st);
+    if (!rc) rc = launch_down(a, n_slots, st);
+    if (side) {
+        const int jr = check_hip(hipStreamWaitEvent(st, side->join, 0), "moe latent layer (T tokens): join");
+        if (!rc) rc = jr;  // an error after the fork still joins
+    }
     if (rc) return rc;
     // R3: out = W_up rmsnorm(ylat) * norm (+ the shared output), in out_dtype
     MRowsArgs u{};

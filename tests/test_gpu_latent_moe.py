@@ -161,6 +161,53 @@ def test_latent_moe_few_tokens_wide_hidden(T):
                 num_experts_per_token=4), seed=70 + T, T=T)
 
 
+def test_latent_moe_multi_graph_replay_and_threads():
+    """Four tokens through the multi-token latent layer, whose shared down rows run on the
+    library's side stream (forked after the first launch, joined before the up rows):
+    repeated eager calls are bit-identical; a CUDA graph of three calls replays
+    bit-identically four times with eager calls between the replays; two host threads, each
+    on its own stream, calling the layer 20 times together get the eager results."""
+    import threading
+
+    from k3hip.moe import LatentMoE
+    cfg = K3Cfg(hidden_size=1024, routed_expert_hidden_size=512, moe_intermediate_size=256, num_experts=16,
+                num_experts_per_token=4)
+    w, source, _ = make(80, 1024, 512, 256, 16, 4, 512)
+    moe = LatentMoE(cfg, 0, w, source)
+    gen = torch.Generator(device=DEV)
+    gen.manual_seed(81)
+    xs = [torch.randn(4, 1024, device=DEV, generator=gen).to(torch.bfloat16) for _ in range(3)]
+    ref = [moe(x).clone() for x in xs]
+    for x, r in zip(xs, ref):
+        assert torch.equal(moe(x), r)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        outs = [moe(x) for x in xs]
+    for i in range(4):
+        g.replay()
+        torch.cuda.synchronize()
+        for o, r in zip(outs, ref):
+            assert torch.equal(o, r)
+        assert torch.equal(moe(xs[i % 3]), ref[i % 3])   # eager work between replays
+    torch.cuda.synchronize()
+    bad = []
+
+    def worker(i):
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
+            ys = [moe(xs[i]) for _ in range(20)]
+        s.synchronize()
+        bad.extend((i, j) for j, y in enumerate(ys) if not torch.equal(y, ref[i]))
+
+    threads = [threading.Thread(target=worker, args=(i,)) for i in range(2)]
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join()
+    assert not bad, bad
+
+
 K3_CFG = dict(hidden_size=7168, routed_expert_hidden_size=3584, moe_intermediate_size=3072, num_experts=896,
               num_experts_per_token=16)
 
