@@ -273,7 +273,7 @@ __global__ __launch_bounds__(256) void multi_gateup_kernel(MultiArgs a) {
 // act vector is staged chunk-major ([chunk q][piece], plus one zero sink slot), so the lanes
 // of a wave read consecutive 16-byte slots.
 template <int S, int NP, int RW>
-__global__ __launch_bounds__(256, 2) void multi_down_kernel(MultiArgs a) {
+__device__ __forceinline__ void down_body(const MultiArgs &a, int bid) {
     static_assert(S == 16 || S == 32, "a piece is half a group or one group");
     constexpr int ND = S / 8;        // packed dwords per piece
     constexpr int NC = S / 4;        // float4 act chunks per piece
@@ -284,7 +284,7 @@ __global__ __launch_bounds__(256, 2) void multi_down_kernel(MultiArgs a) {
     __shared__ int pair_s[kMaxTokens];  // the slot's pair ids
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
     const int nR = (a.Hr + RB - 1) / RB;
-    const int u = blockIdx.x / nR, rr = blockIdx.x % nR;
+    const int u = bid / nR, rr = bid % nR;
     // the slot count, the slot's pair count and down pointers in one round before the exit
     // test (every slot index of the grid has its entries in the workspace)
     const int nu = *a.nu, cnt_u = a.u_count[u];
@@ -376,6 +376,11 @@ __global__ __launch_bounds__(256, 2) void multi_down_kernel(MultiArgs a) {
             }
         }
     }
+}
+
+template <int S, int NP, int RW>
+__global__ __launch_bounds__(256, 2) void multi_down_kernel(MultiArgs a) {
+    down_body<S, NP, RW>(a, static_cast<int>(blockIdx.x));
 }
 
 // ------------------------------------------------------------------ C: combine
@@ -512,13 +517,13 @@ __device__ __forceinline__ void norm_rows(float4 *x4, int nb, int cpr, int K, co
 // R: plain rows per wave (narrow rows take several, so one staged batch serves more rows);
 // NW: waves per block (4, or 8 to stage inputs of up to twice kLdsBudgetR in one batch).
 template <typename IT, int CH, int R, int NW>
-__global__ __launch_bounds__(64 * NW) void multi_rows_kernel(MRowsArgs a) {
+__device__ __forceinline__ void rows_body(const MRowsArgs &a, int bid) {
     extern __shared__ uint4 xs[];  // [tb][K * sizeof(IT) / 16]
     __shared__ float red[kMaxTokens][NW];
     using XC = typename std::conditional<std::is_same<IT, float>::value, float4, uint4>::type;
     constexpr int NR = R > 2 ? R : 2;  // weight rows held per wave (a pair needs two)
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
-    int b = blockIdx.x, s = 0;
+    int b = bid, s = 0;
     while (s < kPlainSets && b >= a.blocks[s]) b -= a.blocks[s++];
     const bool pair = s == kPlainSets;  // uniform
     const int nrows = pair ? 2 : R;    // rows this wave reduces
@@ -615,6 +620,24 @@ __global__ __launch_bounds__(64 * NW) void multi_rows_kernel(MRowsArgs a) {
             }
         }
     }
+}
+
+template <typename IT, int CH, int R, int NW>
+__global__ __launch_bounds__(64 * NW) void multi_rows_kernel(MRowsArgs a) {
+    rows_body<IT, CH, R, NW>(a, static_cast<int>(blockIdx.x));
+}
+
+// D and the 384-expert layer's shared down rows in one launch: blocks [0, nd) run D and the
+// rest the four-wave batched form of R over the rows r (fp32 act input), after D's blocks in
+// launch order, so they run as D's blocks retire and fill its tail.  As launches of their
+// own the shared down rows took 16.8 us for 29 MB (448 blocks, under two per CU) and a
+// launch boundary.
+template <int S, int NP, int RW, int CH, int R>
+__global__ __launch_bounds__(256, 2) void multi_down_rows_kernel(MultiArgs a, MRowsArgs r, int nd) {
+    if (static_cast<int>(blockIdx.x) < nd)
+        down_body<S, NP, RW>(a, static_cast<int>(blockIdx.x));
+    else
+        rows_body<float, CH, R, kRowWaves>(r, static_cast<int>(blockIdx.x) - nd);
 }
 
 // R in its persistent form, for T input rows that fit in LDS together (up to 128 KB; taken
@@ -926,26 +949,74 @@ int launch_gateup(MultiArgs &a, int n_slots, hipStream_t st) {
     return check_hip(hipGetLastError(), "moe routed decode: gate/up launch");
 }
 
-// D, then C
-int launch_down(MultiArgs &a, int n_slots, hipStream_t st) {
+// D's grid and dynamic LDS for the intermediate width's groups GI (sets a.tb_act)
+struct DownShape {
+    unsigned blocks;
+    size_t lds;
+};
+DownShape down_shape(MultiArgs &a, int n_slots) {
     const int GI = a.I / 32;
-    const dim3 gd(static_cast<unsigned>(n_slots * cdiv(a.Hr, down_rows(GI))));
-    auto down = [&](auto kern, int na) {
-        const size_t per = (static_cast<size_t>(na) * 256 + 1) * 16;
-        a.tb_act = static_cast<int>(std::max<size_t>(1, std::min<size_t>(a.T, kLdsBudgetD / per)));
-        kern<<<gd, 256, static_cast<size_t>(a.tb_act) * per, st>>>(a);
-    };
-    if (GI <= 64)
-        down(multi_down_kernel<32, 1, 14>, 2);
-    else if (GI <= 96)
-        down(multi_down_kernel<16, 3, 7>, 3);
-    else
-        down(multi_down_kernel<32, 2, 4>, 4);
-    int rc = check_hip(hipGetLastError(), "moe routed decode: down launch");
-    if (rc) return rc;
+    const int na = GI <= 64 ? 2 : (GI <= 96 ? 3 : 4);  // act float4 per thread and pair
+    const size_t per = (static_cast<size_t>(na) * 256 + 1) * 16;
+    a.tb_act = static_cast<int>(std::max<size_t>(1, std::min<size_t>(a.T, kLdsBudgetD / per)));
+    return {static_cast<unsigned>(n_slots * cdiv(a.Hr, down_rows(GI))), static_cast<size_t>(a.tb_act) * per};
+}
+
+int launch_combine(MultiArgs &a, hipStream_t st) {
     const int64_t n_out = static_cast<int64_t>(a.T) * a.Hr;
     multi_combine_kernel<<<dim3(static_cast<unsigned>(cdiv(n_out, 256))), 256, 0, st>>>(a);
     return check_hip(hipGetLastError(), "moe routed decode: combine launch");
+}
+
+// D, then C
+int launch_down(MultiArgs &a, int n_slots, hipStream_t st) {
+    const DownShape d = down_shape(a, n_slots);
+    const int GI = a.I / 32;
+    if (GI <= 64)
+        multi_down_kernel<32, 1, 14><<<dim3(d.blocks), 256, d.lds, st>>>(a);
+    else if (GI <= 96)
+        multi_down_kernel<16, 3, 7><<<dim3(d.blocks), 256, d.lds, st>>>(a);
+    else
+        multi_down_kernel<32, 2, 4><<<dim3(d.blocks), 256, d.lds, st>>>(a);
+    const int rc = check_hip(hipGetLastError(), "moe routed decode: down launch");
+    return rc ? rc : launch_combine(a, st);
+}
+
+template <int S, int NP, int RW>
+void launch_down_rows_ch(MultiArgs &a, MRowsArgs &r, int ch, dim3 g, size_t lds, int nd, hipStream_t st) {
+    if (ch <= 4)
+        multi_down_rows_kernel<S, NP, RW, 4, 4><<<g, 256, lds, st>>>(a, r, nd);
+    else
+        multi_down_rows_kernel<S, NP, RW, 8, 2><<<g, 256, lds, st>>>(a, r, nd);
+}
+
+// D with the shared down rows r (fp32 act, one plain set) in one launch, then C.  Rows whose
+// T inputs do not fit one kLdsBudgetR batch, or wider than 4096 values (whose registers would
+// take D to two waves per SIMD), run on their own launch of R first.
+int launch_down_rows(MultiArgs &a, int n_slots, MRowsArgs &r, hipStream_t st) {
+    const size_t row = static_cast<size_t>(r.K) * sizeof(float);
+    const int ch = static_cast<int>(cdiv(r.K / 8, 64));
+    if (r.T < 1 || r.T > kMaxTokens || static_cast<size_t>(r.T) * row > static_cast<size_t>(kLdsBudgetR) || ch > 8 ||
+        r.w[1] || r.wg || r.nw) {
+        const int rc = launch_rows_multi<float>(r, st);
+        return rc ? rc : launch_down(a, n_slots, st);
+    }
+    r.tb = r.T;
+    const int R = ch <= 4 ? 4 : 2;
+    r.blocks[0] = r.w[0] ? static_cast<int>(cdiv(r.N[0], kRowWaves * R)) : 0;
+    r.blocks[1] = 0;
+    const DownShape d = down_shape(a, n_slots);
+    const dim3 g(d.blocks + static_cast<unsigned>(r.blocks[0]));
+    const size_t lds = std::max(d.lds, static_cast<size_t>(r.T) * row);
+    const int nd = static_cast<int>(d.blocks), GI = a.I / 32;
+    if (GI <= 64)
+        launch_down_rows_ch<32, 1, 14>(a, r, ch, g, lds, nd, st);
+    else if (GI <= 96)
+        launch_down_rows_ch<16, 3, 7>(a, r, ch, g, lds, nd, st);
+    else
+        launch_down_rows_ch<32, 2, 4>(a, r, ch, g, lds, nd, st);
+    const int rc = check_hip(hipGetLastError(), "moe layer (T tokens): down + shared rows launch");
+    return rc ? rc : launch_combine(a, st);
 }
 
 // The shared expert's down rows depend only on the first launch (R), so the latent layer's
@@ -1197,9 +1268,8 @@ extern "C" int k3_moe_layer_decode_multi(const void *x, int x_dtype, const void 
         d.N[0] = a.Hr;
         d.out[0] = w + L.ysh;
         d.ld[0] = a.Hr;
-        rc = launch_rows_multi<float>(d, st);
-        if (rc) return rc;
         a.yadd = reinterpret_cast<const float *>(w + L.ysh);
+        return launch_down_rows(a, n_slots, d, st);
     }
     return launch_down(a, n_slots, st);
 }
