@@ -227,8 +227,10 @@ int k3_moe_layer_multi_workspace_offsets(int64_t T, int64_t H, int64_t I, int64_
  * rows and the shared gate/up rows against all T tokens in one launch (bf16 rows, exact
  * products, fp32 accumulation), the batched top-k (as k3_moe_topk), the routed experts as in
  * k3_moe_routed_decode (every expert any token selects read once for all the tokens routed to
- * it), the shared down rows, and the fixed-order combine with the shared output: seven
- * stream-ordered launches, no host synchronisation.  Arguments as k3_moe_layer_decode, plus T;
+ * it), the shared down rows (as extra blocks of the routed down launch when the T act rows
+ * fit 32 KB and shared_I <= 4096, else a launch of their own), and the fixed-order combine
+ * with the shared output: six or seven stream-ordered launches, no host synchronisation.
+ * Arguments as k3_moe_layer_decode, plus T;
  * shared_I a multiple of 128, <= 8192.
  * Replaces LatentMoE.__call__ (air_llm/models/kimi_k3/moe.py:110-132, without the latent
  * wrapper) for a decode batch of T tokens, whose dispatch loop gathers every token routed to

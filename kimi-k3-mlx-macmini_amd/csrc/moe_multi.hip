@@ -29,10 +29,13 @@
 //       62 -> 51 us, for a 4.7 us combine launch).
 //
 // The whole layer for T tokens (k3_moe_layer_decode_multi) adds the dense bf16 parts on R, a
-// row kernel for T tokens (4 waves, one row or one (gate, up) row pair per wave, the T input
-// rows staged in LDS once per block; wide fp32 inputs take a persistent form that stages
-// them once per CU): the router logits with the shared gate/up rows in one launch, the
-// batched top-k (k3_moe_topk), U, G, the shared down rows, D and C.
+// row kernel for T tokens (4 waves, or 8 for fp32 inputs of 32-64 KB; one row or one
+// (gate, up) row pair per wave, the T input rows staged in LDS once per block; wider fp32
+// inputs take a persistent form that stages them once per CU): the router logits with the
+// shared gate/up rows in one launch, the batched top-k (k3_moe_topk), U, G, D with the
+// shared down rows as extra blocks of its launch, and C.  The latent layer
+// (k3_moe_latent_layer_decode_multi) runs its shared down rows on a side stream beside the
+// top-k, U, G and D instead.
 //
 // Every launch issues its weight rows before it waits on anything else, and loads what it
 // stages in batches (every load of a batch issued before the first store), so a block's

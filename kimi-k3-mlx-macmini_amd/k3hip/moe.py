@@ -524,7 +524,7 @@ class LatentMoE:
                                  ("expert_indices", "expert_weights", "raw_scores", "corrected_scores")))
 
     def _decode_multi(self, flat, orig, return_router, out_dtype):
-        """2..DECODE_TOKENS tokens in one pass (k3_moe_latent_layer_decode_multi, seven
+        """2..DECODE_TOKENS tokens in one pass (k3_moe_latent_layer_decode_multi, eight
         launches, no host synchronisation): router, latent down, shared experts and the up
         projection on T-token HIP row kernels, every routed expert any token selects read
         once for all the tokens routed to it.  The RouterResult comes from the workspace."""
