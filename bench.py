@@ -844,6 +844,15 @@ def main():
                              "shared_expert": "bf16", "distinct_experts_routed_first32": touched,
                              "launches_per_layer": 3, "step_us": lstats,
                              **counter_fields(cnt.get("moe_layer_b1"))}
+        # the batch-1 MXFP4 GEMV sustained inside the layer: its routed gate/up launch (the 8
+        # selected experts' gate and up rows back to back, with the shared down rows)
+        l2 = [x for x in line["moe_layer"].get("launches", []) if x["kernel"].startswith("layer_l2")]
+        if l2:
+            line["sustained_in_layer"] = {
+                "kernel": l2[0]["kernel"], "GB/s": l2[0]["GB/s"], "pct_hbm_peak": l2[0]["pct_hbm_peak"],
+                "what": "the 384-expert layer's routed gate/up launch (8 experts' MXFP4 gate/up GEMVs "
+                        "and the shared down rows): counter bytes / kernel-trace time",
+                "source": line["moe_layer"]["traffic"]["source"], "current": line["moe_layer"]["traffic"]["current"]}
     if "layer4" in work:
         ms4 = min(K, 128)
         msec4, union4, bytes4, mstats4 = bench_layer_multi(torch, ms4, min(W, 16), dev)
