@@ -260,11 +260,11 @@ int k3_moe_latent_layer_multi_workspace_offsets(int64_t T, int64_t H, int64_t la
  * sigmoid + bias top-k, the routed experts on h at the latent width as in
  * k3_moe_routed_decode (every selected expert read once for all its tokens), the shared down
  * rows, and the up projection rows against rmsnorm(routed sum) * latent_norm with the shared
- * output added: eight launches, no host synchronisation.  The shared down rows run on a
- * library-owned side stream of the current device (created on the first call, default
- * priority), forked from `stream` after the first launch and joined to it before the up
- * projection through events, so the call stays ordered on `stream` and can be captured in a
- * graph (a first call made under capture runs them on `stream`).  Arguments as
+ * output added: eight launches, no host synchronisation.  The shared expert's gate/up and
+ * down rows run on a library-owned side stream of the current device (created on the first
+ * call, default priority), forked from `stream` at the start of the call and joined to it
+ * before the up projection through events, so the call stays ordered on `stream` and can be
+ * captured in a graph (a first call made under capture runs them on `stream`).  Arguments as
  * k3_moe_latent_layer_decode, plus T; shared_I a multiple of 128, <= 8192.
  * Replaces LatentMoE.__call__ (air_llm/models/kimi_k3/moe.py:110-132) for a decode batch of T
  * tokens, including the latent down/norm/up wrapper (moe.py:116,129-130). */

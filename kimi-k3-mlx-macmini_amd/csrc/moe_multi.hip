@@ -34,8 +34,8 @@
 // inputs take a persistent form that stages them once per CU): the router logits with the
 // shared gate/up rows in one launch, the batched top-k (k3_moe_topk), U, G, D with the
 // shared down rows as extra blocks of its launch, and C.  The latent layer
-// (k3_moe_latent_layer_decode_multi) runs its shared down rows on a side stream beside the
-// top-k, U, G and D instead.
+// (k3_moe_latent_layer_decode_multi) runs its whole shared expert on a side stream beside R,
+// the top-k, U, G and D instead.
 //
 // Every launch issues its weight rows before it waits on anything else, and loads what it
 // stages in batches (every load of a batch issued before the first store), so a block's
@@ -1022,9 +1022,9 @@ int launch_down_rows(MultiArgs &a, int n_slots, MRowsArgs &r, hipStream_t st) {
     return rc ? rc : launch_combine(a, st);
 }
 
-// The shared expert's down rows depend only on the first launch (R), so the latent layer's
-// entry point runs them on a side stream, beside the top-k, U, G and D launches on the
-// caller's stream: the few-block top-k and union launches leave most CUs idle.  One side
+// The shared expert depends only on x, so the latent layer's entry point runs its gate/up
+// and down rows on a side stream, beside R, the top-k, U, G and D launches on the caller's
+// stream (the few-block top-k and union launches leave most CUs idle).  One side
 // stream and a fork / join event pair per device, created on the device's first such call
 // (default priority, non-blocking) and kept until the process ends.  A call holds side_mutex
 // while it enqueues, so calls from several host threads cannot interleave their records and
@@ -1061,15 +1061,6 @@ int side_lane(SideLane *&lane, hipStream_t st) {
     }
     lane = &l;
     return K3_OK;
-}
-
-// Fork the side stream from st, run the shared down rows d on it, and record the join event.
-int shared_down_side(MRowsArgs &d, hipStream_t st, SideLane &l) {
-    int rc = check_hip(hipEventRecord(l.fork, st), "moe layer (T tokens): fork");
-    if (!rc) rc = check_hip(hipStreamWaitEvent(l.s, l.fork, 0), "moe layer (T tokens): fork");
-    if (!rc) rc = launch_rows_multi<float>(d, l.s);
-    if (!rc) rc = check_hip(hipEventRecord(l.join, l.s), "moe layer (T tokens): join");
-    return rc;
 }
 
 template <typename XT>
@@ -1336,8 +1327,15 @@ extern "C" int k3_moe_latent_layer_decode_multi(const void *x, int x_dtype, cons
     float *logits = reinterpret_cast<float *>(w + L.logits);
     float *act_sh = reinterpret_cast<float *>(w + L.act_sh);
     float *ysh = reinterpret_cast<float *>(w + L.ysh);
+    std::unique_lock<std::mutex> lock(side_mutex, std::defer_lock);
+    SideLane *side = nullptr;
+    if (has_shared) {
+        lock.lock();
+        rc = side_lane(side, st);
+        if (rc) return rc;
+    }
     // R1 on x: router logits, h = W_down x (bf16 for a bf16 x, as the reference's bf16
-    // matmul; fp32 for an fp32 x), the shared gate/up act
+    // matmul; fp32 for an fp32 x), and the shared gate/up act unless the side stream takes it
     MRowsArgs r{};
     r.in = x;
     r.T = a.T;
@@ -1351,38 +1349,43 @@ extern "C" int k3_moe_latent_layer_decode_multi(const void *x, int x_dtype, cons
     r.out[1] = h;
     r.ld[1] = a.Hr;
     r.out_bf16[1] = bf;
-    if (has_shared) {
-        r.wg = static_cast<const uint16_t *>(shared_gate);
-        r.wu = static_cast<const uint16_t *>(shared_up);
-        r.N1 = static_cast<int>(shared_I);
-        r.act = act_sh;
-        r.ld1 = static_cast<int>(shared_I);
+    MRowsArgs g{};  // the shared gate/up pairs on x
+    g.in = x;
+    g.T = a.T;
+    g.K = static_cast<int>(H);
+    g.wg = static_cast<const uint16_t *>(shared_gate);
+    g.wu = static_cast<const uint16_t *>(shared_up);
+    g.N1 = static_cast<int>(shared_I);
+    g.act = act_sh;
+    g.ld1 = static_cast<int>(shared_I);
+    g.act_kind = act_kind;
+    g.beta = beta;
+    g.lbeta = linear_beta;
+    MRowsArgs d{};  // the shared down rows on the shared act
+    d.in = act_sh;
+    d.T = a.T;
+    d.K = static_cast<int>(shared_I);
+    d.w[0] = static_cast<const uint16_t *>(shared_down);
+    d.N[0] = static_cast<int>(H);
+    d.out[0] = ysh;
+    d.ld[0] = static_cast<int>(H);
+    if (side) {
+        // the whole shared expert (264 MB at K3's shapes) on the side stream from the start of
+        // the call, beside R1, the top-k, U, G and D; R3 adds its output.  K3's four-token step
+        // 338 -> 325 us with the shared down rows alone there (forked after R1), 322 -> 318 us
+        // with the gate/up rows too; forked after U (beside G and D only): 337 us
+        rc = check_hip(hipEventRecord(side->fork, st), "moe layer (T tokens): fork");
+        if (!rc) rc = check_hip(hipStreamWaitEvent(side->s, side->fork, 0), "moe layer (T tokens): fork");
+        if (!rc) rc = bf ? launch_rows_multi<uint16_t>(g, side->s) : launch_rows_multi<float>(g, side->s);
+        if (!rc) rc = launch_rows_multi<float>(d, side->s);
+        const int jr = check_hip(hipEventRecord(side->join, side->s), "moe layer (T tokens): join");
+        if (!rc) rc = jr;
+    } else if (has_shared) {
+        r.wg = g.wg, r.wu = g.wu, r.N1 = g.N1, r.act = g.act, r.ld1 = g.ld1;
+        r.act_kind = act_kind, r.beta = beta, r.lbeta = linear_beta;
     }
-    r.act_kind = act_kind;
-    r.beta = beta;
-    r.lbeta = linear_beta;
-    rc = bf ? launch_rows_multi<uint16_t>(r, st) : launch_rows_multi<float>(r, st);
-    if (rc) return rc;
-    std::unique_lock<std::mutex> lock(side_mutex, std::defer_lock);
-    SideLane *side = nullptr;
-    if (has_shared) {
-        // the shared down rows (88 MB at K3's shapes, the persistent row form) on the side
-        // stream from here on, beside the top-k, U, G and D launches; R3 adds their output.
-        // K3's four-token step 338 -> 325 us; forked after U instead (beside G and D only):
-        // 337 us
-        lock.lock();
-        rc = side_lane(side, st);
-        if (rc) return rc;
-        MRowsArgs d{};
-        d.in = act_sh;
-        d.T = a.T;
-        d.K = static_cast<int>(shared_I);
-        d.w[0] = static_cast<const uint16_t *>(shared_down);
-        d.N[0] = static_cast<int>(H);
-        d.out[0] = ysh;
-        d.ld[0] = static_cast<int>(H);
-        rc = side ? shared_down_side(d, st, *side) : launch_rows_multi<float>(d, st);
-    }
+    if (!rc) rc = bf ? launch_rows_multi<uint16_t>(r, st) : launch_rows_multi<float>(r, st);
+    if (!rc && has_shared && !side) rc = launch_rows_multi<float>(d, st);
     // sigmoid + bias routing (moe.py:65-76) on the logits
     if (!rc)
         rc = k3_moe_topk(logits, a.E, a.T, a.E, static_cast<const float *>(router_bias), K3_ROUTE_SIGMOID_BIAS,

@@ -162,8 +162,8 @@ def test_latent_moe_few_tokens_wide_hidden(T):
 
 
 def test_latent_moe_multi_graph_replay_and_threads():
-    """Four tokens through the multi-token latent layer, whose shared down rows run on the
-    library's side stream (forked after the first launch, joined before the up rows):
+    """Four tokens through the multi-token latent layer, whose shared expert runs on the
+    library's side stream (forked at the start of the call, joined before the up rows):
     repeated eager calls are bit-identical; a CUDA graph of three calls replays
     bit-identically four times with eager calls between the replays; two host threads, each
     on its own stream, calling the layer 20 times together get the eager results."""
