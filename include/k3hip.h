@@ -227,9 +227,13 @@ int k3_moe_layer_multi_workspace_offsets(int64_t T, int64_t H, int64_t I, int64_
  * rows and the shared gate/up rows against all T tokens in one launch (bf16 rows, exact
  * products, fp32 accumulation), the batched top-k (as k3_moe_topk), the routed experts as in
  * k3_moe_routed_decode (every expert any token selects read once for all the tokens routed to
- * it), the shared down rows (as extra blocks of the routed down launch when the T act rows
- * fit 32 KB and shared_I <= 4096, else a launch of their own), and the fixed-order combine
- * with the shared output: six or seven stream-ordered launches, no host synchronisation.
+ * it), the shared down rows, and the fixed-order combine with the shared output: six or seven
+ * launches, no host synchronisation.  The shared expert's gate/up and down rows run on a
+ * library-owned side stream of the current device, forked from `stream` at the start of the
+ * call and joined to it before the combine through events (as k3_moe_latent_layer_decode_multi);
+ * without it (K3HIP_SIDE_STREAM=0 in the environment, or a first call made under capture) the
+ * gate/up rows run with the router rows and the down rows as extra blocks of the routed down
+ * launch (when the T act rows fit 32 KB and shared_I <= 4096, else a launch of their own).
  * Arguments as k3_moe_layer_decode, plus T;
  * shared_I a multiple of 128, <= 8192.
  * Replaces LatentMoE.__call__ (air_llm/models/kimi_k3/moe.py:110-132, without the latent
@@ -264,7 +268,8 @@ int k3_moe_latent_layer_multi_workspace_offsets(int64_t T, int64_t H, int64_t la
  * down rows run on a library-owned side stream of the current device (created on the first
  * call, default priority), forked from `stream` at the start of the call and joined to it
  * before the up projection through events, so the call stays ordered on `stream` and can be
- * captured in a graph (a first call made under capture runs them on `stream`).  Arguments as
+ * captured in a graph (a first call made under capture, or K3HIP_SIDE_STREAM=0 in the
+ * environment, runs them on `stream`).  Arguments as
  * k3_moe_latent_layer_decode, plus T; shared_I a multiple of 128, <= 8192.
  * Replaces LatentMoE.__call__ (air_llm/models/kimi_k3/moe.py:110-132) for a decode batch of T
  * tokens, including the latent down/norm/up wrapper (moe.py:116,129-130). */

@@ -33,9 +33,9 @@
 // (gate, up) row pair per wave, the T input rows staged in LDS once per block; wider fp32
 // inputs take a persistent form that stages them once per CU): the router logits with the
 // shared gate/up rows in one launch, the batched top-k (k3_moe_topk), U, G, D with the
-// shared down rows as extra blocks of its launch, and C.  The latent layer
-// (k3_moe_latent_layer_decode_multi) runs its whole shared expert on a side stream beside R,
-// the top-k, U, G and D instead.
+// shared down rows as extra blocks of its launch, and C; with a side stream (the default) the
+// shared expert's gate/up and down rows run there instead, beside R, the top-k, U, G and D.
+// The latent layer (k3_moe_latent_layer_decode_multi) does the same.
 //
 // Every launch issues its weight rows before it waits on anything else, and loads what it
 // stages in batches (every load of a batch issued before the first store), so a block's
@@ -45,6 +45,8 @@
 // number of tokens routed to it.  Deterministic: no float atomics, fixed orders.
 #include <algorithm>
 #include <atomic>
+#include <cstdlib>
+#include <cstring>
 #include <mutex>
 #include <type_traits>
 
@@ -971,8 +973,8 @@ int launch_combine(MultiArgs &a, hipStream_t st) {
     return check_hip(hipGetLastError(), "moe routed decode: combine launch");
 }
 
-// D, then C
-int launch_down(MultiArgs &a, int n_slots, hipStream_t st) {
+// D alone
+int launch_down_only(MultiArgs &a, int n_slots, hipStream_t st) {
     const DownShape d = down_shape(a, n_slots);
     const int GI = a.I / 32;
     if (GI <= 64)
@@ -981,7 +983,12 @@ int launch_down(MultiArgs &a, int n_slots, hipStream_t st) {
         multi_down_kernel<16, 3, 7><<<dim3(d.blocks), 256, d.lds, st>>>(a);
     else
         multi_down_kernel<32, 2, 4><<<dim3(d.blocks), 256, d.lds, st>>>(a);
-    const int rc = check_hip(hipGetLastError(), "moe routed decode: down launch");
+    return check_hip(hipGetLastError(), "moe routed decode: down launch");
+}
+
+// D, then C
+int launch_down(MultiArgs &a, int n_slots, hipStream_t st) {
+    const int rc = launch_down_only(a, n_slots, st);
     return rc ? rc : launch_combine(a, st);
 }
 
@@ -1022,9 +1029,9 @@ int launch_down_rows(MultiArgs &a, int n_slots, MRowsArgs &r, hipStream_t st) {
     return rc ? rc : launch_combine(a, st);
 }
 
-// The shared expert depends only on x, so the latent layer's entry point runs its gate/up
-// and down rows on a side stream, beside R, the top-k, U, G and D launches on the caller's
-// stream (the few-block top-k and union launches leave most CUs idle).  One side
+// The shared expert depends only on x, so the layer entry points run its gate/up and down
+// rows on a side stream, beside R, the top-k, U, G and D launches on the caller's stream
+// (the few-block top-k and union launches leave most CUs idle).  One side
 // stream and a fork / join event pair per device, created on the device's first such call
 // (default priority, non-blocking) and kept until the process ends.  A call holds side_mutex
 // while it enqueues, so calls from several host threads cannot interleave their records and
@@ -1037,12 +1044,17 @@ struct SideLane {
 std::mutex side_mutex;
 
 // lane: the current device's side lane, or null when it does not exist yet and st is
-// capturing (creating a stream or an event is not a capturable call; the caller then runs
-// the rows in st).
+// capturing (creating a stream or an event is not a capturable call), or when the
+// environment sets K3HIP_SIDE_STREAM=0; the caller then runs the rows in st.
 int side_lane(SideLane *&lane, hipStream_t st) {
     constexpr int kDevs = 64;
     static SideLane lanes[kDevs];
+    static const bool enabled = [] {
+        const char *e = std::getenv("K3HIP_SIDE_STREAM");
+        return !(e && std::strcmp(e, "0") == 0);
+    }();
     lane = nullptr;
+    if (!enabled) return K3_OK;
     int dev = 0;
     int rc = check_hip(hipGetDevice(&dev), "moe layer (T tokens): device query");
     if (rc) return rc;
@@ -1218,7 +1230,19 @@ extern "C" int k3_moe_layer_decode_multi(const void *x, int x_dtype, const void 
         return set_error(K3_ERR_WORKSPACE, "%s: workspace %lld < %zu bytes", what, (long long)workspace_bytes, L.total);
     auto st = static_cast<hipStream_t>(stream);
     const bool bf = x_dtype == K3_BF16;
-    // R: router logits [T, E] and the shared gate/up act [T, shared_I], one launch on x
+    // The shared expert (gate/up and down rows, 88 MB at the 384-expert shape) runs on the
+    // side stream from the start of the call, beside R (then the router rows alone), the
+    // top-k, U, G and D, and joins before C: four tokens 173.5 -> 171.7 us.  Only its down rows
+    // there, forked after R, measured slower (178.4 -> 180.3 us); without a side stream (a
+    // first call under capture) they run as extra blocks of D's launch.
+    std::unique_lock<std::mutex> lock(side_mutex, std::defer_lock);
+    SideLane *side = nullptr;
+    if (has_shared) {
+        lock.lock();
+        rc = side_lane(side, st);
+        if (rc) return rc;
+    }
+    // R: router logits [T, E] (and the shared gate/up act [T, shared_I] without a side stream)
     MRowsArgs r{};
     r.in = x;
     r.T = a.T;
@@ -1228,43 +1252,55 @@ extern "C" int k3_moe_layer_decode_multi(const void *x, int x_dtype, const void 
     r.out[0] = logits;
     r.ld[0] = a.E;
     float *act_sh = reinterpret_cast<float *>(w + L.act_sh);
-    if (has_shared) {
-        r.wg = static_cast<const uint16_t *>(shared_gate);
-        r.wu = static_cast<const uint16_t *>(shared_up);
-        r.N1 = static_cast<int>(shared_I);
-        r.act = act_sh;
-        r.ld1 = static_cast<int>(shared_I);
+    MRowsArgs g{};  // the shared gate/up pairs on x
+    g.in = x;
+    g.T = a.T;
+    g.K = a.Hr;
+    g.wg = static_cast<const uint16_t *>(shared_gate);
+    g.wu = static_cast<const uint16_t *>(shared_up);
+    g.N1 = static_cast<int>(shared_I);
+    g.act = act_sh;
+    g.ld1 = static_cast<int>(shared_I);
+    g.act_kind = act_kind;
+    g.beta = beta;
+    g.lbeta = linear_beta;
+    MRowsArgs d{};  // the shared down rows [H, shared_I] against the fp32 act -> [T, H], added in C
+    d.in = act_sh;
+    d.T = a.T;
+    d.K = static_cast<int>(shared_I);
+    d.w[0] = static_cast<const uint16_t *>(shared_down);
+    d.N[0] = a.Hr;
+    d.out[0] = w + L.ysh;
+    d.ld[0] = a.Hr;
+    if (has_shared) a.yadd = reinterpret_cast<const float *>(w + L.ysh);
+    if (side) {
+        rc = check_hip(hipEventRecord(side->fork, st), "moe layer (T tokens): fork");
+        if (!rc) rc = check_hip(hipStreamWaitEvent(side->s, side->fork, 0), "moe layer (T tokens): fork");
+        if (!rc) rc = bf ? launch_rows_multi<uint16_t>(g, side->s) : launch_rows_multi<float>(g, side->s);
+        if (!rc) rc = launch_rows_multi<float>(d, side->s);
+        const int jr = check_hip(hipEventRecord(side->join, side->s), "moe layer (T tokens): join");
+        if (!rc) rc = jr;
+    } else if (has_shared) {
+        r.wg = g.wg, r.wu = g.wu, r.N1 = g.N1, r.act = g.act, r.ld1 = g.ld1;
+        r.act_kind = act_kind, r.beta = beta, r.lbeta = linear_beta;
     }
-    r.act_kind = act_kind;
-    r.beta = beta;
-    r.lbeta = linear_beta;
-    rc = bf ? launch_rows_multi<uint16_t>(r, st) : launch_rows_multi<float>(r, st);
-    if (rc) return rc;
+    if (!rc) rc = bf ? launch_rows_multi<uint16_t>(r, st) : launch_rows_multi<float>(r, st);
     // the batched top-k on those logits (softmax / sigmoid + bias, renormalised, scaled)
-    rc = k3_moe_topk(logits, a.E, a.T, a.E, static_cast<const float *>(router_bias), route_kind, renormalize, scaling,
-                     a.k, idx, wts, reinterpret_cast<float *>(w + L.scores), reinterpret_cast<float *>(w + L.corrected),
-                     stream);
-    if (rc) return rc;
+    if (!rc)
+        rc = k3_moe_topk(logits, a.E, a.T, a.E, static_cast<const float *>(router_bias), route_kind, renormalize,
+                         scaling, a.k, idx, wts, reinterpret_cast<float *>(w + L.scores),
+                         reinterpret_cast<float *>(w + L.corrected), stream);
     const int n_slots = static_cast<int>(std::min<int64_t>(a.P, n_experts));
-    rc = launch_union(a, st);
+    if (!rc) rc = launch_union(a, st);
     if (!rc) rc = bf ? launch_gateup<uint16_t>(a, n_slots, st) : launch_gateup<float>(a, n_slots, st);
-    if (rc) return rc;
-    if (has_shared) {
-        // the shared down rows [H, shared_I] against the fp32 act -> [T, H], added in C (in
-        // this stream between G and D: on a side stream from R on, beside the top-k, U, G
-        // and D, these 29 MB rows slowed those launches by more than their own 16 us at the
-        // 384-expert layer's four tokens, 178.4 -> 180.3 us)
-        MRowsArgs d{};
-        d.in = act_sh;
-        d.T = a.T;
-        d.K = static_cast<int>(shared_I);
-        d.w[0] = static_cast<const uint16_t *>(shared_down);
-        d.N[0] = a.Hr;
-        d.out[0] = w + L.ysh;
-        d.ld[0] = a.Hr;
-        a.yadd = reinterpret_cast<const float *>(w + L.ysh);
-        return launch_down_rows(a, n_slots, d, st);
+    if (side) {
+        if (!rc) rc = launch_down_only(a, n_slots, st);
+        const int jr = check_hip(hipStreamWaitEvent(st, side->join, 0), "moe layer (T tokens): join");
+        if (!rc) rc = jr;  // an error after the fork still joins
+        return rc ? rc : launch_combine(a, st);
     }
+    if (rc) return rc;
+    if (has_shared) return launch_down_rows(a, n_slots, d, st);
     return launch_down(a, n_slots, st);
 }
 

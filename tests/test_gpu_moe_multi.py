@@ -296,3 +296,27 @@ def test_latent_moe_few_tokens_k3_shapes():
     against the fp64 oracle with the bf16 latent state."""
     from test_gpu_latent_moe import K3_CFG, K3Cfg, check
     check(K3Cfg(**K3_CFG), seed=52, T=4, on_device=True)
+
+
+def test_layers_without_side_stream():
+    """Both whole-layer multi-token entry points with the side stream switched off
+    (K3HIP_SIDE_STREAM=0, read once per process, so in a child process): the 384-expert
+    layer then takes the shared gate/up rows in R and the shared down rows as extra blocks of
+    D's launch, the latent layer the shared rows in order on the caller's stream; both
+    against the fp64 oracle, as with the side stream."""
+    import subprocess
+    import sys
+    from pathlib import Path
+    root = Path(__file__).resolve().parent.parent
+    code = ("import sys, torch; sys.path[:0] = [{t!r}, {r!r}, {p!r}]\n"
+            "from test_gpu_moe_multi import test_routed_moe_few_tokens_and_prefill_dispatch as f\n"
+            "f('sigmoid_bias', torch.bfloat16, 1024)\n"
+            "from test_gpu_latent_moe import K3Cfg, check\n"
+            "check(K3Cfg(hidden_size=1024, routed_expert_hidden_size=512, moe_intermediate_size=256, num_experts=16,"
+            " num_experts_per_token=4), seed=90, T=4)\n"
+            "print('side stream off: ok')\n").format(t=str(root / "tests"), r=str(root),
+                                                     p=str(root / "kimi-k3-mlx-macmini_amd"))
+    env = dict(os.environ, K3HIP_SIDE_STREAM="0")
+    res = subprocess.run([sys.executable, "-c", code], env=env, capture_output=True, text=True, timeout=300)
+    print(res.stdout[-2000:], res.stderr[-2000:])
+    assert res.returncode == 0 and "side stream off: ok" in res.stdout
