@@ -290,12 +290,15 @@ def test_layer_decode_multi_repeatable_and_bf16_out():
                   Tt.ptr(out), _lib.K3_F32, T, H, I, Is, E, k, 0, 1.0, 0.0, Tt.ptr(ws), ws.numel(), None)
 
 
-def test_latent_moe_few_tokens_k3_shapes():
+@pytest.mark.parametrize("T", [4, 8])
+def test_latent_moe_few_tokens_k3_shapes(T):
     """K3's routed layer (latent 3584, experts [3072 x 3584], top-16 of 896 distinct experts
-    on the device, shared width 6144) for four decode tokens through the multi-token path,
-    against the fp64 oracle with the bf16 latent state."""
+    on the device, shared width 6144) for four and eight decode tokens through the
+    multi-token path (eight tokens x top-16: the 128 (token, slot) pairs the union holds at
+    most, and the fp32 act rows the persistent row form stages), against the fp64 oracle with
+    the bf16 latent state."""
     from test_gpu_latent_moe import K3_CFG, K3Cfg, check
-    check(K3Cfg(**K3_CFG), seed=52, T=4, on_device=True)
+    check(K3Cfg(**K3_CFG), seed=52 + T, T=T, on_device=True)
 
 
 def test_layers_without_side_stream():
@@ -320,3 +323,50 @@ def test_layers_without_side_stream():
     res = subprocess.run([sys.executable, "-c", code], env=env, capture_output=True, text=True, timeout=300)
     print(res.stdout[-2000:], res.stderr[-2000:])
     assert res.returncode == 0 and "side stream off: ok" in res.stdout
+
+
+def test_layers_first_call_under_capture():
+    """A first call made while the caller's stream is capturing cannot create the side
+    stream (stream and event creation are not capturable), so it runs the shared expert on
+    the caller's stream inside the graph: in a child process whose first multi-token layer
+    calls are captured (after one-token calls that build the expert tables), the replays
+    equal the eager calls made afterwards (which create and use the side stream) bit for bit,
+    for both whole-layer multi-token entry points."""
+    import subprocess
+    import sys
+    from pathlib import Path
+    root = Path(__file__).resolve().parent.parent
+    code = ("import sys, torch; sys.path[:0] = [{t!r}, {r!r}, {p!r}]\n"
+            "from test_gpu_moe_multi import host_experts\n"
+            "from test_gpu_latent_moe import K3Cfg, make\n"
+            "from k3hip.moe import LatentMoE, MoEConfig, RoutedMoE\n"
+            "import numpy as np\n"
+            "dev = 'cuda'\n"
+            "rng = np.random.default_rng(7)\n"
+            "H, I, E, k, Is = 1024, 256, 16, 4, 512\n"
+            "ex_np, ex_dev = host_experts(rng, E, H, I)\n"
+            "w = {{'gate.weight': (torch.randn(E, H, device=dev) * 0.02).to(torch.bfloat16)}}\n"
+            "for name, shape in (('gate', (Is, H)), ('up', (Is, H)), ('down', (H, Is))):\n"
+            "    w['shared_experts.' + name + '_proj.weight'] = (torch.randn(*shape, device=dev) * 0.02).to(torch.bfloat16)\n"
+            "which = {{'w1': 0, 'w3': 1, 'w2': 2}}\n"
+            "moe = RoutedMoE(MoEConfig(hidden_size=H, moe_intermediate_size=I, num_experts=E, num_experts_per_token=k,"
+            " shared_intermediate_size=Is), 0, w, lambda L, e, wh: ex_dev[e][which[wh]])\n"
+            "cfg = K3Cfg(hidden_size=1024, routed_expert_hidden_size=512, moe_intermediate_size=256, num_experts=16,"
+            " num_experts_per_token=4)\n"
+            "wl, src, _ = make(91, 1024, 512, 256, 16, 4, 512)\n"
+            "lat = LatentMoE(cfg, 0, wl, src)\n"
+            "x = torch.randn(4, 1024, device=dev).to(torch.bfloat16)\n"
+            "moe(x[:1]); lat(x[:1]); torch.cuda.synchronize()  # one-token calls: tables built, no side stream\n"
+            "s = torch.cuda.Stream(); s.wait_stream(torch.cuda.current_stream())\n"
+            "g = torch.cuda.CUDAGraph()\n"
+            "with torch.cuda.graph(g, stream=s):\n"
+            "    a, b = moe(x), lat(x)\n"
+            "for _ in range(3):\n"
+            "    g.replay(); torch.cuda.synchronize()\n"
+            "    ea, eb = moe(x), lat(x); torch.cuda.synchronize()\n"
+            "    assert torch.equal(a, ea) and torch.equal(b, eb)\n"
+            "print('first call under capture: ok')\n").format(t=str(root / "tests"), r=str(root),
+                                                              p=str(root / "kimi-k3-mlx-macmini_amd"))
+    res = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True, timeout=300)
+    print(res.stdout[-2000:], res.stderr[-2000:])
+    assert res.returncode == 0 and "first call under capture: ok" in res.stdout
