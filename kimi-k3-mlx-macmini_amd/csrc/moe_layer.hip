@@ -91,7 +91,10 @@ constexpr int kSharedDownRows = 2;  // shared down rows per wave (L2)
 // shared down rows per wave for CHI chunks per lane: one row past 8 chunks (wide shared
 // experts), so the fp32 activation and the rows stay in registers
 constexpr int shared_down_rows(int chi) { return chi > 8 ? 1 : kSharedDownRows; }
-constexpr int kRoutedPairs = 2;     // routed (gate, up) row pairs per wave (L2)
+// routed (gate, up) row pairs per wave (L2): one keeps L2 at 62-70 VGPRs (seven or eight
+// waves per SIMD); two: 384-expert layer 56.6 -> 57.7 us, K3's 126.8 -> 128.3 us; three or
+// four: 59.4 / 59.7 us
+constexpr int kRoutedPairs = 1;
 
 // ------------------------------------------------------------------ bf16 row dots
 // 8 bf16 weights . 8 bf16 activations
