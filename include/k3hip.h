@@ -231,7 +231,8 @@ int k3_moe_layer_multi_workspace_offsets(int64_t T, int64_t H, int64_t I, int64_
  * launches, no host synchronisation.  The shared expert's gate/up and down rows run on a
  * library-owned side stream of the current device, forked from `stream` at the start of the
  * call and joined to it before the combine through events (as k3_moe_latent_layer_decode_multi);
- * without it (K3HIP_SIDE_STREAM=0 in the environment, or a first call made under capture) the
+ * without it (K3HIP_SIDE_STREAM=0 in the environment, a first call made under capture, or a
+ * call under capture while another capture on the device holds the capture side stream) the
  * gate/up rows run with the router rows and the down rows as extra blocks of the routed down
  * launch (when the T act rows fit 32 KB and shared_I <= 4096, else a launch of their own).
  * Arguments as k3_moe_layer_decode, plus T;
@@ -265,10 +266,11 @@ int k3_moe_latent_layer_multi_workspace_offsets(int64_t T, int64_t H, int64_t la
  * k3_moe_routed_decode (every selected expert read once for all its tokens), the shared down
  * rows, and the up projection rows against rmsnorm(routed sum) * latent_norm with the shared
  * output added: eight launches, no host synchronisation.  The shared expert's gate/up and
- * down rows run on a library-owned side stream of the current device (created on the first
- * call, default priority), forked from `stream` at the start of the call and joined to it
+ * down rows run on a library-owned side stream of the current device (one for calls under
+ * capture, one for the rest, created on the first call, default priority), forked from `stream` at the start of the call and joined to it
  * before the up projection through events, so the call stays ordered on `stream` and can be
- * captured in a graph (a first call made under capture, or K3HIP_SIDE_STREAM=0 in the
+ * captured in a graph (a first call made under capture, a call under capture while another
+ * capture on the device holds the capture side stream, or K3HIP_SIDE_STREAM=0 in the
  * environment, runs them on `stream`).  Arguments as
  * k3_moe_latent_layer_decode, plus T; shared_I a multiple of 128, <= 8192.
  * Replaces LatentMoE.__call__ (air_llm/models/kimi_k3/moe.py:110-132) for a decode batch of T

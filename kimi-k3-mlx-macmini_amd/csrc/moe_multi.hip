@@ -1031,24 +1031,35 @@ int launch_down_rows(MultiArgs &a, int n_slots, MRowsArgs &r, hipStream_t st) {
 
 // The shared expert depends only on x, so the layer entry points run its gate/up and down
 // rows on a side stream, beside R, the top-k, U, G and D launches on the caller's stream
-// (the few-block top-k and union launches leave most CUs idle).  One side
-// stream and a fork / join event pair per device, created on the device's first such call
-// (default priority, non-blocking) and kept until the process ends.  A call holds side_mutex
-// while it enqueues, so calls from several host threads cannot interleave their records and
-// waits on the shared events; under stream capture the side stream joins the capture at the
-// fork and leaves it at the join.
+// (the few-block top-k and union launches leave most CUs idle).  Two side lanes (a stream and
+// a fork / join event pair) per device, created on the device's first such call (default
+// priority, non-blocking) and kept until the process ends: one for calls on a stream that is
+// not capturing, one for calls under capture.  A stream forked into a capture stays in it
+// until that capture ends, so eager calls never use the capture lane; a call under capture
+// takes the capture lane when it is idle or already in the same capture, and otherwise (a
+// second capture open on the device at once) runs the rows in its own stream.  A call holds
+// side_mutex while it enqueues, so calls from several host threads cannot interleave their
+// records and waits on the shared events.
 struct SideLane {
     hipStream_t s = nullptr;
     hipEvent_t fork = nullptr, join = nullptr;
 };
 std::mutex side_mutex;
 
-// lane: the current device's side lane, or null when it does not exist yet and st is
-// capturing (creating a stream or an event is not a capturable call), or when the
-// environment sets K3HIP_SIDE_STREAM=0; the caller then runs the rows in st.
+int new_lane(SideLane &n) {
+    int rc = check_hip(hipStreamCreateWithFlags(&n.s, hipStreamNonBlocking), "moe layer (T tokens): side stream");
+    if (!rc) rc = check_hip(hipEventCreateWithFlags(&n.fork, hipEventDisableTiming), "moe layer (T tokens): event");
+    if (!rc) rc = check_hip(hipEventCreateWithFlags(&n.join, hipEventDisableTiming), "moe layer (T tokens): event");
+    return rc;
+}
+
+// lane: the side lane for a call on st (hold side_mutex), or null when the lanes do not exist
+// yet and st is capturing (creating a stream or an event is not a capturable call), when the
+// capture lane belongs to another open capture, or when the environment sets
+// K3HIP_SIDE_STREAM=0; the caller then runs the rows in st.
 int side_lane(SideLane *&lane, hipStream_t st) {
     constexpr int kDevs = 64;
-    static SideLane lanes[kDevs];
+    static SideLane eager[kDevs], captured[kDevs];
     static const bool enabled = [] {
         const char *e = std::getenv("K3HIP_SIDE_STREAM");
         return !(e && std::strcmp(e, "0") == 0);
@@ -1059,19 +1070,28 @@ int side_lane(SideLane *&lane, hipStream_t st) {
     int rc = check_hip(hipGetDevice(&dev), "moe layer (T tokens): device query");
     if (rc) return rc;
     if (dev < 0 || dev >= kDevs) return set_error(K3_ERR_SHAPE, "moe layer (T tokens): device %d", dev);
-    SideLane &l = lanes[dev];
-    if (!l.s) {
-        hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
-        rc = check_hip(hipStreamIsCapturing(st, &cs), "moe layer (T tokens): capture query");
-        if (rc || cs != hipStreamCaptureStatusNone) return rc;
-        SideLane n;
-        rc = check_hip(hipStreamCreateWithFlags(&n.s, hipStreamNonBlocking), "moe layer (T tokens): side stream");
-        if (!rc) rc = check_hip(hipEventCreateWithFlags(&n.fork, hipEventDisableTiming), "moe layer (T tokens): event");
-        if (!rc) rc = check_hip(hipEventCreateWithFlags(&n.join, hipEventDisableTiming), "moe layer (T tokens): event");
-        if (rc) return rc;
-        l = n;
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    unsigned long long id = 0;
+    rc = check_hip(hipStreamGetCaptureInfo(st, &cs, &id), "moe layer (T tokens): capture query");
+    if (rc) return rc;
+    if (cs == hipStreamCaptureStatusNone) {
+        if (!eager[dev].s) {
+            SideLane e, c;
+            rc = new_lane(e);
+            if (!rc) rc = new_lane(c);
+            if (rc) return rc;
+            eager[dev] = e;
+            captured[dev] = c;
+        }
+        lane = &eager[dev];
+        return K3_OK;
     }
-    lane = &l;
+    if (cs != hipStreamCaptureStatusActive || !captured[dev].s) return K3_OK;
+    hipStreamCaptureStatus ls = hipStreamCaptureStatusNone;
+    unsigned long long lid = 0;
+    rc = check_hip(hipStreamGetCaptureInfo(captured[dev].s, &ls, &lid), "moe layer (T tokens): capture query");
+    if (rc) return rc;
+    if (ls == hipStreamCaptureStatusNone || (ls == hipStreamCaptureStatusActive && lid == id)) lane = &captured[dev];
     return K3_OK;
 }
 
@@ -1233,8 +1253,8 @@ extern "C" int k3_moe_layer_decode_multi(const void *x, int x_dtype, const void 
     // The shared expert (gate/up and down rows, 88 MB at the 384-expert shape) runs on the
     // side stream from the start of the call, beside R (then the router rows alone), the
     // top-k, U, G and D, and joins before C: four tokens 173.5 -> 171.7 us.  Only its down rows
-    // there, forked after R, measured slower (178.4 -> 180.3 us); without a side stream (a
-    // first call under capture) they run as extra blocks of D's launch.
+    // there, forked after R, measured slower (178.4 -> 180.3 us); without a side lane (see
+    // side_lane) they run as extra blocks of D's launch.
     std::unique_lock<std::mutex> lock(side_mutex, std::defer_lock);
     SideLane *side = nullptr;
     if (has_shared) {

@@ -370,3 +370,77 @@ def test_layers_first_call_under_capture():
     res = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True, timeout=300)
     print(res.stdout[-2000:], res.stderr[-2000:])
     assert res.returncode == 0 and "first call under capture: ok" in res.stdout
+
+
+@pytest.mark.gpu
+def test_layers_capture_beside_eager_calls():
+    """Calls under capture use the device's capture side stream, which stays in the capture
+    until it ends; eager calls keep to the other side stream.  In a child process, with the
+    side streams created by eager calls: thread A captures both multi-token layers (the latent
+    layer after thread B's calls, so it finds the capture side stream already in its own
+    capture) while thread B, with A's capture open, makes the same calls eagerly on its own
+    stream.  B's results and every replay of A's graph equal the eager results bit for bit.
+    (A second capture open on the device at once, which runs the shared rows on its own
+    stream, is not exercised: torch's capture set-up synchronises the device, which an open
+    capture forbids.)"""
+    import subprocess
+    import sys
+    from pathlib import Path
+    root = Path(__file__).resolve().parent.parent
+    code = ("import sys, threading, torch; sys.path[:0] = [{t!r}, {r!r}, {p!r}]\n"
+            "from test_gpu_moe_multi import host_experts\n"
+            "from test_gpu_latent_moe import K3Cfg, make\n"
+            "from k3hip.moe import LatentMoE, MoEConfig, RoutedMoE\n"
+            "import numpy as np\n"
+            "dev = 'cuda'\n"
+            "rng = np.random.default_rng(8)\n"
+            "H, I, E, k, Is = 1024, 256, 16, 4, 512\n"
+            "ex_np, ex_dev = host_experts(rng, E, H, I)\n"
+            "w = {{'gate.weight': (torch.randn(E, H, device=dev) * 0.02).to(torch.bfloat16)}}\n"
+            "for name, shape in (('gate', (Is, H)), ('up', (Is, H)), ('down', (H, Is))):\n"
+            "    w['shared_experts.' + name + '_proj.weight'] = (torch.randn(*shape, device=dev) * 0.02).to(torch.bfloat16)\n"
+            "which = {{'w1': 0, 'w3': 1, 'w2': 2}}\n"
+            "moe = RoutedMoE(MoEConfig(hidden_size=H, moe_intermediate_size=I, num_experts=E, num_experts_per_token=k,"
+            " shared_intermediate_size=Is), 0, w, lambda L, e, wh: ex_dev[e][which[wh]])\n"
+            "cfg = K3Cfg(hidden_size=1024, routed_expert_hidden_size=512, moe_intermediate_size=256, num_experts=16,"
+            " num_experts_per_token=4)\n"
+            "wl, src, _ = make(92, 1024, 512, 256, 16, 4, 512)\n"
+            "lat = LatentMoE(cfg, 0, wl, src)\n"
+            "x = torch.randn(4, 1024, device=dev).to(torch.bfloat16)\n"
+            "ea, eb = moe(x).clone(), lat(x).clone(); torch.cuda.synchronize()  # side streams created\n"
+            "a_in, b_done = threading.Event(), threading.Event()\n"
+            "out, errs = {{}}, []\n"
+            "def run(name, fn):\n"
+            "    try:\n"
+            "        fn()\n"
+            "    except BaseException as e:\n"
+            "        errs.append((name, repr(e)))\n"
+            "    finally:\n"
+            "        (a_in if name == 'A' else b_done).set()\n"
+            "def cap_a():\n"
+            "    s = torch.cuda.Stream(); s.wait_stream(torch.cuda.current_stream()); g = torch.cuda.CUDAGraph()\n"
+            "    with torch.cuda.graph(g, stream=s, capture_error_mode='thread_local'):\n"
+            "        out['a'] = moe(x)\n"
+            "        a_in.set(); b_done.wait(60)\n"
+            "        out['la'] = lat(x)\n"
+            "    out['ga'] = g\n"
+            "def eager_b():\n"
+            "    a_in.wait(60)\n"
+            "    s = torch.cuda.Stream(); s.wait_stream(torch.cuda.current_stream())\n"
+            "    with torch.cuda.stream(s):\n"
+            "        out['b'], out['lb'] = moe(x), lat(x)\n"
+            "    s.synchronize()\n"
+            "ts = [threading.Thread(target=run, args=(n, f)) for n, f in (('A', cap_a), ('B', eager_b))]\n"
+            "for t in ts: t.start()\n"
+            "for t in ts: t.join(120)\n"
+            "assert not errs, errs\n"
+            "assert torch.equal(out['b'], ea) and torch.equal(out['lb'], eb), 'eager call beside the captures'\n"
+            "for i in range(3):\n"
+            "    out['ga'].replay(); torch.cuda.synchronize()\n"
+            "    assert torch.equal(out['a'], ea) and torch.equal(out['la'], eb), ('graph A', i)\n"
+            "    assert torch.equal(moe(x), ea) and torch.equal(lat(x), eb); torch.cuda.synchronize()\n"
+            "print('captures beside eager calls: ok')\n").format(t=str(root / "tests"), r=str(root),
+                                                                   p=str(root / "kimi-k3-mlx-macmini_amd"))
+    res = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True, timeout=300)
+    print(res.stdout[-2000:], res.stderr[-2000:])
+    assert res.returncode == 0 and "captures beside eager calls: ok" in res.stdout
