@@ -2,6 +2,8 @@
 against the fp64 oracle, through the LatentMoE-shaped dispatcher."""
 from __future__ import annotations
 
+import os
+
 import numpy as np
 import pytest
 import torch
@@ -106,7 +108,8 @@ def test_layer_matches_oracle(H, I, E, k, Is, distinct, router, act, xdt):
 def test_layer_full_shape_every_expert_distinct():
     """The 384-expert top-8 layer at full size with every expert distinct (9 GB of weights
     drawn on the device; only the selected experts are copied to the host for the oracle),
-    a bf16 shared expert, three tokens in a row through one module."""
+    a bf16 shared expert, three tokens in a row through one module, then four and eight
+    tokens at once through the multi-token decode."""
     from k3hip.moe import MoEConfig, RoutedMoE
     H, I, E, k, Is = 7168, 2048, 384, 8, 2048
     g = torch.Generator(device=DEV)
@@ -142,6 +145,20 @@ def test_layer_full_shape_every_expert_distinct():
         assert rel < 2e-5
         seen.update(sel)
     assert len(seen) > 16  # distinct weights behind distinct experts, not a few aliased sets
+    # four and eight tokens at once: the multi-token decode (k3_moe_layer_decode_multi), each
+    # selected expert read once for all its tokens, the shared expert on the side stream
+    workers = max(1, min(16, len(os.sched_getaffinity(0))))
+    for T in (4, 8):
+        x32 = om.bf16_round(rng.standard_normal((T, H)).astype(np.float32))
+        idx, wts, raw, _ = omoe.route_softmax(x32, router_w, k, True, 1.0)
+        assert min(topk_margin(raw[t], k) for t in range(T)) > 1e-5, "seed gives a near-tie at the top-k boundary"
+        sel = {int(e): tuple(tuple(a.cpu().numpy() for a in pair) for pair in experts[int(e)]) for e in np.unique(idx)}
+        y_want = omoe.moe_layer(x32, idx, wts, sel, shared, workers=workers)
+        y, r = moe(torch.from_numpy(x32).to(DEV).to(torch.bfloat16), return_router=True)
+        assert np.array_equal(np.sort(r.expert_indices.cpu().numpy(), -1), np.sort(idx, -1))
+        rel = om.normwise_rel(y.cpu().numpy(), y_want)
+        print(f"{T} tokens: {len(sel)} distinct experts rel={rel:.3e}")
+        assert rel < 2e-5
 
 
 def test_route_only_matches_layer_record_and_invariants():
