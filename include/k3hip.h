@@ -230,7 +230,8 @@ int k3_moe_layer_multi_workspace_offsets(int64_t T, int64_t H, int64_t I, int64_
  * it), the shared down rows, and the fixed-order combine with the shared output: six or seven
  * launches, no host synchronisation.  The shared expert's gate/up and down rows run on a
  * library-owned side stream of the current device, forked from `stream` at the start of the
- * call and joined to it before the combine through events (as k3_moe_latent_layer_decode_multi);
+ * call and joined to it before the routed down launch through events (as
+ * k3_moe_latent_layer_decode_multi, which joins before the up projection);
  * without it (K3HIP_SIDE_STREAM=0 in the environment, a first call made under capture, or a
  * call under capture while another capture on the device holds the capture side stream) the
  * gate/up rows run with the router rows and the down rows as extra blocks of the routed down

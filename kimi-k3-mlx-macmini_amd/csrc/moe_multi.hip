@@ -1252,7 +1252,7 @@ extern "C" int k3_moe_layer_decode_multi(const void *x, int x_dtype, const void 
     const bool bf = x_dtype == K3_BF16;
     // The shared expert (gate/up and down rows, 88 MB at the 384-expert shape) runs on the
     // side stream from the start of the call, beside R (then the router rows alone), the
-    // top-k, U, G and D, and joins before C: four tokens 173.5 -> 171.7 us.  Only its down rows
+    // top-k, U and G, and joins before D: four tokens 173.5 -> 171.7 us.  Only its down rows
     // there, forked after R, measured slower (178.4 -> 180.3 us); without a side lane (see
     // side_lane) they run as extra blocks of D's launch.
     std::unique_lock<std::mutex> lock(side_mutex, std::defer_lock);
@@ -1294,17 +1294,22 @@ extern "C" int k3_moe_layer_decode_multi(const void *x, int x_dtype, const void 
     d.ld[0] = a.Hr;
     if (has_shared) a.yadd = reinterpret_cast<const float *>(w + L.ysh);
     if (side) {
+        // R is enqueued before the side stream's launches (same dependencies): a graph
+        // replay then dispatches R first (see the latent entry point)
         rc = check_hip(hipEventRecord(side->fork, st), "moe layer (T tokens): fork");
+        if (!rc) rc = bf ? launch_rows_multi<uint16_t>(r, st) : launch_rows_multi<float>(r, st);
         if (!rc) rc = check_hip(hipStreamWaitEvent(side->s, side->fork, 0), "moe layer (T tokens): fork");
         if (!rc) rc = bf ? launch_rows_multi<uint16_t>(g, side->s) : launch_rows_multi<float>(g, side->s);
         if (!rc) rc = launch_rows_multi<float>(d, side->s);
         const int jr = check_hip(hipEventRecord(side->join, side->s), "moe layer (T tokens): join");
         if (!rc) rc = jr;
-    } else if (has_shared) {
-        r.wg = g.wg, r.wu = g.wu, r.N1 = g.N1, r.act = g.act, r.ld1 = g.ld1;
-        r.act_kind = act_kind, r.beta = beta, r.lbeta = linear_beta;
+    } else {
+        if (has_shared) {
+            r.wg = g.wg, r.wu = g.wu, r.N1 = g.N1, r.act = g.act, r.ld1 = g.ld1;
+            r.act_kind = act_kind, r.beta = beta, r.lbeta = linear_beta;
+        }
+        rc = bf ? launch_rows_multi<uint16_t>(r, st) : launch_rows_multi<float>(r, st);
     }
-    if (!rc) rc = bf ? launch_rows_multi<uint16_t>(r, st) : launch_rows_multi<float>(r, st);
     // the batched top-k on those logits (softmax / sigmoid + bias, renormalised, scaled)
     if (!rc)
         rc = k3_moe_topk(logits, a.E, a.T, a.E, static_cast<const float *>(router_bias), route_kind, renormalize,
@@ -1314,9 +1319,11 @@ extern "C" int k3_moe_layer_decode_multi(const void *x, int x_dtype, const void 
     if (!rc) rc = launch_union(a, st);
     if (!rc) rc = bf ? launch_gateup<uint16_t>(a, n_slots, st) : launch_gateup<float>(a, n_slots, st);
     if (side) {
-        if (!rc) rc = launch_down_only(a, n_slots, st);
+        // joined before D rather than before C (the side stream's work ended long before G
+        // does): 170.5 -> 170.0 us
         const int jr = check_hip(hipStreamWaitEvent(st, side->join, 0), "moe layer (T tokens): join");
         if (!rc) rc = jr;  // an error after the fork still joins
+        if (!rc) rc = launch_down_only(a, n_slots, st);
         return rc ? rc : launch_combine(a, st);
     }
     if (rc) return rc;
@@ -1429,19 +1436,26 @@ extern "C" int k3_moe_latent_layer_decode_multi(const void *x, int x_dtype, cons
         // the whole shared expert (264 MB at K3's shapes) on the side stream from the start of
         // the call, beside R1, the top-k, U, G and D; R3 adds its output.  K3's four-token step
         // 338 -> 325 us with the shared down rows alone there (forked after R1), 322 -> 318 us
-        // with the gate/up rows too; forked after U (beside G and D only): 337 us
+        // with the gate/up rows too; forked after U (beside G and D only): 337 us.  R1 is
+        // enqueued after the fork record and before the side stream's wait and launches (the
+        // same dependencies): a graph replay dispatches nodes in the order they were
+        // captured, and with the side stream's launches captured first R1 started about 6 us
+        // after them (319 -> 304.5 us)
         rc = check_hip(hipEventRecord(side->fork, st), "moe layer (T tokens): fork");
+        if (!rc) rc = bf ? launch_rows_multi<uint16_t>(r, st) : launch_rows_multi<float>(r, st);
         if (!rc) rc = check_hip(hipStreamWaitEvent(side->s, side->fork, 0), "moe layer (T tokens): fork");
         if (!rc) rc = bf ? launch_rows_multi<uint16_t>(g, side->s) : launch_rows_multi<float>(g, side->s);
         if (!rc) rc = launch_rows_multi<float>(d, side->s);
         const int jr = check_hip(hipEventRecord(side->join, side->s), "moe layer (T tokens): join");
         if (!rc) rc = jr;
-    } else if (has_shared) {
-        r.wg = g.wg, r.wu = g.wu, r.N1 = g.N1, r.act = g.act, r.ld1 = g.ld1;
-        r.act_kind = act_kind, r.beta = beta, r.lbeta = linear_beta;
+    } else {
+        if (has_shared) {
+            r.wg = g.wg, r.wu = g.wu, r.N1 = g.N1, r.act = g.act, r.ld1 = g.ld1;
+            r.act_kind = act_kind, r.beta = beta, r.lbeta = linear_beta;
+        }
+        rc = bf ? launch_rows_multi<uint16_t>(r, st) : launch_rows_multi<float>(r, st);
+        if (!rc && has_shared) rc = launch_rows_multi<float>(d, st);
     }
-    if (!rc) rc = bf ? launch_rows_multi<uint16_t>(r, st) : launch_rows_multi<float>(r, st);
-    if (!rc && has_shared && !side) rc = launch_rows_multi<float>(d, st);
     // sigmoid + bias routing (moe.py:65-76) on the logits
     if (!rc)
         rc = k3_moe_topk(logits, a.E, a.T, a.E, static_cast<const float *>(router_bias), K3_ROUTE_SIGMOID_BIAS,
