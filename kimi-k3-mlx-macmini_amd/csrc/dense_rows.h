@@ -232,7 +232,7 @@ __global__ __launch_bounds__(64 * NW) void step_rows_kernel(RowsArgs a) {
 #pragma unroll
         for (int u = 0; u < CH; ++u) {
             const int c = u * 64 + lane, n = n0 + r;
-            wr[r][u] = buf_load16(rw, (n < N && c < nch) ? static_cast<uint32_t>(n) * rowb + c * 16u : kOobOffset);
+            wr[r][u] = buf_load16_nt(rw, (n < N && c < nch) ? static_cast<uint32_t>(n) * rowb + c * 16u : kOobOffset);
         }
     // 2. the input vector
     stage_vector<MODE, NW, CH>(a, vs, red);
@@ -299,7 +299,7 @@ __global__ __launch_bounds__(64 * NW) void step_rows_loop_kernel(RowsArgs a) {
 #pragma unroll
         for (int u = 0; u < CH; ++u) {
             const int c = u * 64 + lane;
-            wr[u] = buf_load16(rw, (ok && c < nch) ? static_cast<uint32_t>(n) * rowb + c * 16u : kOobOffset);
+            wr[u] = buf_load16_nt(rw, (ok && c < nch) ? static_cast<uint32_t>(n) * rowb + c * 16u : kOobOffset);
         }
     };
     auto reduce_row = [&](const uint4 (&wr)[CH], int g) {

@@ -74,8 +74,8 @@ __global__ __launch_bounds__(256) void expert_gateup_kernel(GateUpArgs a) {
         const bool ok = has && g < GH;
         const uint32_t off = ok ? static_cast<uint32_t>(i) * rowA + g * 16u : kOobOffset;
         const uint32_t soff = ok ? static_cast<uint32_t>(i * GH + g) : kOobOffset;
-        wg[u] = buf_load16(rg, off);
-        wu[u] = buf_load16(ru, off);
+        wg[u] = buf_load16_nt(rg, off);
+        wu[u] = buf_load16_nt(ru, off);
         sg[u] = __builtin_amdgcn_raw_buffer_load_b8(rgs, soff, 0, 0);
         su[u] = __builtin_amdgcn_raw_buffer_load_b8(rus, soff, 0, 0);
     }

@@ -524,7 +524,7 @@ __global__ __launch_bounds__(256) void layer_l1(LayerArgs a) {
 #pragma unroll
         for (int u = 0; u < CHH; ++u) {
             const int c = u * 64 + lane;
-            w[u] = buf_load16(r, (e < a.E && c < nch) ? static_cast<uint32_t>(e) * row_bytes + c * 16u : kOobOffset);
+            w[u] = buf_load16_nt(r, (e < a.E && c < nch) ? static_cast<uint32_t>(e) * row_bytes + c * 16u : kOobOffset);
         }
         x_store<XT, XREG, false>(smem, xr);
         __syncthreads();
@@ -572,7 +572,7 @@ __global__ __launch_bounds__(256) void layer_l1(LayerArgs a) {
 #pragma unroll
         for (int u = 0; u < CHH; ++u) {
             const int c = u * 64 + lane;
-            w[u] = buf_load16(r, (l < a.Hr && c < nch) ? static_cast<uint32_t>(l) * row_bytes + c * 16u : kOobOffset);
+            w[u] = buf_load16_nt(r, (l < a.Hr && c < nch) ? static_cast<uint32_t>(l) * row_bytes + c * 16u : kOobOffset);
         }
         x_store<XT, XREG, false>(smem, xr);
         __syncthreads();
@@ -612,7 +612,7 @@ __global__ __launch_bounds__(256) void layer_l1(LayerArgs a) {
 #pragma unroll
             for (int u = 0; u < CHH; ++u) {
                 const int c = u * 64 + lane;
-                wg[u] = buf_load16(rg, (v && c < nch) ? static_cast<uint32_t>(i) * row_bytes + c * 16u : kOobOffset);
+                wg[u] = buf_load16_nt(rg, (v && c < nch) ? static_cast<uint32_t>(i) * row_bytes + c * 16u : kOobOffset);
             }
             __builtin_amdgcn_sched_barrier(0);
             __builtin_amdgcn_s_sleep(60);
@@ -620,15 +620,15 @@ __global__ __launch_bounds__(256) void layer_l1(LayerArgs a) {
 #pragma unroll
             for (int u = 0; u < CHH; ++u) {
                 const int c = u * 64 + lane;
-                wu[u] = buf_load16(ru, (v && c < nch) ? static_cast<uint32_t>(i) * row_bytes + c * 16u : kOobOffset);
+                wu[u] = buf_load16_nt(ru, (v && c < nch) ? static_cast<uint32_t>(i) * row_bytes + c * 16u : kOobOffset);
             }
         } else {
 #pragma unroll
             for (int u = 0; u < CHH; ++u) {
                 const int c = u * 64 + lane;
                 const uint32_t off = (v && c < nch) ? static_cast<uint32_t>(i) * row_bytes + c * 16u : kOobOffset;
-                wg[u] = buf_load16(rg, off);
-                wu[u] = buf_load16(ru, off);
+                wg[u] = buf_load16_nt(rg, off);
+                wu[u] = buf_load16_nt(ru, off);
             }
         }
         x_store<XT, XREG, false>(smem, xr);
@@ -682,7 +682,7 @@ __global__ __launch_bounds__(256) void layer_l2(LayerArgs a) {
 #pragma unroll
             for (int u = 0; u < CHI; ++u) {
                 const int c = u * 64 + lane, n = n0 + r;
-                w[r][u] = buf_load16(rr, (n < a.H && c < nch) ? static_cast<uint32_t>(n) * row_bytes + c * 16u
+                w[r][u] = buf_load16_nt(rr, (n < a.H && c < nch) ? static_cast<uint32_t>(n) * row_bytes + c * 16u
                                                                 : kOobOffset);
             }
 #pragma unroll
@@ -724,8 +724,8 @@ __global__ __launch_bounds__(256) void layer_l2(LayerArgs a) {
             const bool ok = v && g < GH;
             const uint32_t off = ok ? static_cast<uint32_t>(i) * rowA + g * 16u : kOobOffset;
             const uint32_t soff = ok ? static_cast<uint32_t>(i * GH + g) : kOobOffset;
-            wg[p][u] = buf_load16(rg, off);
-            wu[p][u] = buf_load16(ru, off);
+            wg[p][u] = buf_load16_nt(rg, off);
+            wu[p][u] = buf_load16_nt(ru, off);
             sg[p][u] = __builtin_amdgcn_raw_buffer_load_b8(rgs, soff, 0, 0);
             su[p][u] = __builtin_amdgcn_raw_buffer_load_b8(rus, soff, 0, 0);
         }
@@ -807,10 +807,10 @@ __global__ __launch_bounds__(256, 4) void layer_l3(LayerArgs a) {
             const bool ok = n < a.Hr && pc < P;
             const uint32_t off = ok ? static_cast<uint32_t>(n) * rowB + pc * (S / 2u) : kOobOffset;
             if constexpr (S == 32) {
-                const uint4 v = buf_load16(rd, off);
+                const uint4 v = buf_load16_nt(rd, off);
                 wd[r][p][0] = v.x, wd[r][p][1] = v.y, wd[r][p][2] = v.z, wd[r][p][3] = v.w;
             } else {
-                const auto v = __builtin_amdgcn_raw_buffer_load_b64(rd, off, 0, 0);
+                const auto v = __builtin_amdgcn_raw_buffer_load_b64(rd, off, 0, 2);  // nt, as buf_load16_nt
                 wd[r][p][0] = v[0], wd[r][p][1] = v[1];
             }
             sd[r][p] = __builtin_amdgcn_raw_buffer_load_b8(

@@ -182,8 +182,8 @@ __global__ __launch_bounds__(256) void multi_gateup_kernel(MultiArgs a) {
             const bool ok = g < GH;
             const uint32_t off = ok ? static_cast<uint32_t>(i) * rowA + g * 16u : kOobOffset;
             const uint32_t soff = ok ? static_cast<uint32_t>(i * GH + g) : kOobOffset;
-            wg[q][v] = buf_load16(rg, off);
-            wu[q][v] = buf_load16(ru, off);
+            wg[q][v] = buf_load16_nt(rg, off);
+            wu[q][v] = buf_load16_nt(ru, off);
             // the scale byte's aligned dword (the byte is picked out where it is used, so no
             // widening of the loaded value is hoisted above the staging)
             sg[q][v] = __builtin_amdgcn_raw_buffer_load_b32(rgs, ok ? soff & ~3u : kOobOffset, 0, 0);
@@ -315,10 +315,10 @@ __device__ __forceinline__ void down_body(const MultiArgs &a, int bid) {
                 const bool ok = n < a.Hr && pc < P;
                 const uint32_t off = ok ? static_cast<uint32_t>(n) * rowB + pc * (S / 2u) : kOobOffset;
                 if constexpr (S == 32) {
-                    const uint4 v = buf_load16(rd, off);
+                    const uint4 v = buf_load16_nt(rd, off);
                     wd[r][p][0] = v.x, wd[r][p][1] = v.y, wd[r][p][2] = v.z, wd[r][p][3] = v.w;
                 } else {
-                    const auto v = __builtin_amdgcn_raw_buffer_load_b64(rd, off, 0, 0);
+                    const auto v = __builtin_amdgcn_raw_buffer_load_b64(rd, off, 0, 2);  // nt, as buf_load16_nt
                     wd[r][p][0] = v[0], wd[r][p][1] = v[1];
                 }
                 // the scale byte's aligned dword (picked out where it is used, so no widening
@@ -548,7 +548,7 @@ __device__ __forceinline__ void rows_body(const MRowsArgs &a, int bid) {
         for (int u = 0; u < CH; ++u) {
             const int c = u * 64 + lane;
             const uint32_t off = (ok && c < nch) ? static_cast<uint32_t>(n) * rowb + c * 16u : kOobOffset;
-            w[r][u] = buf_load16(pair && r == 1 ? ru : rg, off);
+            w[r][u] = buf_load16_nt(pair && r == 1 ? ru : rg, off);
         }
     }
     const int cpr = static_cast<int>(a.K * sizeof(IT) / 16);  // 16-byte chunks per input row
@@ -693,7 +693,7 @@ __device__ __forceinline__ void load_row(uint4 (&w)[CH], __amdgpu_buffer_rsrc_t 
 #pragma unroll
     for (int c = 0; c < CH; ++c) {
         const int cc = c * 64 + lane;
-        w[c] = buf_load16(rs, (n < N && cc < nch) ? static_cast<uint32_t>(n) * rowb + cc * 16u : kOobOffset);
+        w[c] = buf_load16_nt(rs, (n < N && cc < nch) ? static_cast<uint32_t>(n) * rowb + cc * 16u : kOobOffset);
     }
 }
 

@@ -85,7 +85,7 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
             for (int u = 0; u < GPL; ++u) {
                 const int g = gs + u * kWave + lane;
                 const bool ok = n < a.N && g < G;
-                w[r][u] = buf_load16(rw, ok ? static_cast<uint32_t>(n) * row_bytes + static_cast<uint32_t>(g) * 16u
+                w[r][u] = buf_load16_nt(rw, ok ? static_cast<uint32_t>(n) * row_bytes + static_cast<uint32_t>(g) * 16u
                                             : kOobOffset);
                 sb[r][u] = __builtin_amdgcn_raw_buffer_load_b8(rs, ok ? static_cast<uint32_t>(n * G + g) : kOobOffset,
                                                                0, 0);
