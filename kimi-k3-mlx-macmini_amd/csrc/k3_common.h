@@ -104,8 +104,12 @@ __device__ __forceinline__ uint4 buf_load16(__amdgpu_buffer_rsrc_t r, uint32_t o
 // The same load with the non-temporal hint (the nt bit of the cache policy), for weight rows
 // that a launch streams once: measured on the batch-1 expert step 9.4 -> 9.2 us, the
 // 384-expert layer's four-token step 171 -> 161.5 us, K3's layer 128 -> 121-123 us, the KDA
-// step 175 -> 154 us.  Inputs that several blocks stage (x, act, norm weights) keep the
-// default policy: the hint on every load made the expert step 20% slower.
+// step 175 -> 154 us.  The weights' E8M0 scale bytes load with the same hint (aux 2 on
+// their byte and dword loads): expert step 2560 -> 2630 GB/s, batch-1 GEMV 3.98 -> 3.84 us.
+// Inputs that several blocks stage (x, act, norm weights) keep the default policy: the hint
+// on every load made the expert step 20% slower.  The grouped prefill's weight tiles (read
+// once per token tile of an expert) and the MLA cache rows (read by the four head-group
+// blocks of a split) keep it too: with the hint, 4.65 -> 5.18 ms and no gain.
 __device__ __forceinline__ uint4 buf_load16_nt(__amdgpu_buffer_rsrc_t r, uint32_t off) {
     return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 2));
 }

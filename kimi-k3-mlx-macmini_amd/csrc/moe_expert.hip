@@ -76,8 +76,8 @@ __global__ __launch_bounds__(256) void expert_gateup_kernel(GateUpArgs a) {
         const uint32_t soff = ok ? static_cast<uint32_t>(i * GH + g) : kOobOffset;
         wg[u] = buf_load16_nt(rg, off);
         wu[u] = buf_load16_nt(ru, off);
-        sg[u] = __builtin_amdgcn_raw_buffer_load_b8(rgs, soff, 0, 0);
-        su[u] = __builtin_amdgcn_raw_buffer_load_b8(rus, soff, 0, 0);
+        sg[u] = __builtin_amdgcn_raw_buffer_load_b8(rgs, soff, 0, 2);
+        su[u] = __builtin_amdgcn_raw_buffer_load_b8(rus, soff, 0, 2);
     }
 
     // 3. stage x (swizzled chunk order, every slot written)

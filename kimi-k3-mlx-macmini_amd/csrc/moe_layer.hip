@@ -726,8 +726,8 @@ __global__ __launch_bounds__(256) void layer_l2(LayerArgs a) {
             const uint32_t soff = ok ? static_cast<uint32_t>(i * GH + g) : kOobOffset;
             wg[p][u] = buf_load16_nt(rg, off);
             wu[p][u] = buf_load16_nt(ru, off);
-            sg[p][u] = __builtin_amdgcn_raw_buffer_load_b8(rgs, soff, 0, 0);
-            su[p][u] = __builtin_amdgcn_raw_buffer_load_b8(rus, soff, 0, 0);
+            sg[p][u] = __builtin_amdgcn_raw_buffer_load_b8(rgs, soff, 0, 2);
+            su[p][u] = __builtin_amdgcn_raw_buffer_load_b8(rus, soff, 0, 2);
         }
     }
     x_store<XT, XREG, true>(smem, xr);
@@ -814,7 +814,7 @@ __global__ __launch_bounds__(256, 4) void layer_l3(LayerArgs a) {
                 wd[r][p][0] = v[0], wd[r][p][1] = v[1];
             }
             sd[r][p] = __builtin_amdgcn_raw_buffer_load_b8(
-                rds, ok ? static_cast<uint32_t>(n * GI + pc * S / 32) : kOobOffset, 0, 0);
+                rds, ok ? static_cast<uint32_t>(n * GI + pc * S / 32) : kOobOffset, 0, 2);
         }
     __builtin_amdgcn_sched_barrier(0);  // every load in flight before the first wait
     // Unconditional stores and reads: chunks past I store their zeros into the sink slot, and

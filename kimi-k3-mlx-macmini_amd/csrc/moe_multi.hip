@@ -186,8 +186,8 @@ __global__ __launch_bounds__(256) void multi_gateup_kernel(MultiArgs a) {
             wu[q][v] = buf_load16_nt(ru, off);
             // the scale byte's aligned dword (the byte is picked out where it is used, so no
             // widening of the loaded value is hoisted above the staging)
-            sg[q][v] = __builtin_amdgcn_raw_buffer_load_b32(rgs, ok ? soff & ~3u : kOobOffset, 0, 0);
-            su[q][v] = __builtin_amdgcn_raw_buffer_load_b32(rus, ok ? soff & ~3u : kOobOffset, 0, 0);
+            sg[q][v] = __builtin_amdgcn_raw_buffer_load_b32(rgs, ok ? soff & ~3u : kOobOffset, 0, 2);
+            su[q][v] = __builtin_amdgcn_raw_buffer_load_b32(rus, ok ? soff & ~3u : kOobOffset, 0, 2);
         }
     }
     // the slot's pair ids and the byte offsets of their token rows in x
@@ -324,7 +324,7 @@ __device__ __forceinline__ void down_body(const MultiArgs &a, int bid) {
                 // the scale byte's aligned dword (picked out where it is used, so no widening
                 // of the loaded value is hoisted above the act staging)
                 sd[r][p] = __builtin_amdgcn_raw_buffer_load_b32(
-                    rds, ok ? static_cast<uint32_t>(n * GI + pc * S / 32) & ~3u : kOobOffset, 0, 0);
+                    rds, ok ? static_cast<uint32_t>(n * GI + pc * S / 32) & ~3u : kOobOffset, 0, 2);
             }
     }
     if (static_cast<int>(threadIdx.x) < a.T) pair_s[threadIdx.x] = pid;

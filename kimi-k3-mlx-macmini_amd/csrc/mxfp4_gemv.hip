@@ -88,7 +88,7 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
                 w[r][u] = buf_load16_nt(rw, ok ? static_cast<uint32_t>(n) * row_bytes + static_cast<uint32_t>(g) * 16u
                                             : kOobOffset);
                 sb[r][u] = __builtin_amdgcn_raw_buffer_load_b8(rs, ok ? static_cast<uint32_t>(n * G + g) : kOobOffset,
-                                                               0, 0);
+                                                               0, 2);
             }
         }
     };
